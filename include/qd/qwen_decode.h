@@ -1,0 +1,270 @@
+/*
+ * qwen_decode.h -- C ABI of the MI355X-native Qwen2 FP32 decode engine.
+ *
+ * The engine keeps FP32 weights, the KV cache and the decode state resident
+ * in HBM and runs the decode step as hand-written gfx950 HIP kernels. Plain
+ * pointers and sizes only: every host buffer below is ordinary host memory,
+ * every size is in elements unless it says bytes.
+ *
+ * Conventions (mirroring the reference runtime's C ABI, include/lrrt/lrrt.h):
+ *   - every call returns qd_status with the numeric values of lr_status_t
+ *     (include/lrrt/lrrt.h:17-25); no exception crosses the ABI;
+ *   - qd_last_error() returns the calling thread's last diagnostic text;
+ *   - the engine owns all device memory; qd_engine_destroy waits for pending
+ *     work (include/lrrt/lrrt.h:92-93);
+ *   - one engine is driven by one host thread at a time;
+ *   - the KV cache never travels through the host between steps
+ *     (docs/iree-qwen-kv-cache-abi.md:283-290).
+ *
+ * Position convention: every sequence slot has a position = number of tokens
+ * whose K/V are in its cache = the slot the next consumed token writes.
+ */
+#ifndef QD_QWEN_DECODE_H_
+#define QD_QWEN_DECODE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QD_API __attribute__((visibility("default")))
+
+/* Same numeric values as lr_status_t (include/lrrt/lrrt.h:17-25). */
+typedef enum qd_status {
+  QD_SUCCESS = 0,
+  QD_ERROR_INVALID_ARGUMENT = 1,
+  QD_ERROR_NOT_INITIALIZED = 2,
+  QD_ERROR_ALREADY_INITIALIZED = 3,
+  QD_ERROR_NOT_SUPPORTED = 4,
+  QD_ERROR_RUNTIME = 5,
+  QD_ERROR_DEVICE_FAULT = 6
+} qd_status;
+
+/* Mirrors the reference's StopReason (executor/qwen/stateful_graph_context.hpp:87-91). */
+typedef enum qd_stop_reason {
+  QD_STOP_NONE = 0,
+  QD_STOP_MAXIMUM_TOKENS = 1,
+  QD_STOP_EOS_TOKEN = 2
+} qd_stop_reason;
+
+/* Model shape and engine capacity. The shape fields carry the meaning of the
+ * reference's DecoderLayerShape / ModelTailWeights
+ * (executor/qwen/weight_bundle.hpp:21-58) plus the eps and theta the
+ * persistent path hard-codes (benchmarks/qwen_stateful_graph.cpp:379,818). */
+typedef struct qd_config {
+  uint32_t hidden;       /* 896 */
+  uint32_t heads;        /* 14 query heads */
+  uint32_t kv_heads;     /* 2 */
+  uint32_t head_dim;     /* 64 (the only supported value) */
+  uint32_t intermediate; /* 4864 */
+  uint32_t vocab;        /* 151936 */
+  uint32_t layers;       /* 24 */
+  uint32_t capacity;     /* KV positions per sequence slot */
+  uint32_t max_batch;    /* sequence slots */
+  uint32_t tied_lm_head; /* nonzero: LM head aliases the token embeddings */
+  float rms_eps;         /* 1e-6 */
+  float rope_theta;      /* 1e6 */
+  int32_t device;        /* HIP device ordinal */
+  uint32_t reserved;
+} qd_config;
+
+/* Distributions for qd_load_synthetic (0.02, 0.01, 1.0). */
+typedef struct qd_synthetic_init {
+  float weight_std; /* projections and token embeddings: N(0, weight_std) */
+  float bias_std;   /* q/k/v biases: N(0, bias_std) */
+  float norm_gain;  /* every RMSNorm gain */
+  float reserved;
+} qd_synthetic_init;
+
+/* Device-resident decode state of one sequence slot; same fields as the
+ * reference's DecodeState (executor/qwen/stateful_graph_context.hpp:96-105),
+ * except that `token_position` is the next free slot (see above). */
+typedef struct qd_decode_state {
+  uint32_t token_position;
+  uint32_t kv_length;
+  uint32_t sampled_token;
+  uint32_t eos_token;
+  uint32_t generated_tokens;
+  uint32_t maximum_tokens;
+  uint32_t stop_reason;
+  float sampled_logit;
+} qd_decode_state;
+
+/* Per-engine timing of the last qd_generate_resident call (HIP events on the
+ * engine stream), in microseconds. */
+typedef struct qd_timing {
+  double total_us;
+  double per_token_us;
+  uint32_t tokens;
+  uint32_t reserved;
+} qd_timing;
+
+/* Per-kernel totals from qd_profile_kernels: summed HIP-event durations and
+ * summed algorithmic bytes (bytes the kernel must move at minimum) of its
+ * launches. */
+typedef struct qd_kernel_stat {
+  char name[48];
+  uint32_t launches;
+  uint32_t reserved;
+  double total_us;
+  double bytes;
+} qd_kernel_stat;
+
+typedef struct qd_engine qd_engine;
+
+QD_API const char *qd_status_string(qd_status status);
+QD_API const char *qd_last_error(void);
+QD_API uint32_t qd_abi_version(void);
+/* Number of visible HIP devices (0 on a host without a GPU). */
+QD_API qd_status qd_device_count(uint32_t *count);
+
+/* Creates an engine: allocates weights, KV cache [max_batch][layers]
+ * [capacity][kv_heads*head_dim] and scratch on `config->device`. Replaces
+ * the reference's DecoderLayer / ModelTail constructors
+ * (examples/triton/mini_decoder_layer.hpp:205-254,770-800) and the device
+ * buffers of benchmarks/qwen_stateful_graph.cpp:935-1010. */
+QD_API qd_status qd_engine_create(const qd_config *config, qd_engine **engine);
+/* Waits for pending work, then frees everything. */
+QD_API qd_status qd_engine_destroy(qd_engine *engine);
+QD_API qd_status qd_engine_config(const qd_engine *engine, qd_config *config);
+/* Total device bytes held by the engine. */
+QD_API qd_status qd_engine_device_bytes(const qd_engine *engine, uint64_t *bytes);
+
+/* Loads a reference weight bundle directory: layer_<i>/weights.json for each
+ * layer plus model_tail/weights.json. Replaces load_decoder_layer_weights and
+ * load_model_tail_weights (executor/qwen/weight_bundle.hpp:460-602) feeding
+ * the device copies of benchmarks/qwen_stateful_graph.cpp:858-910. */
+QD_API qd_status qd_load_bundle(qd_engine *engine, const char *directory);
+/* Fills every weight from the counter-based generator (seeded, identical to
+ * the oracle's). Replaces the synthetic fill of
+ * benchmarks/qwen_stateful_graph.cpp:615-621,794-832. */
+QD_API qd_status qd_load_synthetic(qd_engine *engine, uint64_t seed,
+                                   const qd_synthetic_init *init);
+/* Copies one tensor of the resident weights back to the host (tests).
+ * kind: 0..11 layer tensors in bundle order, 0x100 embeddings, 0x101 final
+ * norm, 0x102 LM head. `count` must equal the tensor's element count. */
+QD_API qd_status qd_read_weight(qd_engine *engine, uint32_t layer,
+                                uint32_t kind, float *out, size_t count);
+
+/* Sets a sequence slot's position (KV length) without touching cache
+ * contents; resets its decode state. Mirrors ResidentExecutor::initialize and
+ * initialize_decode_state (include/lrrt/persistent_graph/resident_executor.hpp:329-356,
+ * benchmarks/qwen_stateful_graph.cpp:1256-1270). */
+QD_API qd_status qd_kv_reset(qd_engine *engine, uint32_t seq,
+                             uint32_t position);
+/* Writes / reads `count` positions of one layer's K and V starting at
+ * `start`, token-major [count][kv_heads*head_dim]. Writing mirrors the KV
+ * half of DecoderLayer::copy_inputs (examples/triton/mini_decoder_layer.hpp:256-276). */
+QD_API qd_status qd_write_kv(qd_engine *engine, uint32_t seq, uint32_t layer,
+                             uint32_t start, uint32_t count, const float *k,
+                             const float *v);
+QD_API qd_status qd_read_kv(qd_engine *engine, uint32_t seq, uint32_t layer,
+                            uint32_t start, uint32_t count, float *k,
+                            float *v);
+QD_API qd_status qd_read_decode_state(qd_engine *engine, uint32_t seq,
+                                      qd_decode_state *state);
+
+/* One decoder layer on a host hidden vector at the slot's current position
+ * (writes K/V at that position, attends over 0..position). Does not advance
+ * the position. Replaces DecoderLayer::decode_to_hidden_state
+ * (examples/triton/mini_decoder_layer.hpp:345-372). */
+QD_API qd_status qd_layer_step(qd_engine *engine, uint32_t seq,
+                               uint32_t layer, float *hidden);
+
+/* One full decode step of `token_in` at the slot's position: embedding, all
+ * layers, final norm, LM head, argmax (lowest index on ties); advances the
+ * position by one. logits_out (vocab floats) and top_logit may be NULL.
+ * Replaces the per-token loop body of
+ * benchmarks/triton_mini_decoder_layer.cpp:1041-1076 (stack + ModelTail::run
+ * + copy_logits + host top_logits). */
+QD_API qd_status qd_step(qd_engine *engine, uint32_t seq, uint32_t token_in,
+                         float *logits_out, uint32_t *greedy_out,
+                         float *top_logit);
+
+/* Prefill of n tokens from the slot's position; advances it by n. Writes the
+ * last position's logits (nullable) and greedy token. Semantically n
+ * sequential qd_step calls (the reference's prompt stack,
+ * benchmarks/triton_mini_decoder_layer.cpp:811-849). */
+QD_API qd_status qd_prefill(qd_engine *engine, uint32_t seq,
+                            const uint32_t *tokens, uint32_t n,
+                            float *last_logits, uint32_t *greedy_out,
+                            float *top_logit);
+
+/* One decode step for n_seq independent sequences at their own positions.
+ * logits [n_seq][vocab] and greedy [n_seq] (both nullable). */
+QD_API qd_status qd_step_batch(qd_engine *engine, uint32_t n_seq,
+                               const uint32_t *seq_ids, const uint32_t *tokens,
+                               float *logits, uint32_t *greedy);
+
+/* Device-resident greedy generation: consumes first_token, then feeds each
+ * argmax back on the device until max_tokens tokens were produced or eos
+ * was produced; one host synchronisation at the end. Mirrors the resident
+ * loop and embedding feedback of benchmarks/qwen_stateful_graph_kernel.cpp:358-390
+ * driven by ResidentExecutor::launch (resident_executor.hpp:358-361).
+ * out_tokens has room for max_tokens; all_logits (max_tokens * vocab floats)
+ * may be NULL. eos = UINT32_MAX disables the EOS test. */
+QD_API qd_status qd_generate_resident(qd_engine *engine, uint32_t seq,
+                                      uint32_t first_token,
+                                      uint32_t max_tokens, uint32_t eos,
+                                      uint32_t *out_tokens,
+                                      uint32_t *generated,
+                                      uint32_t *stop_reason,
+                                      float *all_logits);
+
+/* Runs `tokens` greedy generate-mode steps from the slot's position with a
+ * HIP event pair around every kernel launch on the engine stream, and
+ * reports per-kernel totals (at most `capacity` entries). Advances the
+ * position like qd_generate_resident; pair with qd_kv_reset. Plays the role
+ * of the reference's stage profile (benchmarks/qwen_stateful_graph.cpp:547-602
+ * byte model, qwen_stateful_graph_kernel.cpp:837-865 stage timing). */
+QD_API qd_status qd_profile_kernels(qd_engine *engine, uint32_t seq,
+                                    uint32_t first_token, uint32_t tokens,
+                                    qd_kernel_stat *stats, uint32_t capacity,
+                                    uint32_t *count);
+
+/* Timing of the last qd_generate_resident call. */
+QD_API qd_status qd_last_timing(const qd_engine *engine, qd_timing *timing);
+
+/* Waits for all work queued by the engine. */
+QD_API qd_status qd_sync(qd_engine *engine);
+
+/* ---- weight-bundle I/O (host only, no device needed) -----------------------
+ * C-ABI form of load/write_decoder_layer_weights and
+ * load/write_model_tail_weights (executor/qwen/weight_bundle.hpp:460-757):
+ * same files, same validation, same diagnostics (qd_last_error).
+ * shape6 = {keys, hidden, heads, kv_heads, head_dim, intermediate}; layer
+ * tensors travel concatenated in bundle order (attention_norm, mlp_norm, q,
+ * k, v, q_bias, k_bias, v_bias, out, gate, up, down). */
+QD_API qd_status qd_bundle_write_layer(const char *manifest_path,
+                                       const char *data_name,
+                                       const uint32_t *shape6,
+                                       float rope_theta,
+                                       const float *tensors);
+/* On success *count = floats written; capacity too small -> INVALID_ARGUMENT
+ * with *count = floats needed. */
+QD_API qd_status qd_bundle_read_layer(const char *manifest_path,
+                                      uint32_t *shape6, float *rope_theta,
+                                      float *tensors, size_t capacity,
+                                      size_t *count);
+QD_API qd_status qd_bundle_write_tail(const char *manifest_path,
+                                      const char *data_name, uint32_t hidden,
+                                      uint32_t vocab,
+                                      const uint32_t *token_ids,
+                                      size_t token_count,
+                                      const float *token_embeddings,
+                                      const float *final_norm,
+                                      const float *lm_head);
+/* Tensors concatenated: token_embeddings | final_norm | lm_head. */
+QD_API qd_status qd_bundle_read_tail(const char *manifest_path,
+                                     uint32_t *hidden, uint32_t *vocab,
+                                     uint32_t *token_ids, size_t ids_capacity,
+                                     size_t *token_count, float *tensors,
+                                     size_t capacity, size_t *count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QD_QWEN_DECODE_H_ */

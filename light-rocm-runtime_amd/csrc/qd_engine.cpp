@@ -1,0 +1,944 @@
+// Host engine behind the C ABI in include/qd/qwen_decode.h.
+//
+// Owns every device allocation: packed FP32 weights, the KV cache
+// [slot][layer][capacity][kv_heads*64], RoPE tables, per-slot activations and
+// decode state. All work is queued on one HIP stream of the engine's device;
+// errors surface as qd_status at the call that observes them (launch errors
+// immediately, device faults at the next synchronisation).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <tuple>
+#include <vector>
+
+#include "qd/qwen_decode.h"
+#include "qd_bundle.hpp"
+#include "qd_device.hpp"
+#include "qd_kernels.hpp"
+#include "qd_rng.hpp"
+
+namespace {
+
+constexpr uint32_t kAbiVersion = 1;
+constexpr int kLmHeadParts = 1024;  // LM-head workgroups = top-1 partials
+
+thread_local std::string g_error;
+
+struct QdError : std::runtime_error {
+  qd_status status;
+  QdError(qd_status s, const std::string &m) : std::runtime_error(m), status(s) {}
+};
+
+[[noreturn]] void fail(qd_status s, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  throw QdError(s, buf);
+}
+
+qd_status hip_status(hipError_t e) {
+  switch (e) {
+    case hipErrorIllegalAddress:
+    case hipErrorLaunchFailure:
+    case hipErrorAssert:
+    case hipErrorLaunchTimeOut:
+      return QD_ERROR_DEVICE_FAULT;
+    case hipErrorInvalidValue:
+      return QD_ERROR_INVALID_ARGUMENT;
+    default:
+      return QD_ERROR_RUNTIME;
+  }
+}
+
+void check(hipError_t e, const char *what) {
+  if (e != hipSuccess) fail(hip_status(e), "%s: %s", what, hipGetErrorString(e));
+}
+
+int host_threads() {
+  const char *env = std::getenv("OMP_NUM_THREADS");
+  int n = env ? std::atoi(env) : 0;
+  if (n <= 0) n = static_cast<int>(std::thread::hardware_concurrency());
+  return std::max(1, std::min(n, 64));
+}
+
+// Fills out[0..n) with N(0, std) from the generator, elements [first, first+n)
+// of the stream, on all host threads.
+void fill_normal(float *out, size_t n, uint64_t first, uint64_t seed,
+                 uint64_t stream, float stddev) {
+  const qd::rng::Stream s(seed, stream);
+  const int t = static_cast<int>(std::min<size_t>(host_threads(), n / 65536 + 1));
+  std::vector<std::thread> pool;
+  for (int k = 0; k < t; ++k) {
+    pool.emplace_back([=, &s] {
+      const size_t b = n * k / t, e = n * (k + 1) / t;
+      for (size_t i = b; i < e; ++i)
+        out[i] = static_cast<float>(static_cast<double>(stddev) * s.normal(first + i));
+    });
+  }
+  for (auto &th : pool) th.join();
+}
+
+}  // namespace
+
+struct qd_engine {
+  qd_config cfg{};
+  size_t H = 0, I = 0, NQ = 0, NKV = 0, QD = 0, KVD = 0, QKV = 0, V = 0, L = 0,
+         CAP = 0, B = 0;
+  int max_chunks = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+  std::vector<void *> allocs;
+  uint64_t device_bytes = 0;
+
+  float *weights = nullptr;  // arena of all layer weights
+  std::vector<qd::LayerPtrs> layers;
+  float *embed = nullptr, *lm_head = nullptr, *final_norm = nullptr;
+  float *k_cache = nullptr, *v_cache = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  float *hidden = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr,
+        *logits = nullptr;
+  float *part_m = nullptr, *part_l = nullptr, *part_acc = nullptr;
+  float *part_val = nullptr;
+  uint32_t *part_idx = nullptr;
+  uint32_t *tokens_dev = nullptr;  // [capacity]
+  qd::SeqState *states = nullptr;  // [max_batch]
+  float *history = nullptr;        // generate-mode logits [capacity][vocab]
+  size_t history_rows = 0;
+
+  qd::SeqState *h_states = nullptr;  // pinned [max_batch]
+  uint32_t *h_tokens = nullptr;      // pinned [capacity]
+  std::vector<uint32_t> positions;   // host mirror of each slot's position
+  bool loaded = false;
+  qd_timing timing{};
+
+  // Teardown cannot report errors; a device fault was already reported by
+  // the call that observed it.
+  ~qd_engine() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (void *p : allocs) (void)hipFree(p);
+    if (h_states) (void)hipHostFree(h_states);
+    if (h_tokens) (void)hipHostFree(h_tokens);
+    if (ev_begin) (void)hipEventDestroy(ev_begin);
+    if (ev_end) (void)hipEventDestroy(ev_end);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  template <typename T>
+  T *alloc(size_t count) {
+    void *p = nullptr;
+    const size_t bytes = std::max<size_t>(count * sizeof(T), 256);
+    check(hipMalloc(&p, bytes), "hipMalloc");
+    allocs.push_back(p);
+    device_bytes += bytes;
+    return static_cast<T *>(p);
+  }
+
+  float *kv_slice(float *base, size_t seq, size_t layer) const {
+    return base + ((seq * L + layer) * CAP) * KVD;
+  }
+
+  void set_device() const { check(hipSetDevice(cfg.device), "hipSetDevice"); }
+
+  void upload(float *dst, const float *src, size_t n) {
+    check(hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyHostToDevice, stream),
+          "hipMemcpyAsync H2D");
+  }
+
+  void build_rope_tables(float theta) {
+    // Same FP32 recipe as the Hugging Face rotary embedding: inv_freq =
+    // 1 / theta^(2i/d), angle = p * inv_freq, both rounded to FP32.
+    std::vector<float> c(CAP * qd::kRotary), s(CAP * qd::kRotary);
+    for (int i = 0; i < qd::kRotary; ++i) {
+      const float exponent = static_cast<float>(2 * i) / static_cast<float>(qd::kHeadDim);
+      const float inv_freq = 1.0f / std::pow(theta, exponent);
+      for (size_t p = 0; p < CAP; ++p) {
+        const float angle = static_cast<float>(p) * inv_freq;
+        c[p * qd::kRotary + i] = static_cast<float>(std::cos(static_cast<double>(angle)));
+        s[p * qd::kRotary + i] = static_cast<float>(std::sin(static_cast<double>(angle)));
+      }
+    }
+    upload(rope_cos, c.data(), c.size());
+    upload(rope_sin, s.data(), s.size());
+    check(hipStreamSynchronize(stream), "rope upload");
+    cfg.rope_theta = theta;
+  }
+
+  void check_seq(uint32_t seq) const {
+    if (seq >= B) fail(QD_ERROR_INVALID_ARGUMENT, "sequence slot %u out of range (max_batch %zu)", seq, B);
+  }
+  void check_loaded() const {
+    if (!loaded) fail(QD_ERROR_NOT_INITIALIZED, "weights are not loaded");
+  }
+
+  // Writes the slot's device state from the host mirror.
+  void push_state(uint32_t seq, uint32_t token, uint32_t mode, uint32_t eos,
+                  uint32_t max_tokens) {
+    qd::SeqState &h = h_states[seq];
+    std::memset(&h, 0, sizeof(h));
+    h.position = positions[seq];
+    h.token = token;
+    h.eos = eos;
+    h.max_tokens = max_tokens;
+    h.mode = mode;
+    check(hipMemcpyAsync(states + seq, &h, sizeof(h), hipMemcpyHostToDevice, stream),
+          "state upload");
+  }
+
+  qd::LayerLaunch layer_args(uint32_t seq, size_t layer) {
+    qd::LayerLaunch a{};
+    a.w = layers[layer];
+    a.rope_cos = rope_cos;
+    a.rope_sin = rope_sin;
+    a.st = states + seq;
+    a.hidden = hidden + seq * H;
+    a.q = q + seq * QD;
+    a.attn = attn + seq * QD;
+    a.act = act + seq * I;
+    a.k_cache = kv_slice(k_cache, seq, layer);
+    a.v_cache = kv_slice(v_cache, seq, layer);
+    a.part_m = part_m;
+    a.part_l = part_l;
+    a.part_acc = part_acc;
+    a.max_chunks = max_chunks;
+    a.capacity = static_cast<int>(CAP);
+    a.nq = static_cast<int>(NQ);
+    a.nkv = static_cast<int>(NKV);
+    a.eps = cfg.rms_eps;
+    return a;
+  }
+
+  qd::TailLaunch tail_args(uint32_t seq, float *out_logits, int hist,
+                           uint32_t *out_tokens) {
+    qd::TailLaunch t{};
+    t.hidden = hidden + seq * H;
+    t.final_norm = final_norm;
+    t.head = lm_head;
+    t.st = states + seq;
+    t.logits = out_logits;
+    t.history = hist;
+    t.vocab = static_cast<int>(V);
+    t.eps = cfg.rms_eps;
+    t.part_val = part_val;
+    t.part_idx = part_idx;
+    t.parts = kLmHeadParts;
+    t.out_tokens = out_tokens;
+    return t;
+  }
+
+  // Embedding + every layer + LM head + argmax for one slot (state already
+  // on the device).
+  void enqueue_step(uint32_t seq, float *out_logits, int hist,
+                    uint32_t *out_tokens, qd::Marker *m = nullptr) {
+    check(qd::launch_embed(stream, embed, states + seq, hidden + seq * H,
+                           static_cast<int>(H), static_cast<int>(V), m),
+          "embed launch");
+    for (size_t l = 0; l < L; ++l)
+      check(qd::launch_layer(stream, layer_args(seq, l), m), "layer launch");
+    check(qd::launch_tail(stream, tail_args(seq, out_logits, hist, out_tokens), m),
+          "tail launch");
+  }
+
+  // Algorithmic bytes of one launch of `kernel` when the step attends over
+  // `length` positions: weights, KV rows and activations each moved once.
+  double kernel_bytes(int kernel, double length) const {
+    const double f = 4.0;
+    const double chunks = std::ceil(length / qd::kAttnChunk);
+    switch (kernel) {
+      case qd::kKEmbed: return 2 * H * f;
+      case qd::kKQkvRope:
+        return (QKV * H + QKV + 2 * H + 2 * qd::kRotary + QD + 2 * KVD) * f;
+      case qd::kKAttnPartial:
+        return (2 * length * KVD + QD + chunks * NQ * (qd::kHeadDim + 2)) * f;
+      case qd::kKAttnCombine: return (chunks * NQ * (qd::kHeadDim + 2) + QD) * f;
+      case qd::kKOproj: return (H * QD + QD + 2 * H) * f;
+      case qd::kKGateUp: return (2 * I * H + 2 * H + I) * f;
+      case qd::kKDown: return (H * I + I + 2 * H) * f;
+      case qd::kKLmHead: return (V * H + 2 * H + V + 2 * 1024) * f;
+      case qd::kKArgmax: return 2 * 1024 * f;
+    }
+    return 0;
+  }
+
+  void sync() { check(hipStreamSynchronize(stream), "hipStreamSynchronize"); }
+};
+
+namespace {
+
+qd_status guard(const std::function<void()> &fn) {
+  try {
+    fn();
+    return QD_SUCCESS;
+  } catch (const QdError &e) {
+    g_error = e.what();
+    return e.status;
+  } catch (const std::bad_alloc &) {
+    g_error = "host allocation failed";
+    return QD_ERROR_RUNTIME;
+  } catch (const std::invalid_argument &e) {
+    g_error = e.what();
+    return QD_ERROR_INVALID_ARGUMENT;
+  } catch (const std::exception &e) {
+    g_error = e.what();
+    return QD_ERROR_RUNTIME;
+  }
+}
+
+void layer_shape_matches(const qd_engine &e, const qd::bundle::LayerWeights &w) {
+  const auto &s = w.shape;
+  if (s.hidden != e.H || s.heads != e.NQ || s.kv_heads != e.NKV ||
+      s.head_dim != qd::kHeadDim || s.intermediate != e.I)
+    fail(QD_ERROR_INVALID_ARGUMENT,
+         "bundle decoder shape (hidden %u heads %u kv_heads %u head_dim %u "
+         "intermediate %u) does not match the engine",
+         s.hidden, s.heads, s.kv_heads, s.head_dim, s.intermediate);
+}
+
+}  // namespace
+
+namespace qd {
+qd_status guard_call(void (*fn)(void *), void *ctx) {
+  return guard([&] { fn(ctx); });
+}
+}  // namespace qd
+
+extern "C" {
+
+const char *qd_status_string(qd_status s) {
+  switch (s) {
+    case QD_SUCCESS: return "success";
+    case QD_ERROR_INVALID_ARGUMENT: return "invalid argument";
+    case QD_ERROR_NOT_INITIALIZED: return "not initialized";
+    case QD_ERROR_ALREADY_INITIALIZED: return "already initialized";
+    case QD_ERROR_NOT_SUPPORTED: return "not supported";
+    case QD_ERROR_RUNTIME: return "runtime error";
+    case QD_ERROR_DEVICE_FAULT: return "device fault";
+  }
+  return "unknown status";
+}
+
+const char *qd_last_error(void) { return g_error.c_str(); }
+
+uint32_t qd_abi_version(void) { return kAbiVersion; }
+
+qd_status qd_device_count(uint32_t *count) {
+  return guard([&] {
+    if (!count) fail(QD_ERROR_INVALID_ARGUMENT, "count is null");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = static_cast<uint32_t>(std::max(n, 0));
+  });
+}
+
+qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
+  return guard([&] {
+    if (!config || !out) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    const qd_config &c = *config;
+    if (c.hidden == 0 || c.heads == 0 || c.kv_heads == 0 || c.intermediate == 0 ||
+        c.vocab == 0 || c.layers == 0 || c.capacity == 0 || c.max_batch == 0)
+      fail(QD_ERROR_INVALID_ARGUMENT, "zero-sized engine dimension");
+    if (c.heads % c.kv_heads != 0)
+      fail(QD_ERROR_INVALID_ARGUMENT, "heads %u not a multiple of kv_heads %u", c.heads, c.kv_heads);
+    if (!(c.rms_eps > 0.0f) || !(c.rope_theta > 0.0f))
+      fail(QD_ERROR_INVALID_ARGUMENT, "rms_eps and rope_theta must be positive");
+    if (!qd::shape_supported(static_cast<int>(c.hidden), static_cast<int>(c.intermediate),
+                             static_cast<int>(c.heads), static_cast<int>(c.kv_heads),
+                             static_cast<int>(c.head_dim)))
+      fail(QD_ERROR_NOT_SUPPORTED,
+           "unsupported shape: kernels are built for hidden 896, intermediate 4864, "
+           "head_dim 64, heads*head_dim == hidden");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+      fail(QD_ERROR_NOT_SUPPORTED, "no HIP device visible");
+    if (c.device < 0 || c.device >= ndev)
+      fail(QD_ERROR_INVALID_ARGUMENT, "device %d out of range (%d visible)", c.device, ndev);
+
+    auto e = std::make_unique<qd_engine>();
+    e->cfg = c;
+    e->H = c.hidden;
+    e->I = c.intermediate;
+    e->NQ = c.heads;
+    e->NKV = c.kv_heads;
+    e->QD = size_t(c.heads) * qd::kHeadDim;
+    e->KVD = size_t(c.kv_heads) * qd::kHeadDim;
+    e->QKV = e->QD + 2 * e->KVD;
+    e->V = c.vocab;
+    e->L = c.layers;
+    e->CAP = c.capacity;
+    e->B = c.max_batch;
+    e->max_chunks = static_cast<int>((e->CAP + qd::kAttnChunk - 1) / qd::kAttnChunk);
+    e->set_device();
+    check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
+    check(hipEventCreate(&e->ev_begin), "hipEventCreate");
+    check(hipEventCreate(&e->ev_end), "hipEventCreate");
+
+    // Layer weights in one arena: per layer wqkv | bqkv | wo | wg | wu | wd |
+    // attn_norm | mlp_norm, each 256-byte aligned.
+    auto round = [](size_t n) { return (n + 63) / 64 * 64; };  // floats
+    const size_t per_layer = round(e->QKV * e->H) + round(e->QKV) + round(e->H * e->QD) +
+                             2 * round(e->I * e->H) + round(e->H * e->I) + 2 * round(e->H);
+    e->weights = e->alloc<float>(per_layer * e->L);
+    e->layers.resize(e->L);
+    for (size_t l = 0; l < e->L; ++l) {
+      float *p = e->weights + l * per_layer;
+      qd::LayerPtrs &w = e->layers[l];
+      w.wqkv = p; p += round(e->QKV * e->H);
+      w.bqkv = p; p += round(e->QKV);
+      w.wo = p; p += round(e->H * e->QD);
+      w.wg = p; p += round(e->I * e->H);
+      w.wu = p; p += round(e->I * e->H);
+      w.wd = p; p += round(e->H * e->I);
+      w.attn_norm = p; p += round(e->H);
+      w.mlp_norm = p;
+    }
+    e->embed = e->alloc<float>(e->V * e->H);
+    e->lm_head = c.tied_lm_head ? e->embed : e->alloc<float>(e->V * e->H);
+    e->final_norm = e->alloc<float>(e->H);
+    e->k_cache = e->alloc<float>(e->B * e->L * e->CAP * e->KVD);
+    e->v_cache = e->alloc<float>(e->B * e->L * e->CAP * e->KVD);
+    e->rope_cos = e->alloc<float>(e->CAP * qd::kRotary);
+    e->rope_sin = e->alloc<float>(e->CAP * qd::kRotary);
+    e->hidden = e->alloc<float>(e->B * e->H);
+    e->q = e->alloc<float>(e->B * e->QD);
+    e->attn = e->alloc<float>(e->B * e->QD);
+    e->act = e->alloc<float>(e->B * e->I);
+    e->logits = e->alloc<float>(e->B * e->V);
+    e->part_m = e->alloc<float>(size_t(e->max_chunks) * e->NQ);
+    e->part_l = e->alloc<float>(size_t(e->max_chunks) * e->NQ);
+    e->part_acc = e->alloc<float>(size_t(e->max_chunks) * e->NQ * qd::kHeadDim);
+    e->part_val = e->alloc<float>(kLmHeadParts);
+    e->part_idx = e->alloc<uint32_t>(kLmHeadParts);
+    e->tokens_dev = e->alloc<uint32_t>(e->CAP);
+    e->states = e->alloc<qd::SeqState>(e->B);
+    check(hipMemsetAsync(e->k_cache, 0, e->B * e->L * e->CAP * e->KVD * 4, e->stream), "memset");
+    check(hipMemsetAsync(e->v_cache, 0, e->B * e->L * e->CAP * e->KVD * 4, e->stream), "memset");
+    check(hipMemsetAsync(e->states, 0, e->B * sizeof(qd::SeqState), e->stream), "memset");
+    check(hipHostMalloc(reinterpret_cast<void **>(&e->h_states), e->B * sizeof(qd::SeqState),
+                        hipHostMallocDefault),
+          "hipHostMalloc");
+    check(hipHostMalloc(reinterpret_cast<void **>(&e->h_tokens), e->CAP * sizeof(uint32_t),
+                        hipHostMallocDefault),
+          "hipHostMalloc");
+    e->positions.assign(e->B, 0);
+    e->build_rope_tables(c.rope_theta);
+    *out = e.release();
+  });
+}
+
+qd_status qd_engine_destroy(qd_engine *engine) {
+  return guard([&] {
+    if (!engine) return;
+    engine->set_device();
+    delete engine;
+  });
+}
+
+qd_status qd_engine_config(const qd_engine *e, qd_config *config) {
+  return guard([&] {
+    if (!e || !config) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    *config = e->cfg;
+  });
+}
+
+qd_status qd_engine_device_bytes(const qd_engine *e, uint64_t *bytes) {
+  return guard([&] {
+    if (!e || !bytes) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    *bytes = e->device_bytes;
+  });
+}
+
+qd_status qd_load_synthetic(qd_engine *e, uint64_t seed, const qd_synthetic_init *init) {
+  return guard([&] {
+    if (!e || !init) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->set_device();
+    // Two pinned staging buffers, alternating, so host generation of one
+    // chunk overlaps the copy of the previous one.
+    const size_t chunk = size_t(16) << 20;  // floats
+    float *stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    auto cleanup = [&] {
+      for (int k = 0; k < 2; ++k) {
+        if (done[k]) (void)hipEventDestroy(done[k]);
+        if (stage[k]) (void)hipHostFree(stage[k]);
+      }
+    };
+    try {
+      for (int k = 0; k < 2; ++k) {
+        check(hipHostMalloc(reinterpret_cast<void **>(&stage[k]), chunk * 4, hipHostMallocDefault),
+              "hipHostMalloc");
+        check(hipEventCreateWithFlags(&done[k], hipEventDisableTiming), "hipEventCreate");
+      }
+      int slot = 0;
+      bool pending[2] = {false, false};
+      auto emit = [&](float *dst, size_t n, uint64_t stream_id, float stddev, bool constant) {
+        for (size_t off = 0; off < n; off += chunk) {
+          const size_t m = std::min(chunk, n - off);
+          if (pending[slot]) check(hipEventSynchronize(done[slot]), "stage sync");
+          if (constant) {
+            std::fill(stage[slot], stage[slot] + m, stddev);
+          } else {
+            fill_normal(stage[slot], m, off, seed, stream_id, stddev);
+          }
+          e->upload(dst + off, stage[slot], m);
+          check(hipEventRecord(done[slot], e->stream), "hipEventRecord");
+          pending[slot] = true;
+          slot ^= 1;
+        }
+      };
+      namespace b = qd::bundle;
+      for (size_t l = 0; l < e->L; ++l) {
+        const uint32_t li = static_cast<uint32_t>(l);
+        const qd::LayerPtrs &w = e->layers[l];
+        float *wq = const_cast<float *>(w.wqkv);
+        float *bq = const_cast<float *>(w.bqkv);
+        emit(wq, e->QD * e->H, qd::rng::layer_stream(li, b::kQW), init->weight_std, false);
+        emit(wq + e->QD * e->H, e->KVD * e->H, qd::rng::layer_stream(li, b::kKW), init->weight_std, false);
+        emit(wq + (e->QD + e->KVD) * e->H, e->KVD * e->H, qd::rng::layer_stream(li, b::kVW),
+             init->weight_std, false);
+        emit(bq, e->QD, qd::rng::layer_stream(li, b::kQB), init->bias_std, false);
+        emit(bq + e->QD, e->KVD, qd::rng::layer_stream(li, b::kKB), init->bias_std, false);
+        emit(bq + e->QD + e->KVD, e->KVD, qd::rng::layer_stream(li, b::kVB), init->bias_std, false);
+        emit(const_cast<float *>(w.wo), e->H * e->QD, qd::rng::layer_stream(li, b::kOW),
+             init->weight_std, false);
+        emit(const_cast<float *>(w.wg), e->I * e->H, qd::rng::layer_stream(li, b::kGateW),
+             init->weight_std, false);
+        emit(const_cast<float *>(w.wu), e->I * e->H, qd::rng::layer_stream(li, b::kUpW),
+             init->weight_std, false);
+        emit(const_cast<float *>(w.wd), e->H * e->I, qd::rng::layer_stream(li, b::kDownW),
+             init->weight_std, false);
+        emit(const_cast<float *>(w.attn_norm), e->H, 0, init->norm_gain, true);
+        emit(const_cast<float *>(w.mlp_norm), e->H, 0, init->norm_gain, true);
+      }
+      emit(e->embed, e->V * e->H, qd::rng::tail_stream(0), init->weight_std, false);
+      emit(e->final_norm, e->H, 0, init->norm_gain, true);
+      if (e->lm_head != e->embed)
+        emit(e->lm_head, e->V * e->H, qd::rng::tail_stream(2), init->weight_std, false);
+      e->sync();
+    } catch (...) {
+      (void)hipStreamSynchronize(e->stream);
+      cleanup();
+      throw;
+    }
+    cleanup();
+    e->loaded = true;
+  });
+}
+
+qd_status qd_load_bundle(qd_engine *e, const char *directory) {
+  return guard([&] {
+    if (!e || !directory) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->set_device();
+    const std::string dir(directory);
+    float theta = 0.0f;
+    for (size_t l = 0; l < e->L; ++l) {
+      const std::string path = dir + "/layer_" + std::to_string(l) + "/weights.json";
+      qd::bundle::LayerWeights w = qd::bundle::load_layer(path);
+      layer_shape_matches(*e, w);
+      if (l == 0) {
+        theta = w.rope_theta;
+      } else if (w.rope_theta != theta) {
+        fail(QD_ERROR_INVALID_ARGUMENT, "decoder layers use different rope_theta");
+      }
+      namespace b = qd::bundle;
+      const qd::LayerPtrs &p = e->layers[l];
+      float *wq = const_cast<float *>(p.wqkv);
+      float *bq = const_cast<float *>(p.bqkv);
+      e->upload(wq, w.tensors[b::kQW].data(), e->QD * e->H);
+      e->upload(wq + e->QD * e->H, w.tensors[b::kKW].data(), e->KVD * e->H);
+      e->upload(wq + (e->QD + e->KVD) * e->H, w.tensors[b::kVW].data(), e->KVD * e->H);
+      e->upload(bq, w.tensors[b::kQB].data(), e->QD);
+      e->upload(bq + e->QD, w.tensors[b::kKB].data(), e->KVD);
+      e->upload(bq + e->QD + e->KVD, w.tensors[b::kVB].data(), e->KVD);
+      e->upload(const_cast<float *>(p.wo), w.tensors[b::kOW].data(), e->H * e->QD);
+      e->upload(const_cast<float *>(p.wg), w.tensors[b::kGateW].data(), e->I * e->H);
+      e->upload(const_cast<float *>(p.wu), w.tensors[b::kUpW].data(), e->I * e->H);
+      e->upload(const_cast<float *>(p.wd), w.tensors[b::kDownW].data(), e->H * e->I);
+      e->upload(const_cast<float *>(p.attn_norm), w.tensors[b::kAttnNorm].data(), e->H);
+      e->upload(const_cast<float *>(p.mlp_norm), w.tensors[b::kMlpNorm].data(), e->H);
+      e->sync();  // host vectors die at the end of this iteration
+    }
+    qd::bundle::TailWeights t = qd::bundle::load_tail(dir + "/model_tail/weights.json");
+    // The persistent path requires full-vocabulary embeddings in vocabulary
+    // order (benchmarks/qwen_stateful_graph.cpp:635-653).
+    if (t.hidden != e->H || t.vocab != e->V || t.token_ids.size() != e->V)
+      fail(QD_ERROR_INVALID_ARGUMENT, "model tail requires full-vocabulary embeddings");
+    for (uint32_t i = 0; i < t.vocab; ++i)
+      if (t.token_ids[i] != i)
+        fail(QD_ERROR_INVALID_ARGUMENT, "model tail embeddings must use vocabulary order");
+    if (e->lm_head == e->embed &&
+        std::memcmp(t.lm_head_weight.data(), t.token_embeddings.data(),
+                    t.lm_head_weight.size() * sizeof(float)) != 0)
+      fail(QD_ERROR_INVALID_ARGUMENT,
+           "engine has a tied LM head but the bundle's lm_head_weight differs from "
+           "its token_embeddings");
+    e->upload(e->embed, t.token_embeddings.data(), e->V * e->H);
+    e->upload(e->final_norm, t.final_norm_weight.data(), e->H);
+    if (e->lm_head != e->embed) e->upload(e->lm_head, t.lm_head_weight.data(), e->V * e->H);
+    e->sync();
+    if (theta != e->cfg.rope_theta) e->build_rope_tables(theta);
+    e->loaded = true;
+  });
+}
+
+qd_status qd_read_weight(qd_engine *e, uint32_t layer, uint32_t kind, float *out, size_t count) {
+  return guard([&] {
+    if (!e || !out) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->set_device();
+    const float *src = nullptr;
+    size_t n = 0;
+    namespace b = qd::bundle;
+    if (kind == 0x100) {
+      src = e->embed; n = e->V * e->H;
+    } else if (kind == 0x101) {
+      src = e->final_norm; n = e->H;
+    } else if (kind == 0x102) {
+      src = e->lm_head; n = e->V * e->H;
+    } else if (kind < b::kLayerTensorCount && layer < e->L) {
+      const qd::LayerPtrs &p = e->layers[layer];
+      switch (kind) {
+        case b::kAttnNorm: src = p.attn_norm; n = e->H; break;
+        case b::kMlpNorm: src = p.mlp_norm; n = e->H; break;
+        case b::kQW: src = p.wqkv; n = e->QD * e->H; break;
+        case b::kKW: src = p.wqkv + e->QD * e->H; n = e->KVD * e->H; break;
+        case b::kVW: src = p.wqkv + (e->QD + e->KVD) * e->H; n = e->KVD * e->H; break;
+        case b::kQB: src = p.bqkv; n = e->QD; break;
+        case b::kKB: src = p.bqkv + e->QD; n = e->KVD; break;
+        case b::kVB: src = p.bqkv + e->QD + e->KVD; n = e->KVD; break;
+        case b::kOW: src = p.wo; n = e->H * e->QD; break;
+        case b::kGateW: src = p.wg; n = e->I * e->H; break;
+        case b::kUpW: src = p.wu; n = e->I * e->H; break;
+        case b::kDownW: src = p.wd; n = e->H * e->I; break;
+      }
+    }
+    if (!src) fail(QD_ERROR_INVALID_ARGUMENT, "unknown tensor layer %u kind %u", layer, kind);
+    if (count != n) fail(QD_ERROR_INVALID_ARGUMENT, "tensor has %zu elements, caller asked %zu", n, count);
+    check(hipMemcpyAsync(out, src, n * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    e->sync();
+  });
+}
+
+qd_status qd_kv_reset(qd_engine *e, uint32_t seq, uint32_t position) {
+  return guard([&] {
+    if (!e) fail(QD_ERROR_INVALID_ARGUMENT, "null engine");
+    e->check_seq(seq);
+    if (position > e->CAP) fail(QD_ERROR_INVALID_ARGUMENT, "position %u beyond capacity %zu", position, e->CAP);
+    e->set_device();
+    e->positions[seq] = position;
+    e->push_state(seq, 0, qd::kModeStep, UINT32_MAX, 0);
+    e->sync();
+  });
+}
+
+static void kv_copy(qd_engine *e, uint32_t seq, uint32_t layer, uint32_t start, uint32_t count,
+                    float *k, float *v, bool write) {
+  if (!e) fail(QD_ERROR_INVALID_ARGUMENT, "null engine");
+  e->check_seq(seq);
+  if (layer >= e->L) fail(QD_ERROR_INVALID_ARGUMENT, "layer %u out of range", layer);
+  if (size_t(start) + count > e->CAP)
+    fail(QD_ERROR_INVALID_ARGUMENT, "positions [%u, %u) beyond capacity %zu", start, start + count, e->CAP);
+  if (count == 0) return;
+  e->set_device();
+  const size_t off = size_t(start) * e->KVD;
+  const size_t bytes = size_t(count) * e->KVD * 4;
+  float *dk = e->kv_slice(e->k_cache, seq, layer) + off;
+  float *dv = e->kv_slice(e->v_cache, seq, layer) + off;
+  const hipMemcpyKind kind = write ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+  if (k) check(hipMemcpyAsync(write ? static_cast<void *>(dk) : k, write ? static_cast<const void *>(k) : dk, bytes, kind, e->stream), "kv copy");
+  if (v) check(hipMemcpyAsync(write ? static_cast<void *>(dv) : v, write ? static_cast<const void *>(v) : dv, bytes, kind, e->stream), "kv copy");
+  e->sync();
+}
+
+qd_status qd_write_kv(qd_engine *e, uint32_t seq, uint32_t layer, uint32_t start, uint32_t count,
+                      const float *k, const float *v) {
+  return guard([&] { kv_copy(e, seq, layer, start, count, const_cast<float *>(k), const_cast<float *>(v), true); });
+}
+
+qd_status qd_read_kv(qd_engine *e, uint32_t seq, uint32_t layer, uint32_t start, uint32_t count,
+                     float *k, float *v) {
+  return guard([&] { kv_copy(e, seq, layer, start, count, k, v, false); });
+}
+
+qd_status qd_read_decode_state(qd_engine *e, uint32_t seq, qd_decode_state *out) {
+  return guard([&] {
+    if (!e || !out) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_seq(seq);
+    e->set_device();
+    qd::SeqState s{};
+    check(hipMemcpyAsync(&s, e->states + seq, sizeof(s), hipMemcpyDeviceToHost, e->stream), "D2H");
+    e->sync();
+    out->token_position = s.position;
+    out->kv_length = s.position;
+    out->sampled_token = s.token;
+    out->eos_token = s.eos;
+    out->generated_tokens = s.generated;
+    out->maximum_tokens = s.max_tokens;
+    out->stop_reason = s.stop_reason;
+    out->sampled_logit = s.top_logit;
+  });
+}
+
+qd_status qd_layer_step(qd_engine *e, uint32_t seq, uint32_t layer, float *hidden) {
+  return guard([&] {
+    if (!e || !hidden) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_seq(seq);
+    e->check_loaded();
+    if (layer >= e->L) fail(QD_ERROR_INVALID_ARGUMENT, "layer %u out of range", layer);
+    if (e->positions[seq] >= e->CAP)
+      fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full (capacity %zu)", seq, e->CAP);
+    e->set_device();
+    e->push_state(seq, 0, qd::kModeStep, UINT32_MAX, 0);
+    e->upload(e->hidden + seq * e->H, hidden, e->H);
+    check(qd::launch_layer(e->stream, e->layer_args(seq, layer)), "layer launch");
+    check(hipMemcpyAsync(hidden, e->hidden + seq * e->H, e->H * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    e->sync();
+  });
+}
+
+qd_status qd_step(qd_engine *e, uint32_t seq, uint32_t token, float *logits_out, uint32_t *greedy,
+                  float *top_logit) {
+  return guard([&] {
+    if (!e) fail(QD_ERROR_INVALID_ARGUMENT, "null engine");
+    e->check_seq(seq);
+    e->check_loaded();
+    if (token >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab %zu", token, e->V);
+    if (e->positions[seq] >= e->CAP)
+      fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full (capacity %zu)", seq, e->CAP);
+    e->set_device();
+    e->push_state(seq, token, qd::kModeStep, UINT32_MAX, 0);
+    float *dev_logits = e->logits + seq * e->V;
+    e->enqueue_step(seq, dev_logits, 0, nullptr);
+    check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState),
+                         hipMemcpyDeviceToHost, e->stream), "D2H");
+    if (logits_out)
+      check(hipMemcpyAsync(logits_out, dev_logits, e->V * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    e->sync();
+    e->positions[seq] += 1;
+    if (greedy) *greedy = e->h_states[seq].token;
+    if (top_logit) *top_logit = e->h_states[seq].top_logit;
+  });
+}
+
+qd_status qd_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t n, float *last_logits,
+                     uint32_t *greedy, float *top_logit) {
+  return guard([&] {
+    if (!e || (!tokens && n)) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_seq(seq);
+    e->check_loaded();
+    if (n == 0) fail(QD_ERROR_INVALID_ARGUMENT, "empty prompt");
+    if (size_t(e->positions[seq]) + n > e->CAP)
+      fail(QD_ERROR_INVALID_ARGUMENT, "prompt of %u tokens overflows capacity %zu at position %u", n, e->CAP,
+           e->positions[seq]);
+    for (uint32_t i = 0; i < n; ++i)
+      if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u at %u >= vocab", tokens[i], i);
+    e->set_device();
+    // Sequential decode steps; the argmax finaliser advances the position and
+    // the next token is pushed from the host mirror.
+    for (uint32_t i = 0; i < n; ++i) {
+      e->push_state(seq, tokens[i], qd::kModeStep, UINT32_MAX, 0);
+      e->enqueue_step(seq, e->logits + seq * e->V, 0, nullptr);
+      e->positions[seq] += 1;
+      e->sync();  // h_states[seq] is reused by the next push
+    }
+    check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState),
+                         hipMemcpyDeviceToHost, e->stream), "D2H");
+    if (last_logits)
+      check(hipMemcpyAsync(last_logits, e->logits + seq * e->V, e->V * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    e->sync();
+    if (greedy) *greedy = e->h_states[seq].token;
+    if (top_logit) *top_logit = e->h_states[seq].top_logit;
+  });
+}
+
+qd_status qd_step_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, const uint32_t *tokens,
+                        float *logits, uint32_t *greedy) {
+  return guard([&] {
+    if (!e || !seq_ids || !tokens) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_loaded();
+    if (n_seq == 0 || n_seq > e->B) fail(QD_ERROR_INVALID_ARGUMENT, "n_seq %u out of range", n_seq);
+    std::vector<bool> seen(e->B, false);
+    for (uint32_t i = 0; i < n_seq; ++i) {
+      e->check_seq(seq_ids[i]);
+      if (seen[seq_ids[i]]) fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u listed twice", seq_ids[i]);
+      seen[seq_ids[i]] = true;
+      if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", tokens[i]);
+      if (e->positions[seq_ids[i]] >= e->CAP) fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full", seq_ids[i]);
+    }
+    e->set_device();
+    for (uint32_t i = 0; i < n_seq; ++i) {
+      const uint32_t s = seq_ids[i];
+      e->push_state(s, tokens[i], qd::kModeStep, UINT32_MAX, 0);
+      e->enqueue_step(s, e->logits + size_t(s) * e->V, 0, nullptr);
+    }
+    for (uint32_t i = 0; i < n_seq; ++i) {
+      const uint32_t s = seq_ids[i];
+      check(hipMemcpyAsync(&e->h_states[s], e->states + s, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
+                           e->stream), "D2H");
+      if (logits)
+        check(hipMemcpyAsync(logits + size_t(i) * e->V, e->logits + size_t(s) * e->V, e->V * 4,
+                             hipMemcpyDeviceToHost, e->stream), "D2H");
+    }
+    e->sync();
+    for (uint32_t i = 0; i < n_seq; ++i) {
+      e->positions[seq_ids[i]] += 1;
+      if (greedy) greedy[i] = e->h_states[seq_ids[i]].token;
+    }
+  });
+}
+
+qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token, uint32_t max_tokens,
+                               uint32_t eos, uint32_t *out_tokens, uint32_t *generated,
+                               uint32_t *stop_reason, float *all_logits) {
+  return guard([&] {
+    if (!e || !out_tokens) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_seq(seq);
+    e->check_loaded();
+    if (max_tokens == 0) fail(QD_ERROR_INVALID_ARGUMENT, "max_tokens must be positive");
+    if (first_token >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", first_token);
+    if (size_t(e->positions[seq]) + max_tokens > e->CAP)
+      fail(QD_ERROR_INVALID_ARGUMENT, "generation of %u tokens from position %u overflows capacity %zu",
+           max_tokens, e->positions[seq], e->CAP);
+    e->set_device();
+    float *hist = e->logits + size_t(seq) * e->V;
+    int use_hist = 0;
+    if (all_logits) {
+      if (e->history_rows < max_tokens) {
+        if (e->history) {
+          check(hipFree(e->history), "hipFree");
+          e->allocs.erase(std::find(e->allocs.begin(), e->allocs.end(), static_cast<void *>(e->history)));
+          e->device_bytes -= std::max<size_t>(e->history_rows * e->V * 4, 256);
+        }
+        e->history = e->alloc<float>(size_t(max_tokens) * e->V);
+        e->history_rows = max_tokens;
+      }
+      hist = e->history;
+      use_hist = 1;
+    }
+    e->push_state(seq, first_token, qd::kModeGenerate, eos, max_tokens);
+    check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
+    for (uint32_t t = 0; t < max_tokens; ++t) e->enqueue_step(seq, hist, use_hist, e->tokens_dev);
+    check(hipEventRecord(e->ev_end, e->stream), "hipEventRecord");
+    check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
+                         e->stream), "D2H");
+    e->sync();
+    const qd::SeqState &s = e->h_states[seq];
+    const uint32_t n = s.generated;
+    check(hipMemcpyAsync(out_tokens, e->tokens_dev, size_t(n) * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    if (all_logits && n)
+      check(hipMemcpyAsync(all_logits, e->history, size_t(n) * e->V * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    e->sync();
+    float ms = 0.f;
+    check(hipEventElapsedTime(&ms, e->ev_begin, e->ev_end), "hipEventElapsedTime");
+    e->timing.total_us = ms * 1000.0;
+    e->timing.tokens = n;
+    e->timing.per_token_us = n ? e->timing.total_us / n : 0.0;
+    e->positions[seq] = s.position;
+    if (generated) *generated = n;
+    if (stop_reason) *stop_reason = s.stop_reason;
+  });
+}
+
+namespace {
+
+// Event pair around every launch; durations are read after one sync.
+struct EventMarker : qd::Marker {
+  qd_engine *e;
+  std::vector<hipEvent_t> pool;
+  std::vector<std::pair<int, size_t>> open;  // (kernel, begin event index)
+  std::vector<std::tuple<int, size_t, size_t, double>> spans;  // kernel, begin, end, length
+  size_t used = 0;
+  double length = 0;
+  explicit EventMarker(qd_engine *engine) : e(engine) {}
+  ~EventMarker() override {
+    for (hipEvent_t ev : pool) (void)hipEventDestroy(ev);
+  }
+  size_t next() {
+    if (used == pool.size()) {
+      hipEvent_t ev;
+      check(hipEventCreate(&ev), "hipEventCreate");
+      pool.push_back(ev);
+    }
+    check(hipEventRecord(pool[used], e->stream), "hipEventRecord");
+    return used++;
+  }
+  void before(int kernel) override { open.emplace_back(kernel, next()); }
+  void after(int kernel) override {
+    const size_t b = open.back().second;
+    open.pop_back();
+    spans.emplace_back(kernel, b, next(), length);
+  }
+};
+
+}  // namespace
+
+qd_status qd_profile_kernels(qd_engine *e, uint32_t seq, uint32_t first_token, uint32_t tokens,
+                             qd_kernel_stat *stats, uint32_t capacity, uint32_t *count) {
+  return guard([&] {
+    if (!e || !stats || !count) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_seq(seq);
+    e->check_loaded();
+    if (tokens == 0) fail(QD_ERROR_INVALID_ARGUMENT, "tokens must be positive");
+    if (first_token >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", first_token);
+    if (size_t(e->positions[seq]) + tokens > e->CAP)
+      fail(QD_ERROR_INVALID_ARGUMENT, "profiling %u tokens overflows capacity", tokens);
+    e->set_device();
+    EventMarker marker(e);
+    e->push_state(seq, first_token, qd::kModeGenerate, UINT32_MAX, tokens);
+    for (uint32_t t = 0; t < tokens; ++t) {
+      marker.length = double(e->positions[seq]) + t + 1;
+      e->enqueue_step(seq, e->logits + size_t(seq) * e->V, 0, e->tokens_dev, &marker);
+    }
+    e->sync();
+    e->positions[seq] += tokens;
+    std::vector<qd_kernel_stat> agg(qd::kKernelCount);
+    for (int k = 0; k < qd::kKernelCount; ++k) {
+      std::memset(&agg[k], 0, sizeof(qd_kernel_stat));
+      std::snprintf(agg[k].name, sizeof(agg[k].name), "%s", qd::kernel_name(k));
+    }
+    for (const auto &span : marker.spans) {
+      float ms = 0.f;
+      check(hipEventElapsedTime(&ms, marker.pool[std::get<1>(span)], marker.pool[std::get<2>(span)]),
+            "hipEventElapsedTime");
+      qd_kernel_stat &s = agg[std::get<0>(span)];
+      s.launches += 1;
+      s.total_us += ms * 1000.0;
+      s.bytes += e->kernel_bytes(std::get<0>(span), std::get<3>(span));
+    }
+    uint32_t n = 0;
+    for (const auto &s : agg) {
+      if (s.launches == 0) continue;
+      if (n < capacity) stats[n] = s;
+      ++n;
+    }
+    *count = std::min(n, capacity);
+  });
+}
+
+qd_status qd_last_timing(const qd_engine *e, qd_timing *timing) {
+  return guard([&] {
+    if (!e || !timing) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    *timing = e->timing;
+  });
+}
+
+qd_status qd_sync(qd_engine *e) {
+  return guard([&] {
+    if (!e) fail(QD_ERROR_INVALID_ARGUMENT, "null engine");
+    e->set_device();
+    e->sync();
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,646 @@
+// Qwen2 FP32 decode-step kernels for gfx950 (CDNA4, wave64).
+//
+// Every kernel is bandwidth-bound: weights stream from HBM once per token in
+// 128-bit (float4) coalesced loads, each wave owns whole output rows, and the
+// activation operand sits in per-lane registers whose slot layout matches the
+// weight slots the lane loads. Reductions are wave64 butterflies.
+//
+// Reference semantics (file:line under the reference tree):
+//   RMSNorm                 benchmarks/qwen_stateful_graph_kernel.cpp:665-701
+//   QKV + bias              benchmarks/qwen_stateful_graph_kernel.cpp:392-492
+//   RoPE + KV-cache write   benchmarks/qwen_stateful_graph_kernel.cpp:517-552
+//   GQA attention           benchmarks/qwen_stateful_graph_kernel.cpp:554-600
+//   O projection + residual benchmarks/qwen_stateful_graph_kernel.cpp:602-659
+//   gate/up + SiLU          benchmarks/qwen_stateful_graph_kernel.cpp:494-515
+//   down + residual         benchmarks/qwen_stateful_graph_kernel.cpp:158-223,749-760
+//   LM head + top-1         benchmarks/qwen_stateful_graph_kernel.cpp:225-356
+//   embedding feedback      benchmarks/qwen_stateful_graph_kernel.cpp:358-390
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "qd_device.hpp"
+#include "qd_kernels.hpp"
+
+namespace qd {
+namespace {
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float fma4(float4 w, float4 x, float acc) {
+  acc = fmaf(w.x, x.x, acc);
+  acc = fmaf(w.y, x.y, acc);
+  acc = fmaf(w.z, x.z, acc);
+  acc = fmaf(w.w, x.w, acc);
+  return acc;
+}
+
+// Greater value wins; equal values go to the lower index; NaN never wins
+// (benchmarks/qwen_stateful_graph_kernel.cpp:225-229).
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv,
+                                       uint32_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// 1/rms of x[0..N) computed by the whole workgroup (every thread gets it).
+template <int N>
+__device__ float block_inv_rms(const float *x, float eps, float *red) {
+  constexpr int N4 = N / 4;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  float s = 0.f;
+  for (int c = threadIdx.x; c < N4; c += kBlock) {
+    const float4 v = x4[c];
+    s = fmaf(v.x, v.x, s);
+    s = fmaf(v.y, v.y, s);
+    s = fmaf(v.z, v.z, s);
+    s = fmaf(v.w, v.w, s);
+  }
+  s = wave_sum(s);
+  if (lane_id() == 0) red[wave_id()] = s;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWavesPerBlock; ++w) t += red[w];
+  __syncthreads();
+  return rsqrtf(t / static_cast<float>(N) + eps);
+}
+
+// A wave computes the dot products of two weight rows with one K-vector.
+// The two rows are viewed as one run of 2*K/4 float4 slots; lane l loads
+// slots f = 64*j + l. The operand register xv[j] holds the x float4 that
+// slot f multiplies, so the same registers serve every row pair.
+template <int K>
+struct PairSlots {
+  static_assert(K % 4 == 0, "rows must be float4 aligned");
+  static constexpr int K4 = K / 4;
+  static constexpr int NJ = (2 * K4 + kWave - 1) / kWave;
+};
+
+// xv[j] = x[c] (optionally * inv * gain[c]) for the column c of slot j.
+template <int K, bool kNorm>
+__device__ __forceinline__ void load_pair_operand(
+    const float *x, float inv, const float *gain,
+    float4 (&xv)[PairSlots<K>::NJ]) {
+  constexpr int K4 = PairSlots<K>::K4;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const float4 *g4 = reinterpret_cast<const float4 *>(gain);
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < PairSlots<K>::NJ; ++j) {
+    const int f = j * kWave + lane;
+    const int c = f < K4 ? f : f - K4;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (f < 2 * K4) {
+      v = x4[c];
+      if (kNorm) {
+        const float4 g = g4[c];
+        v.x = v.x * inv * g.x;
+        v.y = v.y * inv * g.y;
+        v.z = v.z * inv * g.z;
+        v.w = v.w * inv * g.w;
+      }
+    }
+    xv[j] = v;
+  }
+}
+
+// Dot products of rows a and b (K floats each) with the slot operand.
+// Returns wave-reduced sums in every lane.
+template <int K>
+__device__ __forceinline__ void dot_pair(const float *a, const float *b,
+                                         const float4 (&xv)[PairSlots<K>::NJ],
+                                         float &sa, float &sb) {
+  constexpr int K4 = PairSlots<K>::K4;
+  constexpr int NJ = PairSlots<K>::NJ;
+  const float4 *a4 = reinterpret_cast<const float4 *>(a);
+  const float4 *b4 = reinterpret_cast<const float4 *>(b);
+  const int lane = lane_id();
+  float4 w[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int f = j * kWave + lane;
+    if (j * kWave + kWave <= K4) {
+      w[j] = a4[f];
+    } else if (j * kWave >= K4) {
+      w[j] = f < 2 * K4 ? b4[f - K4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+      w[j] = *(f < K4 ? a4 + f : b4 + (f - K4));
+    }
+  }
+  float accA = 0.f, accB = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int f = j * kWave + lane;
+    if (j * kWave + kWave <= K4) {
+      accA = fma4(w[j], xv[j], accA);
+    } else if (j * kWave >= K4) {
+      accB = fma4(w[j], xv[j], accB);
+    } else {
+      const float d = fma4(w[j], xv[j], 0.f);
+      if (f < K4) {
+        accA += d;
+      } else {
+        accB += d;
+      }
+    }
+  }
+  sa = wave_sum(accA);
+  sb = wave_sum(accB);
+}
+
+// Single-row dot for K a multiple of 256 floats: lane l loads float4 slots
+// 64*j + l; xv[j] is the matching operand.
+template <int K>
+struct RowSlots {
+  static_assert(K % (4 * kWave) == 0, "row must be a whole number of wave loads");
+  static constexpr int NJ = K / (4 * kWave);
+};
+
+template <int K>
+__device__ __forceinline__ void load_row_operand(
+    const float *x, float4 (&xv)[RowSlots<K>::NJ]) {
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < RowSlots<K>::NJ; ++j) xv[j] = x4[j * kWave + lane];
+}
+
+template <int K>
+__device__ __forceinline__ float dot_row(const float *a,
+                                         const float4 (&xv)[RowSlots<K>::NJ]) {
+  constexpr int NJ = RowSlots<K>::NJ;
+  const float4 *a4 = reinterpret_cast<const float4 *>(a);
+  const int lane = lane_id();
+  float4 w[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) w[j] = a4[j * kWave + lane];
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) acc = fma4(w[j], xv[j], acc);
+  return wave_sum(acc);
+}
+
+// ---- kernels ----------------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void embed_kernel(
+    const float *__restrict__ emb, const SeqState *__restrict__ st,
+    float *__restrict__ hidden, int H, int vocab) {
+  if (st->stopped || st->token >= static_cast<uint32_t>(vocab)) return;
+  const size_t base = static_cast<size_t>(st->token) * H;
+  for (int i = blockIdx.x * kBlock + threadIdx.x; i < H; i += gridDim.x * kBlock)
+    hidden[i] = emb[base + i];
+}
+
+// attention RMSNorm + packed QKV + bias + RoPE + KV-cache write.
+// Work unit u = (head, i): rows head*64+i and head*64+i+32 of the packed
+// matrix, which are exactly the pair a rotate-half rotation mixes. Heads
+// [0, nq) are queries, [nq, nq+nkv) keys, then values (not rotated).
+template <int H>
+__global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
+    const float *__restrict__ hidden, const float *__restrict__ gain,
+    const float *__restrict__ wqkv, const float *__restrict__ bqkv,
+    const float *__restrict__ rope_cos, const float *__restrict__ rope_sin,
+    const SeqState *__restrict__ st, float *__restrict__ q,
+    float *__restrict__ k_cache, float *__restrict__ v_cache, int nq, int nkv,
+    float eps, int capacity) {
+  __shared__ float red[kWavesPerBlock];
+  if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
+  const float inv = block_inv_rms<H>(hidden, eps, red);
+  float4 xv[PairSlots<H>::NJ];
+  load_pair_operand<H, true>(hidden, inv, gain, xv);
+  const int position = static_cast<int>(st->position);
+  const int kv_dim = nkv * kHeadDim;
+  const int units = (nq + 2 * nkv) * kRotary;
+  for (int u = blockIdx.x * kWavesPerBlock + wave_id(); u < units;
+       u += gridDim.x * kWavesPerBlock) {
+    const int head = u / kRotary;
+    const int i = u % kRotary;
+    const int ra = head * kHeadDim + i;
+    const int rb = ra + kRotary;
+    float sa, sb;
+    dot_pair<H>(wqkv + static_cast<size_t>(ra) * H,
+                wqkv + static_cast<size_t>(rb) * H, xv, sa, sb);
+    if (lane_id() == 0) {
+      const float a = sa + bqkv[ra];
+      const float b = sb + bqkv[rb];
+      if (head < nq + nkv) {
+        const float c = rope_cos[position * kRotary + i];
+        const float s = rope_sin[position * kRotary + i];
+        const float first = a * c - b * s;
+        const float second = b * c + a * s;
+        if (head < nq) {
+          q[ra] = first;
+          q[rb] = second;
+        } else {
+          float *dst = k_cache + static_cast<size_t>(position) * kv_dim +
+                       (head - nq) * kHeadDim;
+          dst[i] = first;
+          dst[i + kRotary] = second;
+        }
+      } else {
+        float *dst = v_cache + static_cast<size_t>(position) * kv_dim +
+                     (head - nq - nkv) * kHeadDim;
+        dst[i] = a;
+        dst[i + kRotary] = b;
+      }
+    }
+  }
+}
+
+// Split-KV decode attention: workgroup (chunk, kv head) scores the chunk's
+// positions against every query head of the group (the KV tile is read once
+// for all of them) and writes an online-softmax partial (max, sum, acc[64]).
+// Thread t owns position t/4 of the chunk and dims [16*(t%4), +16).
+__global__ __launch_bounds__(kBlock) void attn_partial_kernel(
+    const float *__restrict__ q, const float *__restrict__ k_cache,
+    const float *__restrict__ v_cache, const SeqState *__restrict__ st,
+    int nq, int nkv, float *__restrict__ part_m, float *__restrict__ part_l,
+    float *__restrict__ part_acc, int capacity) {
+  __shared__ float qs[kMaxGroup * kHeadDim];
+  __shared__ float red[kWavesPerBlock];
+  __shared__ float acc_red[kWavesPerBlock][kHeadDim];
+  if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
+  const int length = static_cast<int>(st->position) + 1;
+  const int chunk = blockIdx.x;
+  if (chunk * kAttnChunk >= length) return;
+  const int kvh = blockIdx.y;
+  const int group = nq / nkv;
+  const int kv_dim = nkv * kHeadDim;
+  const int t = threadIdx.x;
+  const int lane = lane_id();
+  const int quarter = t & 3;
+  const int j = chunk * kAttnChunk + (t >> 2);
+  const bool valid = j < length;
+
+  for (int e = t; e < group * kHeadDim; e += kBlock)
+    qs[e] = q[kvh * group * kHeadDim + e];
+
+  float4 kr[4], vr[4];
+  const size_t row = static_cast<size_t>(valid ? j : 0) * kv_dim +
+                     kvh * kHeadDim + quarter * 16;
+  const float4 *k4 = reinterpret_cast<const float4 *>(k_cache + row);
+  const float4 *v4 = reinterpret_cast<const float4 *>(v_cache + row);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    kr[e] = k4[e];
+    vr[e] = v4[e];
+  }
+  __syncthreads();
+
+  for (int g = 0; g < group; ++g) {
+    const float4 *q4 =
+        reinterpret_cast<const float4 *>(qs + g * kHeadDim + quarter * 16);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s = fma4(kr[e], q4[e], s);
+    s += __shfl_xor(s, 1, kWave);
+    s += __shfl_xor(s, 2, kWave);
+    s = valid ? s * rsqrtf(static_cast<float>(kHeadDim)) : -INFINITY;
+
+    float m = s;
+#pragma unroll
+    for (int o = 4; o < kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+    if (lane == 0) red[wave_id()] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+
+    const float p = valid ? expf(s - m) : 0.f;
+    float l = p;
+#pragma unroll
+    for (int o = 4; o < kWave; o <<= 1) l += __shfl_xor(l, o, kWave);
+    if (lane == 0) red[wave_id()] = l;
+
+    float a[16];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[4 * e + 0] = p * vr[e].x;
+      a[4 * e + 1] = p * vr[e].y;
+      a[4 * e + 2] = p * vr[e].z;
+      a[4 * e + 3] = p * vr[e].w;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+#pragma unroll
+      for (int o = 4; o < kWave; o <<= 1) a[e] += __shfl_xor(a[e], o, kWave);
+    }
+    if (lane < 4) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc_red[wave_id()][quarter * 16 + e] = a[e];
+    }
+    __syncthreads();
+    const int h = kvh * group + g;
+    if (t < kHeadDim) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWavesPerBlock; ++w) sum += acc_red[w][t];
+      part_acc[(static_cast<size_t>(chunk) * nq + h) * kHeadDim + t] = sum;
+    }
+    if (t == 0) {
+      part_m[chunk * nq + h] = m;
+      part_l[chunk * nq + h] = red[0] + red[1] + red[2] + red[3];
+    }
+    __syncthreads();
+  }
+}
+
+// Merges the split-KV partials of each query head into attn[h*64 + d].
+__global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(
+    const float *__restrict__ part_m, const float *__restrict__ part_l,
+    const float *__restrict__ part_acc, const SeqState *__restrict__ st,
+    int nq, float *__restrict__ attn, int capacity) {
+  if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
+  const int length = static_cast<int>(st->position) + 1;
+  const int chunks = (length + kAttnChunk - 1) / kAttnChunk;
+  const int h = blockIdx.x;
+  const int d = threadIdx.x;
+  float m = -INFINITY;
+  for (int c = 0; c < chunks; ++c) m = fmaxf(m, part_m[c * nq + h]);
+  float num = 0.f, den = 0.f;
+  for (int c = 0; c < chunks; ++c) {
+    const float scale = expf(part_m[c * nq + h] - m);
+    den = fmaf(scale, part_l[c * nq + h], den);
+    num = fmaf(scale, part_acc[(static_cast<size_t>(c) * nq + h) * kHeadDim + d],
+               num);
+  }
+  attn[h * kHeadDim + d] = num / den;
+}
+
+// hidden[r] += Wo[r,:] . attn; unit u = rows (2u, 2u+1), contiguous.
+template <int H, int QD>
+__global__ __launch_bounds__(kBlock) void oproj_residual_kernel(
+    const float *__restrict__ attn, const float *__restrict__ wo,
+    const SeqState *__restrict__ st, float *__restrict__ hidden) {
+  if (st->stopped) return;
+  float4 xv[PairSlots<QD>::NJ];
+  load_pair_operand<QD, false>(attn, 1.f, nullptr, xv);
+  constexpr int units = H / 2;
+  for (int u = blockIdx.x * kWavesPerBlock + wave_id(); u < units;
+       u += gridDim.x * kWavesPerBlock) {
+    const float *a = wo + static_cast<size_t>(2 * u) * QD;
+    float sa, sb;
+    dot_pair<QD>(a, a + QD, xv, sa, sb);
+    if (lane_id() == 0) {
+      hidden[2 * u] += sa;
+      hidden[2 * u + 1] += sb;
+    }
+  }
+}
+
+// MLP RMSNorm + gate/up + SiLU: unit r = (gate row r, up row r).
+template <int H>
+__global__ __launch_bounds__(kBlock) void gateup_silu_kernel(
+    const float *__restrict__ hidden, const float *__restrict__ gain,
+    const float *__restrict__ wg, const float *__restrict__ wu,
+    const SeqState *__restrict__ st, float *__restrict__ act, int inter,
+    float eps) {
+  __shared__ float red[kWavesPerBlock];
+  if (st->stopped) return;
+  const float inv = block_inv_rms<H>(hidden, eps, red);
+  float4 xv[PairSlots<H>::NJ];
+  load_pair_operand<H, true>(hidden, inv, gain, xv);
+  for (int r = blockIdx.x * kWavesPerBlock + wave_id(); r < inter;
+       r += gridDim.x * kWavesPerBlock) {
+    float g, up;
+    dot_pair<H>(wg + static_cast<size_t>(r) * H,
+                wu + static_cast<size_t>(r) * H, xv, g, up);
+    if (lane_id() == 0) act[r] = g / (1.f + expf(-g)) * up;
+  }
+}
+
+// hidden[r] += Wd[r,:] . act; one row per wave.
+template <int H, int I>
+__global__ __launch_bounds__(kBlock) void down_residual_kernel(
+    const float *__restrict__ act, const float *__restrict__ wd,
+    const SeqState *__restrict__ st, float *__restrict__ hidden) {
+  if (st->stopped) return;
+  float4 xv[RowSlots<I>::NJ];
+  load_row_operand<I>(act, xv);
+  for (int r = blockIdx.x * kWavesPerBlock + wave_id(); r < H;
+       r += gridDim.x * kWavesPerBlock) {
+    const float s = dot_row<I>(wd + static_cast<size_t>(r) * I, xv);
+    if (lane_id() == 0) hidden[r] += s;
+  }
+}
+
+// Final RMSNorm + LM head over row pairs + per-workgroup top-1 partial.
+// Logits go to logits + (history ? generated * vocab : 0).
+template <int H>
+__global__ __launch_bounds__(kBlock) void lmhead_kernel(
+    const float *__restrict__ hidden, const float *__restrict__ gain,
+    const float *__restrict__ head, const SeqState *__restrict__ st,
+    float *__restrict__ logits, int history, int vocab, float eps,
+    float *__restrict__ part_val, uint32_t *__restrict__ part_idx) {
+  __shared__ float red[kWavesPerBlock];
+  __shared__ float bv[kWavesPerBlock];
+  __shared__ uint32_t bi[kWavesPerBlock];
+  if (st->stopped) return;
+  const float inv = block_inv_rms<H>(hidden, eps, red);
+  float4 xv[PairSlots<H>::NJ];
+  load_pair_operand<H, true>(hidden, inv, gain, xv);
+  float *out = logits + (history ? static_cast<size_t>(st->generated) * vocab : 0);
+  float best = -INFINITY;
+  uint32_t best_i = UINT32_MAX;
+  const int units = (vocab + 1) / 2;
+  for (int u = blockIdx.x * kWavesPerBlock + wave_id(); u < units;
+       u += gridDim.x * kWavesPerBlock) {
+    const int r0 = 2 * u;
+    const bool has1 = r0 + 1 < vocab;
+    const float *a = head + static_cast<size_t>(r0) * H;
+    float sa, sb;
+    dot_pair<H>(a, has1 ? a + H : a, xv, sa, sb);
+    if (lane_id() == 0) {
+      out[r0] = sa;
+      if (has1) out[r0 + 1] = sb;
+    }
+    if (better(sa, r0, best, best_i)) {
+      best = sa;
+      best_i = r0;
+    }
+    if (has1 && better(sb, r0 + 1, best, best_i)) {
+      best = sb;
+      best_i = r0 + 1;
+    }
+  }
+  if (lane_id() == 0) {
+    bv[wave_id()] = best;
+    bi[wave_id()] = best_i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWavesPerBlock; ++w) {
+      if (better(bv[w], bi[w], best, best_i)) {
+        best = bv[w];
+        best_i = bi[w];
+      }
+    }
+    part_val[blockIdx.x] = best;
+    part_idx[blockIdx.x] = best_i;
+  }
+}
+
+// Reduces the top-1 partials, records the sampled token and advances the
+// sequence (step mode), or applies the EOS / limit rule (generate mode).
+__global__ __launch_bounds__(kBlock) void argmax_finalize_kernel(
+    const float *__restrict__ part_val, const uint32_t *__restrict__ part_idx,
+    int parts, SeqState *__restrict__ st, uint32_t *__restrict__ out_tokens) {
+  __shared__ float bv[kWavesPerBlock];
+  __shared__ uint32_t bi[kWavesPerBlock];
+  if (st->stopped) return;
+  float best = -INFINITY;
+  uint32_t best_i = UINT32_MAX;
+  for (int p = threadIdx.x; p < parts; p += kBlock) {
+    if (better(part_val[p], part_idx[p], best, best_i)) {
+      best = part_val[p];
+      best_i = part_idx[p];
+    }
+  }
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, kWave);
+    const uint32_t oi = __shfl_xor(best_i, o, kWave);
+    if (better(ov, oi, best, best_i)) {
+      best = ov;
+      best_i = oi;
+    }
+  }
+  if (lane_id() == 0) {
+    bv[wave_id()] = best;
+    bi[wave_id()] = best_i;
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  for (int w = 1; w < kWavesPerBlock; ++w) {
+    if (better(bv[w], bi[w], best, best_i)) {
+      best = bv[w];
+      best_i = bi[w];
+    }
+  }
+  st->token = best_i;
+  st->top_logit = best;
+  st->position += 1;
+  if (best_i == UINT32_MAX) {
+    // Every logit was NaN: nothing can be fed back.
+    st->stop_reason = 0u;
+    st->stopped = 1u;
+    return;
+  }
+  if (st->mode == kModeGenerate) {
+    if (out_tokens) out_tokens[st->generated] = best_i;
+    st->generated += 1;
+    const bool eos = best_i == st->eos;
+    if (eos || st->generated >= st->max_tokens) {
+      st->stop_reason = eos ? 2u : 1u;
+      st->stopped = 1u;
+    }
+  }
+}
+
+}  // namespace
+
+// ---- host launchers -----------------------------------------------------------
+
+const char *kernel_name(int id) {
+  static const char *const names[kKernelCount] = {
+      "embed_kernel",         "qkv_rope_kernel",   "attn_partial_kernel",
+      "attn_combine_kernel",  "oproj_residual_kernel", "gateup_silu_kernel",
+      "down_residual_kernel", "lmhead_kernel",     "argmax_finalize_kernel"};
+  return id >= 0 && id < kKernelCount ? names[id] : "unknown";
+}
+
+bool shape_supported(int hidden, int intermediate, int heads, int kv_heads,
+                     int head_dim) {
+  return hidden == 896 && intermediate == 4864 && head_dim == kHeadDim &&
+         kv_heads > 0 && heads % kv_heads == 0 && heads / kv_heads <= kMaxGroup &&
+         heads * head_dim == 896;
+}
+
+namespace {
+struct Scope {
+  Marker *m;
+  int id;
+  Scope(Marker *marker, int kernel) : m(marker), id(kernel) {
+    if (m) m->before(id);
+  }
+  ~Scope() {
+    if (m) m->after(id);
+  }
+};
+}  // namespace
+
+hipError_t launch_embed(hipStream_t s, const float *emb, const SeqState *st,
+                        float *hidden, int hidden_size, int vocab, Marker *m) {
+  Scope scope(m, kKEmbed);
+  embed_kernel<<<(hidden_size + kBlock - 1) / kBlock, kBlock, 0, s>>>(
+      emb, st, hidden, hidden_size, vocab);
+  return hipGetLastError();
+}
+
+hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
+  constexpr int H = 896, I = 4864, QD = 896;
+  const int qkv_units = (p.nq + 2 * p.nkv) * kRotary;
+  {
+    Scope scope(m, kKQkvRope);
+    qkv_rope_kernel<H><<<(qkv_units + kWavesPerBlock - 1) / kWavesPerBlock,
+                         kBlock, 0, s>>>(
+        p.hidden, p.w.attn_norm, p.w.wqkv, p.w.bqkv, p.rope_cos, p.rope_sin,
+        p.st, p.q, p.k_cache, p.v_cache, p.nq, p.nkv, p.eps, p.capacity);
+  }
+  {
+    Scope scope(m, kKAttnPartial);
+    attn_partial_kernel<<<dim3(p.max_chunks, p.nkv), kBlock, 0, s>>>(
+        p.q, p.k_cache, p.v_cache, p.st, p.nq, p.nkv, p.part_m, p.part_l,
+        p.part_acc, p.capacity);
+  }
+  {
+    Scope scope(m, kKAttnCombine);
+    attn_combine_kernel<<<p.nq, kHeadDim, 0, s>>>(p.part_m, p.part_l,
+                                                  p.part_acc, p.st, p.nq,
+                                                  p.attn, p.capacity);
+  }
+  {
+    Scope scope(m, kKOproj);
+    oproj_residual_kernel<H, QD>
+        <<<(H / 2 + kWavesPerBlock - 1) / kWavesPerBlock, kBlock, 0, s>>>(
+            p.attn, p.w.wo, p.st, p.hidden);
+  }
+  {
+    Scope scope(m, kKGateUp);
+    gateup_silu_kernel<H><<<(I + kWavesPerBlock - 1) / kWavesPerBlock, kBlock,
+                            0, s>>>(p.hidden, p.w.mlp_norm, p.w.wg, p.w.wu,
+                                    p.st, p.act, I, p.eps);
+  }
+  {
+    Scope scope(m, kKDown);
+    down_residual_kernel<H, I><<<(H + kWavesPerBlock - 1) / kWavesPerBlock,
+                                 kBlock, 0, s>>>(p.act, p.w.wd, p.st,
+                                                 p.hidden);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_tail(hipStream_t s, const TailLaunch &p, Marker *m) {
+  constexpr int H = 896;
+  {
+    Scope scope(m, kKLmHead);
+    lmhead_kernel<H><<<p.parts, kBlock, 0, s>>>(
+        p.hidden, p.final_norm, p.head, p.st, p.logits, p.history, p.vocab,
+        p.eps, p.part_val, p.part_idx);
+  }
+  {
+    Scope scope(m, kKArgmax);
+    argmax_finalize_kernel<<<1, kBlock, 0, s>>>(p.part_val, p.part_idx,
+                                                p.parts, p.st, p.out_tokens);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace qd
