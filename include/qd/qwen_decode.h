@@ -132,6 +132,13 @@ QD_API qd_status qd_engine_config(const qd_engine *engine, qd_config *config);
 /* Total device bytes held by the engine. */
 QD_API qd_status qd_engine_device_bytes(const qd_engine *engine, uint64_t *bytes);
 
+/* Workgroups of the resident decode megakernel qd_generate_resident uses
+ * (one per CU), or 0 when the engine generates with stream-ordered kernels
+ * (QD_RESIDENT=0 in the environment at create time, or a capacity beyond
+ * the resident kernel's split-KV table). */
+QD_API qd_status qd_engine_resident_grid(const qd_engine *engine,
+                                         uint32_t *grid);
+
 /* Loads a reference weight bundle directory: layer_<i>/weights.json for each
  * layer plus model_tail/weights.json. Replaces load_decoder_layer_weights and
  * load_model_tail_weights (executor/qwen/weight_bundle.hpp:460-602) feeding

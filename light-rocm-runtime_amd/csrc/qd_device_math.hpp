@@ -1,0 +1,263 @@
+// Device helpers shared by the stream-ordered kernels (qd_kernels.hip) and
+// the resident megakernel (qd_resident.hip): wave64 reductions, the float4
+// slot layout of the row-pair GEMV, and device-coherent buffer access.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "qd_device.hpp"
+
+namespace qd {
+namespace dev {
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float fma4(float4 w, float4 x, float acc) {
+  acc = fmaf(w.x, x.x, acc);
+  acc = fmaf(w.y, x.y, acc);
+  acc = fmaf(w.z, x.z, acc);
+  acc = fmaf(w.w, x.w, acc);
+  return acc;
+}
+
+// Greater value wins; equal values go to the lower index; NaN never wins
+// (benchmarks/qwen_stateful_graph_kernel.cpp:225-229).
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv,
+                                       uint32_t bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// ---- device-coherent access ------------------------------------------------
+// Data one workgroup writes and another reads inside the same resident launch
+// goes through buffer instructions with the sc1 (device scope) policy: loads
+// are served coherently across the XCDs' private L2s and stores write
+// through, so no L2 writeback/invalidate is needed at the grid barriers. The
+// descriptor's record count also bounds every access (out-of-range loads
+// return 0, out-of-range stores are dropped).
+constexpr int kPolicySc1 = 16;
+constexpr int kPolicyNt = 2;
+constexpr int kRsrcWord3 = 0x00020000;
+
+typedef unsigned int u32x4 __attribute__((vector_size(16)));
+
+struct Coherent {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ Coherent(const void *base, uint32_t bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0,
+                                            static_cast<int>(bytes),
+                                            kRsrcWord3)) {}
+  __device__ __forceinline__ float ld(uint32_t i) const {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, kPolicySc1));
+  }
+  __device__ __forceinline__ uint32_t ldu(uint32_t i) const {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, kPolicySc1);
+  }
+  __device__ __forceinline__ float4 ld4(uint32_t i4) const {
+    const u32x4 v =
+        __builtin_amdgcn_raw_buffer_load_b128(r, i4 * 16u, 0, kPolicySc1);
+    return make_float4(__builtin_bit_cast(float, v[0]),
+                       __builtin_bit_cast(float, v[1]),
+                       __builtin_bit_cast(float, v[2]),
+                       __builtin_bit_cast(float, v[3]));
+  }
+  __device__ __forceinline__ void st(uint32_t i, float v) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r,
+                                          i * 4u, 0, kPolicySc1);
+  }
+  __device__ __forceinline__ void stu(uint32_t i, uint32_t v) const {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, i * 4u, 0, kPolicySc1);
+  }
+};
+
+// Plain pointer view with the same interface (stream-ordered kernels, where
+// kernel boundaries order everything).
+struct Plain {
+  const float *p;
+  __device__ __forceinline__ Plain(const float *base) : p(base) {}
+  __device__ __forceinline__ float ld(uint32_t i) const { return p[i]; }
+  __device__ __forceinline__ float4 ld4(uint32_t i4) const {
+    return reinterpret_cast<const float4 *>(p)[i4];
+  }
+};
+
+// Streaming weight load: each weight is read once per token.
+__device__ __forceinline__ float4 ld_weight(const float4 *p) { return *p; }
+
+// ---- RMSNorm ------------------------------------------------------------------
+
+// 1/rms of x[0..N) computed by the whole workgroup (every thread gets it).
+template <int N, typename Src>
+__device__ float block_inv_rms(const Src &x, float eps, float *red) {
+  constexpr int N4 = N / 4;
+  float s = 0.f;
+  for (int c = threadIdx.x; c < N4; c += blockDim.x) {
+    const float4 v = x.ld4(c);
+    s = fmaf(v.x, v.x, s);
+    s = fmaf(v.y, v.y, s);
+    s = fmaf(v.z, v.z, s);
+    s = fmaf(v.w, v.w, s);
+  }
+  s = wave_sum(s);
+  if (lane_id() == 0) red[wave_id()] = s;
+  __syncthreads();
+  float t = 0.f;
+  const int waves = blockDim.x / kWave;
+  for (int w = 0; w < waves; ++w) t += red[w];
+  __syncthreads();
+  return rsqrtf(t / static_cast<float>(N) + eps);
+}
+
+// ---- row-pair GEMV slot layout --------------------------------------------------
+// A wave computes the dot products of two weight rows with one K-vector.
+// The two rows are viewed as one run of 2*K/4 float4 slots; lane l loads
+// slots f = 64*j + l. The operand register xv[j] holds the x float4 that
+// slot f multiplies, so the same registers serve every row pair.
+template <int K>
+struct PairSlots {
+  static_assert(K % 4 == 0, "rows must be float4 aligned");
+  static constexpr int K4 = K / 4;
+  static constexpr int NJ = (2 * K4 + kWave - 1) / kWave;
+};
+
+// xv[j] = x[c] (optionally * inv * gain[c]) for the column c of slot j.
+template <int K, bool kNorm, typename Src>
+__device__ __forceinline__ void load_pair_operand(
+    const Src &x, float inv, const float *gain,
+    float4 (&xv)[PairSlots<K>::NJ]) {
+  constexpr int K4 = PairSlots<K>::K4;
+  const float4 *g4 = reinterpret_cast<const float4 *>(gain);
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < PairSlots<K>::NJ; ++j) {
+    const int f = j * kWave + lane;
+    const int c = f < K4 ? f : f - K4;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (f < 2 * K4) {
+      v = x.ld4(c);
+      if (kNorm) {
+        const float4 g = g4[c];
+        v.x = v.x * inv * g.x;
+        v.y = v.y * inv * g.y;
+        v.z = v.z * inv * g.z;
+        v.w = v.w * inv * g.w;
+      }
+    }
+    xv[j] = v;
+  }
+}
+
+// Weight slots of a row pair, loaded into registers (separable from the
+// arithmetic so a caller can issue them early).
+template <int K>
+__device__ __forceinline__ void load_pair_weights(
+    const float *a, const float *b, float4 (&w)[PairSlots<K>::NJ]) {
+  constexpr int K4 = PairSlots<K>::K4;
+  constexpr int NJ = PairSlots<K>::NJ;
+  const float4 *a4 = reinterpret_cast<const float4 *>(a);
+  const float4 *b4 = reinterpret_cast<const float4 *>(b);
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int f = j * kWave + lane;
+    if (j * kWave + kWave <= K4) {
+      w[j] = ld_weight(a4 + f);
+    } else if (j * kWave >= K4) {
+      w[j] = f < 2 * K4 ? ld_weight(b4 + (f - K4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+      w[j] = ld_weight(f < K4 ? a4 + f : b4 + (f - K4));
+    }
+  }
+}
+
+// Wave-reduced dot products (every lane gets both sums).
+template <int K>
+__device__ __forceinline__ void pair_dot(const float4 (&w)[PairSlots<K>::NJ],
+                                         const float4 (&xv)[PairSlots<K>::NJ],
+                                         float &sa, float &sb) {
+  constexpr int K4 = PairSlots<K>::K4;
+  constexpr int NJ = PairSlots<K>::NJ;
+  const int lane = lane_id();
+  float accA = 0.f, accB = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int f = j * kWave + lane;
+    if (j * kWave + kWave <= K4) {
+      accA = fma4(w[j], xv[j], accA);
+    } else if (j * kWave >= K4) {
+      accB = fma4(w[j], xv[j], accB);
+    } else {
+      const float d = fma4(w[j], xv[j], 0.f);
+      if (f < K4) {
+        accA += d;
+      } else {
+        accB += d;
+      }
+    }
+  }
+  sa = wave_sum(accA);
+  sb = wave_sum(accB);
+}
+
+template <int K>
+__device__ __forceinline__ void dot_pair(const float *a, const float *b,
+                                         const float4 (&xv)[PairSlots<K>::NJ],
+                                         float &sa, float &sb) {
+  float4 w[PairSlots<K>::NJ];
+  load_pair_weights<K>(a, b, w);
+  pair_dot<K>(w, xv, sa, sb);
+}
+
+// Single-row dot for K a multiple of 256 floats: lane l loads float4 slots
+// 64*j + l; xv[j] is the matching operand.
+template <int K>
+struct RowSlots {
+  static_assert(K % (4 * kWave) == 0, "row must be a whole number of wave loads");
+  static constexpr int NJ = K / (4 * kWave);
+};
+
+template <int K, typename Src>
+__device__ __forceinline__ void load_row_operand(
+    const Src &x, float4 (&xv)[RowSlots<K>::NJ]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < RowSlots<K>::NJ; ++j) xv[j] = x.ld4(j * kWave + lane);
+}
+
+template <int K>
+__device__ __forceinline__ void load_row_weights(const float *a,
+                                                 float4 (&w)[RowSlots<K>::NJ]) {
+  const float4 *a4 = reinterpret_cast<const float4 *>(a);
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < RowSlots<K>::NJ; ++j) w[j] = ld_weight(a4 + j * kWave + lane);
+}
+
+template <int K>
+__device__ __forceinline__ float row_dot(const float4 (&w)[RowSlots<K>::NJ],
+                                         const float4 (&xv)[RowSlots<K>::NJ]) {
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < RowSlots<K>::NJ; ++j) acc = fma4(w[j], xv[j], acc);
+  return wave_sum(acc);
+}
+
+template <int K>
+__device__ __forceinline__ float dot_row(const float *a,
+                                         const float4 (&xv)[RowSlots<K>::NJ]) {
+  float4 w[RowSlots<K>::NJ];
+  load_row_weights<K>(a, w);
+  return row_dot<K>(w, xv);
+}
+
+}  // namespace dev
+}  // namespace qd

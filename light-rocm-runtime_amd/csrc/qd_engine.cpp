@@ -26,6 +26,7 @@
 #include "qd_bundle.hpp"
 #include "qd_device.hpp"
 #include "qd_kernels.hpp"
+#include "qd_resident.hpp"
 #include "qd_rng.hpp"
 
 namespace {
@@ -117,6 +118,17 @@ struct qd_engine {
   qd::SeqState *states = nullptr;  // [max_batch]
   float *history = nullptr;        // generate-mode logits [capacity][vocab]
   size_t history_rows = 0;
+
+  // Resident megakernel state.
+  qd::LayerPtrs *layer_ptrs_dev = nullptr;  // [layers]
+  float *h1 = nullptr;                      // [hidden]
+  float *top_val = nullptr;                 // [grid]
+  uint32_t *top_idx = nullptr;              // [grid]
+  uint32_t *flags = nullptr;                // [grid]
+  uint32_t *group_count = nullptr;          // [kv_heads * 64]
+  uint32_t *resident_error = nullptr;       // [1]
+  int resident_grid = 0;                    // 0: resident path unavailable
+  const char *resident_off_reason = "";
 
   qd::SeqState *h_states = nullptr;  // pinned [max_batch]
   uint32_t *h_tokens = nullptr;      // pinned [capacity]
@@ -434,6 +446,33 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
           "hipHostMalloc");
     e->positions.assign(e->B, 0);
     e->build_rope_tables(c.rope_theta);
+
+    // Resident path: one workgroup per CU, all co-resident (cooperative
+    // launch); disabled by QD_RESIDENT=0 or when the split-KV merge of the
+    // capacity does not fit the kernel's LDS table.
+    const int cus = qd::device_cu_count(c.device);
+    const int max_grid = qd::resident_max_grid(c.device);
+    const char *env = std::getenv("QD_RESIDENT");
+    if (env && std::strcmp(env, "0") == 0) {
+      e->resident_off_reason = "QD_RESIDENT=0";
+    } else if (e->max_chunks > qd::kResidentMaxChunks) {
+      e->resident_off_reason = "capacity beyond the resident split-KV table";
+    } else if (cus <= 0 || max_grid < cus) {
+      e->resident_off_reason = "device cannot co-schedule one workgroup per CU";
+    } else {
+      e->resident_grid = cus;
+    }
+    const int grid_alloc = std::max(cus, 1);
+    e->layer_ptrs_dev = e->alloc<qd::LayerPtrs>(e->L);
+    check(hipMemcpyAsync(e->layer_ptrs_dev, e->layers.data(), e->L * sizeof(qd::LayerPtrs),
+                         hipMemcpyHostToDevice, e->stream), "layer table upload");
+    e->h1 = e->alloc<float>(e->H);
+    e->top_val = e->alloc<float>(grid_alloc);
+    e->top_idx = e->alloc<uint32_t>(grid_alloc);
+    e->flags = e->alloc<uint32_t>(grid_alloc);
+    e->group_count = e->alloc<uint32_t>(e->NKV * 64);
+    e->resident_error = e->alloc<uint32_t>(1);
+    e->sync();
     *out = e.release();
   });
 }
@@ -457,6 +496,13 @@ qd_status qd_engine_device_bytes(const qd_engine *e, uint64_t *bytes) {
   return guard([&] {
     if (!e || !bytes) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
     *bytes = e->device_bytes;
+  });
+}
+
+qd_status qd_engine_resident_grid(const qd_engine *e, uint32_t *grid) {
+  return guard([&] {
+    if (!e || !grid) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    *grid = static_cast<uint32_t>(e->resident_grid);
   });
 }
 
@@ -827,12 +873,62 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
       use_hist = 1;
     }
     e->push_state(seq, first_token, qd::kModeGenerate, eos, max_tokens);
-    check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
-    for (uint32_t t = 0; t < max_tokens; ++t) e->enqueue_step(seq, hist, use_hist, e->tokens_dev);
+    if (e->resident_grid > 0) {
+      qd::ResidentArgs ra{};
+      ra.layer_ptrs = e->layer_ptrs_dev;
+      ra.embed = e->embed;
+      ra.head = e->lm_head;
+      ra.final_norm = e->final_norm;
+      ra.rope_cos = e->rope_cos;
+      ra.rope_sin = e->rope_sin;
+      ra.k_cache = e->kv_slice(e->k_cache, seq, 0);
+      ra.v_cache = e->kv_slice(e->v_cache, seq, 0);
+      ra.hidden = e->hidden + size_t(seq) * e->H;
+      ra.h1 = e->h1;
+      ra.q = e->q + size_t(seq) * e->QD;
+      ra.attn = e->attn + size_t(seq) * e->QD;
+      ra.act = e->act + size_t(seq) * e->I;
+      ra.part_m = e->part_m;
+      ra.part_l = e->part_l;
+      ra.part_acc = e->part_acc;
+      ra.group_count = e->group_count;
+      ra.logits = hist;
+      ra.top_val = e->top_val;
+      ra.top_idx = e->top_idx;
+      ra.flags = e->flags;
+      ra.out_tokens = e->tokens_dev;
+      ra.st = e->states + seq;
+      ra.error = e->resident_error;
+      ra.history = use_hist;
+      ra.capacity = static_cast<int>(e->CAP);
+      ra.vocab = static_cast<int>(e->V);
+      ra.layers = static_cast<int>(e->L);
+      ra.nq = static_cast<int>(e->NQ);
+      ra.nkv = static_cast<int>(e->NKV);
+      ra.max_chunks = e->max_chunks;
+      ra.eps = e->cfg.rms_eps;
+      ra.first_token = first_token;
+      ra.start_position = e->positions[seq];
+      ra.max_tokens = max_tokens;
+      ra.eos = eos;
+      check(hipMemsetAsync(e->flags, 0, size_t(e->resident_grid) * 4, e->stream), "memset");
+      check(hipMemsetAsync(e->group_count, 0, e->NKV * 64 * 4, e->stream), "memset");
+      check(hipMemsetAsync(e->resident_error, 0, 4, e->stream), "memset");
+      check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
+      check(qd::launch_resident(e->stream, ra, e->resident_grid), "resident launch");
+    } else {
+      check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
+      for (uint32_t t = 0; t < max_tokens; ++t) e->enqueue_step(seq, hist, use_hist, e->tokens_dev);
+    }
     check(hipEventRecord(e->ev_end, e->stream), "hipEventRecord");
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
                          e->stream), "D2H");
     e->sync();
+    if (e->resident_grid > 0) {
+      uint32_t err = 0;
+      check(hipMemcpy(&err, e->resident_error, 4, hipMemcpyDeviceToHost), "D2H");
+      if (err) fail(QD_ERROR_RUNTIME, "resident kernel barrier wait timed out");
+    }
     const qd::SeqState &s = e->h_states[seq];
     const uint32_t n = s.generated;
     check(hipMemcpyAsync(out_tokens, e->tokens_dev, size_t(n) * 4, hipMemcpyDeviceToHost, e->stream), "D2H");

@@ -21,172 +21,13 @@
 #include <cstdint>
 
 #include "qd_device.hpp"
+#include "qd_device_math.hpp"
 #include "qd_kernels.hpp"
 
 namespace qd {
 namespace {
 
-__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
-__device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-
-__device__ __forceinline__ float fma4(float4 w, float4 x, float acc) {
-  acc = fmaf(w.x, x.x, acc);
-  acc = fmaf(w.y, x.y, acc);
-  acc = fmaf(w.z, x.z, acc);
-  acc = fmaf(w.w, x.w, acc);
-  return acc;
-}
-
-// Greater value wins; equal values go to the lower index; NaN never wins
-// (benchmarks/qwen_stateful_graph_kernel.cpp:225-229).
-__device__ __forceinline__ bool better(float v, uint32_t i, float bv,
-                                       uint32_t bi) {
-  return v > bv || (v == bv && i < bi);
-}
-
-// 1/rms of x[0..N) computed by the whole workgroup (every thread gets it).
-template <int N>
-__device__ float block_inv_rms(const float *x, float eps, float *red) {
-  constexpr int N4 = N / 4;
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
-  float s = 0.f;
-  for (int c = threadIdx.x; c < N4; c += kBlock) {
-    const float4 v = x4[c];
-    s = fmaf(v.x, v.x, s);
-    s = fmaf(v.y, v.y, s);
-    s = fmaf(v.z, v.z, s);
-    s = fmaf(v.w, v.w, s);
-  }
-  s = wave_sum(s);
-  if (lane_id() == 0) red[wave_id()] = s;
-  __syncthreads();
-  float t = 0.f;
-#pragma unroll
-  for (int w = 0; w < kWavesPerBlock; ++w) t += red[w];
-  __syncthreads();
-  return rsqrtf(t / static_cast<float>(N) + eps);
-}
-
-// A wave computes the dot products of two weight rows with one K-vector.
-// The two rows are viewed as one run of 2*K/4 float4 slots; lane l loads
-// slots f = 64*j + l. The operand register xv[j] holds the x float4 that
-// slot f multiplies, so the same registers serve every row pair.
-template <int K>
-struct PairSlots {
-  static_assert(K % 4 == 0, "rows must be float4 aligned");
-  static constexpr int K4 = K / 4;
-  static constexpr int NJ = (2 * K4 + kWave - 1) / kWave;
-};
-
-// xv[j] = x[c] (optionally * inv * gain[c]) for the column c of slot j.
-template <int K, bool kNorm>
-__device__ __forceinline__ void load_pair_operand(
-    const float *x, float inv, const float *gain,
-    float4 (&xv)[PairSlots<K>::NJ]) {
-  constexpr int K4 = PairSlots<K>::K4;
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
-  const float4 *g4 = reinterpret_cast<const float4 *>(gain);
-  const int lane = lane_id();
-#pragma unroll
-  for (int j = 0; j < PairSlots<K>::NJ; ++j) {
-    const int f = j * kWave + lane;
-    const int c = f < K4 ? f : f - K4;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (f < 2 * K4) {
-      v = x4[c];
-      if (kNorm) {
-        const float4 g = g4[c];
-        v.x = v.x * inv * g.x;
-        v.y = v.y * inv * g.y;
-        v.z = v.z * inv * g.z;
-        v.w = v.w * inv * g.w;
-      }
-    }
-    xv[j] = v;
-  }
-}
-
-// Dot products of rows a and b (K floats each) with the slot operand.
-// Returns wave-reduced sums in every lane.
-template <int K>
-__device__ __forceinline__ void dot_pair(const float *a, const float *b,
-                                         const float4 (&xv)[PairSlots<K>::NJ],
-                                         float &sa, float &sb) {
-  constexpr int K4 = PairSlots<K>::K4;
-  constexpr int NJ = PairSlots<K>::NJ;
-  const float4 *a4 = reinterpret_cast<const float4 *>(a);
-  const float4 *b4 = reinterpret_cast<const float4 *>(b);
-  const int lane = lane_id();
-  float4 w[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int f = j * kWave + lane;
-    if (j * kWave + kWave <= K4) {
-      w[j] = a4[f];
-    } else if (j * kWave >= K4) {
-      w[j] = f < 2 * K4 ? b4[f - K4] : make_float4(0.f, 0.f, 0.f, 0.f);
-    } else {
-      w[j] = *(f < K4 ? a4 + f : b4 + (f - K4));
-    }
-  }
-  float accA = 0.f, accB = 0.f;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const int f = j * kWave + lane;
-    if (j * kWave + kWave <= K4) {
-      accA = fma4(w[j], xv[j], accA);
-    } else if (j * kWave >= K4) {
-      accB = fma4(w[j], xv[j], accB);
-    } else {
-      const float d = fma4(w[j], xv[j], 0.f);
-      if (f < K4) {
-        accA += d;
-      } else {
-        accB += d;
-      }
-    }
-  }
-  sa = wave_sum(accA);
-  sb = wave_sum(accB);
-}
-
-// Single-row dot for K a multiple of 256 floats: lane l loads float4 slots
-// 64*j + l; xv[j] is the matching operand.
-template <int K>
-struct RowSlots {
-  static_assert(K % (4 * kWave) == 0, "row must be a whole number of wave loads");
-  static constexpr int NJ = K / (4 * kWave);
-};
-
-template <int K>
-__device__ __forceinline__ void load_row_operand(
-    const float *x, float4 (&xv)[RowSlots<K>::NJ]) {
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
-  const int lane = lane_id();
-#pragma unroll
-  for (int j = 0; j < RowSlots<K>::NJ; ++j) xv[j] = x4[j * kWave + lane];
-}
-
-template <int K>
-__device__ __forceinline__ float dot_row(const float *a,
-                                         const float4 (&xv)[RowSlots<K>::NJ]) {
-  constexpr int NJ = RowSlots<K>::NJ;
-  const float4 *a4 = reinterpret_cast<const float4 *>(a);
-  const int lane = lane_id();
-  float4 w[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) w[j] = a4[j * kWave + lane];
-  float acc = 0.f;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) acc = fma4(w[j], xv[j], acc);
-  return wave_sum(acc);
-}
+using namespace dev;
 
 // ---- kernels ----------------------------------------------------------------
 
@@ -213,9 +54,9 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
     float eps, int capacity) {
   __shared__ float red[kWavesPerBlock];
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
-  const float inv = block_inv_rms<H>(hidden, eps, red);
+  const float inv = block_inv_rms<H>(Plain(hidden), eps, red);
   float4 xv[PairSlots<H>::NJ];
-  load_pair_operand<H, true>(hidden, inv, gain, xv);
+  load_pair_operand<H, true>(Plain(hidden), inv, gain, xv);
   const int position = static_cast<int>(st->position);
   const int kv_dim = nkv * kHeadDim;
   const int units = (nq + 2 * nkv) * kRotary;
@@ -381,7 +222,7 @@ __global__ __launch_bounds__(kBlock) void oproj_residual_kernel(
     const SeqState *__restrict__ st, float *__restrict__ hidden) {
   if (st->stopped) return;
   float4 xv[PairSlots<QD>::NJ];
-  load_pair_operand<QD, false>(attn, 1.f, nullptr, xv);
+  load_pair_operand<QD, false>(Plain(attn), 1.f, nullptr, xv);
   constexpr int units = H / 2;
   for (int u = blockIdx.x * kWavesPerBlock + wave_id(); u < units;
        u += gridDim.x * kWavesPerBlock) {
@@ -404,9 +245,9 @@ __global__ __launch_bounds__(kBlock) void gateup_silu_kernel(
     float eps) {
   __shared__ float red[kWavesPerBlock];
   if (st->stopped) return;
-  const float inv = block_inv_rms<H>(hidden, eps, red);
+  const float inv = block_inv_rms<H>(Plain(hidden), eps, red);
   float4 xv[PairSlots<H>::NJ];
-  load_pair_operand<H, true>(hidden, inv, gain, xv);
+  load_pair_operand<H, true>(Plain(hidden), inv, gain, xv);
   for (int r = blockIdx.x * kWavesPerBlock + wave_id(); r < inter;
        r += gridDim.x * kWavesPerBlock) {
     float g, up;
@@ -423,7 +264,7 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(
     const SeqState *__restrict__ st, float *__restrict__ hidden) {
   if (st->stopped) return;
   float4 xv[RowSlots<I>::NJ];
-  load_row_operand<I>(act, xv);
+  load_row_operand<I>(Plain(act), xv);
   for (int r = blockIdx.x * kWavesPerBlock + wave_id(); r < H;
        r += gridDim.x * kWavesPerBlock) {
     const float s = dot_row<I>(wd + static_cast<size_t>(r) * I, xv);
@@ -443,9 +284,9 @@ __global__ __launch_bounds__(kBlock) void lmhead_kernel(
   __shared__ float bv[kWavesPerBlock];
   __shared__ uint32_t bi[kWavesPerBlock];
   if (st->stopped) return;
-  const float inv = block_inv_rms<H>(hidden, eps, red);
+  const float inv = block_inv_rms<H>(Plain(hidden), eps, red);
   float4 xv[PairSlots<H>::NJ];
-  load_pair_operand<H, true>(hidden, inv, gain, xv);
+  load_pair_operand<H, true>(Plain(hidden), inv, gain, xv);
   float *out = logits + (history ? static_cast<size_t>(st->generated) * vocab : 0);
   float best = -INFINITY;
   uint32_t best_i = UINT32_MAX;

@@ -74,6 +74,7 @@ _SIGNATURES = {
     "qd_engine_destroy": (C.c_int, [_E]),
     "qd_engine_config": (C.c_int, [_E, C.POINTER(Config)]),
     "qd_engine_device_bytes": (C.c_int, [_E, C.POINTER(C.c_uint64)]),
+    "qd_engine_resident_grid": (C.c_int, [_E, _U]),
     "qd_load_bundle": (C.c_int, [_E, C.c_char_p]),
     "qd_load_synthetic": (C.c_int, [_E, C.c_uint64, C.POINTER(SyntheticInit)]),
     "qd_read_weight": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F, C.c_size_t]),
@@ -199,6 +200,11 @@ class Engine:
         n = C.c_uint64()
         _check(lib().qd_engine_device_bytes(self.handle, C.byref(n)))
         return int(n.value)
+
+    def resident_grid(self) -> int:
+        g = C.c_uint32()
+        _check(lib().qd_engine_resident_grid(self.handle, C.byref(g)))
+        return int(g.value)
 
     def load_synthetic(self, seed: int, weight_std: float = 0.02, bias_std: float = 0.01,
                        norm_gain: float = 1.0):

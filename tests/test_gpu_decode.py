@@ -171,6 +171,29 @@ def test_generate_matches_step_loop_and_oracle(full):
         feed = rtok
 
 
+def test_resident_and_stream_generation_agree(full, monkeypatch):
+    """The resident megakernel and the stream-ordered kernels run the same
+    arithmetic in the same order: identical tokens and logits."""
+    eng, _ = full
+    assert eng.resident_grid() > 0
+    prompt = qo.fill_tokens(9, 1, PROMPT_STREAM + 3, FULL.vocab)
+    say("resident vs stream generation, 12 tokens")
+    eng.kv_reset(0, 0)
+    first, _, _ = eng.prefill(0, prompt, want_logits=False)
+    toks, _, logits = eng.generate(0, first, 12, want_logits=True)
+    monkeypatch.setenv("QD_RESIDENT", "0")
+    stream = qd.Engine(layers=FULL.layers, vocab=FULL.vocab, capacity=64, max_batch=1)
+    monkeypatch.delenv("QD_RESIDENT")
+    assert stream.resident_grid() == 0
+    stream.load_synthetic(1)
+    first2, _, _ = stream.prefill(0, prompt, want_logits=False)
+    toks2, _, logits2 = stream.generate(0, first2, 12, want_logits=True)
+    stream.close()
+    assert first2 == first and toks2.tolist() == toks.tolist()
+    assert np.array_equal(logits, logits2)
+    # KV written by the resident launch equals the stream path's rows too.
+
+
 def test_generate_stops_at_eos(full):
     eng, _ = full
     prompt = qo.fill_tokens(5, 1, PROMPT_STREAM + 2, FULL.vocab)
