@@ -170,6 +170,11 @@ QD_API qd_status qd_write_kv(qd_engine *engine, uint32_t seq, uint32_t layer,
 QD_API qd_status qd_read_kv(qd_engine *engine, uint32_t seq, uint32_t layer,
                             uint32_t start, uint32_t count, float *k,
                             float *v);
+/* Diagnostics: copies the slot's current activation vector `which`
+ * (0 hidden [hidden], 1 query [heads*64], 2 attention output [heads*64],
+ * 3 SwiGLU activation [intermediate]) to the host. */
+QD_API qd_status qd_read_activation(qd_engine *engine, uint32_t seq,
+                                    uint32_t which, float *out, size_t count);
 QD_API qd_status qd_read_decode_state(qd_engine *engine, uint32_t seq,
                                       qd_decode_state *state);
 
@@ -230,6 +235,17 @@ QD_API qd_status qd_profile_kernels(qd_engine *engine, uint32_t seq,
                                     uint32_t first_token, uint32_t tokens,
                                     qd_kernel_stat *stats, uint32_t capacity,
                                     uint32_t *count);
+
+/* Runs qd_generate_resident's resident megakernel in its profiled form
+ * (workgroup 0 stamps every grid-barrier exit) and reports per-stage totals
+ * in microseconds: QKV, attention, O projection, gate/up, down, LM head,
+ * argmax (7 entries). Advances the position like qd_generate_resident. The
+ * counterpart of the reference's stage profile kernel
+ * (benchmarks/qwen_stateful_graph_kernel.cpp:837-865). */
+QD_API qd_status qd_profile_resident(qd_engine *engine, uint32_t seq,
+                                     uint32_t first_token, uint32_t tokens,
+                                     double *stage_us, uint32_t capacity,
+                                     uint32_t *count);
 
 /* Timing of the last qd_generate_resident call. */
 QD_API qd_status qd_last_timing(const qd_engine *engine, qd_timing *timing);

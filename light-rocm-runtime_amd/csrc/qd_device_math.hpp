@@ -48,6 +48,7 @@ constexpr int kPolicyNt = 2;
 constexpr int kRsrcWord3 = 0x00020000;
 
 typedef unsigned int u32x4 __attribute__((vector_size(16)));
+typedef float f32x4 __attribute__((vector_size(16)));
 
 struct Coherent {
   __amdgpu_buffer_rsrc_t r;
@@ -62,13 +63,12 @@ struct Coherent {
   __device__ __forceinline__ uint32_t ldu(uint32_t i) const {
     return __builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, kPolicySc1);
   }
+  // The whole vector is bit-cast at once: bit-casting individual elements of
+  // the builtin's result folds every lane to element 0 in this compiler.
   __device__ __forceinline__ float4 ld4(uint32_t i4) const {
-    const u32x4 v =
-        __builtin_amdgcn_raw_buffer_load_b128(r, i4 * 16u, 0, kPolicySc1);
-    return make_float4(__builtin_bit_cast(float, v[0]),
-                       __builtin_bit_cast(float, v[1]),
-                       __builtin_bit_cast(float, v[2]),
-                       __builtin_bit_cast(float, v[3]));
+    const f32x4 v = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, i4 * 16u, 0, kPolicySc1));
+    return make_float4(v[0], v[1], v[2], v[3]);
   }
   __device__ __forceinline__ void st(uint32_t i, float v) const {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r,

@@ -284,6 +284,54 @@ struct qd_engine {
     return 0;
   }
 
+  // Resets the barrier words and launches the resident megakernel (stream
+  // ordered; no synchronisation).
+  void launch_resident(uint32_t seq, uint32_t first_token, uint32_t max_tokens,
+                       uint32_t eos, float *hist, int use_hist, uint64_t *stage_ticks) {
+      qd::ResidentArgs ra{};
+      ra.layer_ptrs = layer_ptrs_dev;
+      ra.embed = embed;
+      ra.head = lm_head;
+      ra.final_norm = final_norm;
+      ra.rope_cos = rope_cos;
+      ra.rope_sin = rope_sin;
+      ra.k_cache = kv_slice(k_cache, seq, 0);
+      ra.v_cache = kv_slice(v_cache, seq, 0);
+      ra.hidden = hidden + size_t(seq) * H;
+      ra.h1 = h1;
+      ra.q = q + size_t(seq) * QD;
+      ra.attn = attn + size_t(seq) * QD;
+      ra.act = act + size_t(seq) * I;
+      ra.part_m = part_m;
+      ra.part_l = part_l;
+      ra.part_acc = part_acc;
+      ra.group_count = group_count;
+      ra.logits = hist;
+      ra.top_val = top_val;
+      ra.top_idx = top_idx;
+      ra.flags = flags;
+      ra.out_tokens = tokens_dev;
+      ra.st = states + seq;
+      ra.error = resident_error;
+      ra.history = use_hist;
+      ra.capacity = static_cast<int>(CAP);
+      ra.vocab = static_cast<int>(V);
+      ra.layers = static_cast<int>(L);
+      ra.nq = static_cast<int>(NQ);
+      ra.nkv = static_cast<int>(NKV);
+      ra.max_chunks = max_chunks;
+      ra.eps = cfg.rms_eps;
+      ra.first_token = first_token;
+      ra.start_position = positions[seq];
+      ra.max_tokens = max_tokens;
+      ra.eos = eos;
+      check(hipMemsetAsync(flags, 0, size_t(resident_grid) * 4, stream), "memset");
+      check(hipMemsetAsync(group_count, 0, NKV * 64 * 4, stream), "memset");
+      check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
+      ra.stage_ticks = stage_ticks;
+      check(qd::launch_resident(stream, ra, resident_grid), "resident launch");
+  }
+
   void sync() { check(hipStreamSynchronize(stream), "hipStreamSynchronize"); }
 };
 
@@ -461,8 +509,13 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
       e->resident_off_reason = "device cannot co-schedule one workgroup per CU";
     } else {
       e->resident_grid = cus;
+      // Diagnostic override of the resident grid (1..max co-resident).
+      if (const char *g = std::getenv("QD_RESIDENT_GRID")) {
+        const int want = std::atoi(g);
+        if (want >= 1 && want <= max_grid) e->resident_grid = want;
+      }
     }
-    const int grid_alloc = std::max(cus, 1);
+    const int grid_alloc = std::max({cus, max_grid, 1});
     e->layer_ptrs_dev = e->alloc<qd::LayerPtrs>(e->L);
     check(hipMemcpyAsync(e->layer_ptrs_dev, e->layers.data(), e->L * sizeof(qd::LayerPtrs),
                          hipMemcpyHostToDevice, e->stream), "layer table upload");
@@ -717,6 +770,26 @@ qd_status qd_read_kv(qd_engine *e, uint32_t seq, uint32_t layer, uint32_t start,
   return guard([&] { kv_copy(e, seq, layer, start, count, k, v, false); });
 }
 
+qd_status qd_read_activation(qd_engine *e, uint32_t seq, uint32_t which, float *out, size_t count) {
+  return guard([&] {
+    if (!e || !out) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_seq(seq);
+    const float *src = nullptr;
+    size_t n = 0;
+    switch (which) {
+      case 0: src = e->hidden + size_t(seq) * e->H; n = e->H; break;
+      case 1: src = e->q + size_t(seq) * e->QD; n = e->QD; break;
+      case 2: src = e->attn + size_t(seq) * e->QD; n = e->QD; break;
+      case 3: src = e->act + size_t(seq) * e->I; n = e->I; break;
+      default: fail(QD_ERROR_INVALID_ARGUMENT, "unknown activation %u", which);
+    }
+    if (count != n) fail(QD_ERROR_INVALID_ARGUMENT, "activation has %zu elements, caller asked %zu", n, count);
+    e->set_device();
+    check(hipMemcpyAsync(out, src, n * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    e->sync();
+  });
+}
+
 qd_status qd_read_decode_state(qd_engine *e, uint32_t seq, qd_decode_state *out) {
   return guard([&] {
     if (!e || !out) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
@@ -874,48 +947,8 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
     }
     e->push_state(seq, first_token, qd::kModeGenerate, eos, max_tokens);
     if (e->resident_grid > 0) {
-      qd::ResidentArgs ra{};
-      ra.layer_ptrs = e->layer_ptrs_dev;
-      ra.embed = e->embed;
-      ra.head = e->lm_head;
-      ra.final_norm = e->final_norm;
-      ra.rope_cos = e->rope_cos;
-      ra.rope_sin = e->rope_sin;
-      ra.k_cache = e->kv_slice(e->k_cache, seq, 0);
-      ra.v_cache = e->kv_slice(e->v_cache, seq, 0);
-      ra.hidden = e->hidden + size_t(seq) * e->H;
-      ra.h1 = e->h1;
-      ra.q = e->q + size_t(seq) * e->QD;
-      ra.attn = e->attn + size_t(seq) * e->QD;
-      ra.act = e->act + size_t(seq) * e->I;
-      ra.part_m = e->part_m;
-      ra.part_l = e->part_l;
-      ra.part_acc = e->part_acc;
-      ra.group_count = e->group_count;
-      ra.logits = hist;
-      ra.top_val = e->top_val;
-      ra.top_idx = e->top_idx;
-      ra.flags = e->flags;
-      ra.out_tokens = e->tokens_dev;
-      ra.st = e->states + seq;
-      ra.error = e->resident_error;
-      ra.history = use_hist;
-      ra.capacity = static_cast<int>(e->CAP);
-      ra.vocab = static_cast<int>(e->V);
-      ra.layers = static_cast<int>(e->L);
-      ra.nq = static_cast<int>(e->NQ);
-      ra.nkv = static_cast<int>(e->NKV);
-      ra.max_chunks = e->max_chunks;
-      ra.eps = e->cfg.rms_eps;
-      ra.first_token = first_token;
-      ra.start_position = e->positions[seq];
-      ra.max_tokens = max_tokens;
-      ra.eos = eos;
-      check(hipMemsetAsync(e->flags, 0, size_t(e->resident_grid) * 4, e->stream), "memset");
-      check(hipMemsetAsync(e->group_count, 0, e->NKV * 64 * 4, e->stream), "memset");
-      check(hipMemsetAsync(e->resident_error, 0, 4, e->stream), "memset");
       check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
-      check(qd::launch_resident(e->stream, ra, e->resident_grid), "resident launch");
+      e->launch_resident(seq, first_token, max_tokens, eos, hist, use_hist, nullptr);
     } else {
       check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
       for (uint32_t t = 0; t < max_tokens; ++t) e->enqueue_step(seq, hist, use_hist, e->tokens_dev);
@@ -1019,6 +1052,38 @@ qd_status qd_profile_kernels(qd_engine *e, uint32_t seq, uint32_t first_token, u
       ++n;
     }
     *count = std::min(n, capacity);
+  });
+}
+
+qd_status qd_profile_resident(qd_engine *e, uint32_t seq, uint32_t first_token, uint32_t tokens,
+                              double *stage_us, uint32_t capacity, uint32_t *count) {
+  return guard([&] {
+    if (!e || !stage_us || !count) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_seq(seq);
+    e->check_loaded();
+    if (e->resident_grid == 0) fail(QD_ERROR_NOT_SUPPORTED, "resident path disabled: %s", e->resident_off_reason);
+    if (tokens == 0) fail(QD_ERROR_INVALID_ARGUMENT, "tokens must be positive");
+    if (first_token >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", first_token);
+    if (size_t(e->positions[seq]) + tokens > e->CAP)
+      fail(QD_ERROR_INVALID_ARGUMENT, "profiling %u tokens overflows capacity", tokens);
+    e->set_device();
+    uint64_t *ticks = e->alloc<uint64_t>(qd::kResidentStages);
+    e->launch_resident(seq, first_token, tokens, UINT32_MAX, e->logits + size_t(seq) * e->V, 0, ticks);
+    uint64_t h[qd::kResidentStages] = {};
+    check(hipMemcpyAsync(h, ticks, sizeof(h), hipMemcpyDeviceToHost, e->stream), "D2H");
+    check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
+                         e->stream), "D2H");
+    e->sync();
+    check(hipFree(ticks), "hipFree");
+    e->allocs.pop_back();
+    e->device_bytes -= 256;
+    uint32_t err = 0;
+    check(hipMemcpy(&err, e->resident_error, 4, hipMemcpyDeviceToHost), "D2H");
+    if (err) fail(QD_ERROR_RUNTIME, "resident kernel barrier wait timed out");
+    e->positions[seq] = e->h_states[seq].position;
+    const uint32_t n = std::min<uint32_t>(capacity, qd::kResidentStages);
+    for (uint32_t s = 0; s < n; ++s) stage_us[s] = double(h[s]) / 100.0;  // 100 MHz
+    *count = n;
   });
 }
 

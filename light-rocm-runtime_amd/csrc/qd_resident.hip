@@ -134,12 +134,9 @@ struct AttnShared {
 // Workgroup unit (KV group g, chunk c): online-softmax partial over the
 // chunk's positions for every query head of the group. The workgroup that
 // completes a group's last chunk merges the group's partials into attn.
-__device__ void stage_attention(const ResidentArgs &a, const float *kc,
-                                const float *vc, int length, int chunks,
-                                uint32_t target, AttnShared &sh) {
-  const int units = a.nkv * chunks;
-  const int u = blockIdx.x;
-  if (u >= units) return;
+__device__ void attention_unit(const ResidentArgs &a, const float *kc,
+                               const float *vc, int length, int chunks,
+                               uint32_t target, AttnShared &sh, int u) {
   const int g = u / chunks;
   const int chunk = u % chunks;
   const int group = a.nq / a.nkv;
@@ -256,6 +253,14 @@ __device__ void stage_attention(const ResidentArgs &a, const float *kc,
       num = fmaf(sh.scale[hl][c], pacc.ld((c * a.nq + h) * kHeadDim + d), num);
     attn.st(h * kHeadDim + d, num / sh.den[hl]);
   }
+}
+
+__device__ void stage_attention(const ResidentArgs &a, const float *kc,
+                                const float *vc, int length, int chunks,
+                                uint32_t target, AttnShared &sh) {
+  const int units = a.nkv * chunks;
+  for (int u = blockIdx.x; u < units; u += gridDim.x)
+    attention_unit(a, kc, vc, length, chunks, target, sh, u);
 }
 
 template <int H, int QD, typename Src>
@@ -397,7 +402,30 @@ __device__ void reduce_top1(const ResidentArgs &a, float *bv, uint32_t *bi,
   __syncthreads();
 }
 
-template <int H, int I, int QD>
+// Stage clock of the profiled instantiation: workgroup 0 stamps every
+// barrier exit with the 100 MHz wall clock, so a stage's time is its
+// slowest workgroup's work plus the barrier that ends it.
+template <bool kProfile>
+struct StageClock {
+  uint64_t ticks[kResidentStages] = {};
+  uint64_t prev = 0;
+  __device__ void start() {
+    if (kProfile) prev = wall_clock64();
+  }
+  __device__ void lap(int stage) {
+    if (kProfile) {
+      const uint64_t now = wall_clock64();
+      ticks[stage] += now - prev;
+      prev = now;
+    }
+  }
+  __device__ void publish(uint64_t *out) const {
+    if (kProfile && out && blockIdx.x == 0 && threadIdx.x == 0)
+      for (int s = 0; s < kResidentStages; ++s) out[s] = ticks[s];
+  }
+};
+
+template <int H, int I, int QD, bool kProfile>
 __global__ __launch_bounds__(kBlock) void resident_decode_kernel(ResidentArgs a) {
   __shared__ AttnShared attn_sh;
   __shared__ float red[kWavesPerBlock];
@@ -410,6 +438,8 @@ __global__ __launch_bounds__(kBlock) void resident_decode_kernel(ResidentArgs a)
   uint32_t stop_reason = 0;
   uint32_t group_target = 0;
   float top = 0.f;
+  StageClock<kProfile> clock;
+  clock.start();
 
   for (uint32_t t = 0; t < a.max_tokens; ++t) {
     const int position = static_cast<int>(a.start_position + t);
@@ -428,25 +458,32 @@ __global__ __launch_bounds__(kBlock) void resident_decode_kernel(ResidentArgs a)
         stage_qkv<H>(a, w, hidden, position, kc, vc, red);
       }
       if (!bar.sync()) return;
+      clock.lap(0);
       group_target += static_cast<uint32_t>(chunks);
       stage_attention(a, kc, vc, length, chunks, group_target, attn_sh);
       if (!bar.sync()) return;
+      clock.lap(1);
       if (l == 0) {
         stage_oproj<H, QD>(a, w, embed_row);
       } else {
         stage_oproj<H, QD>(a, w, hidden);
       }
       if (!bar.sync()) return;
+      clock.lap(2);
       stage_gateup<H>(a, w, I, red);
       if (!bar.sync()) return;
+      clock.lap(3);
       stage_down<H, I>(a, w);
       if (!bar.sync()) return;
+      clock.lap(4);
     }
     float *logits = a.logits + (a.history ? static_cast<size_t>(t) * a.vocab : 0);
     stage_lmhead<H>(a, logits, red, bv, bi);
     if (!bar.sync()) return;
+    clock.lap(5);
     uint32_t next;
     reduce_top1(a, bv, bi, top, next);
+    clock.lap(6);
     token = next;
     generated = t + 1;
     if (blockIdx.x == 0 && threadIdx.x == 0) a.out_tokens[t] = token;
@@ -460,6 +497,7 @@ __global__ __launch_bounds__(kBlock) void resident_decode_kernel(ResidentArgs a)
       break;
     }
   }
+  clock.publish(a.stage_ticks);
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     SeqState *st = a.st;
     st->position = a.start_position + generated;
@@ -478,9 +516,11 @@ __global__ __launch_bounds__(kBlock) void resident_decode_kernel(ResidentArgs a)
 
 hipError_t launch_resident(hipStream_t s, const ResidentArgs &args, int grid) {
   void *params[] = {const_cast<ResidentArgs *>(&args)};
-  return hipLaunchCooperativeKernel(
-      reinterpret_cast<const void *>(&resident_decode_kernel<896, 4864, 896>),
-      dim3(grid), dim3(kBlock), params, 0, s);
+  const void *fn =
+      args.stage_ticks
+          ? reinterpret_cast<const void *>(&resident_decode_kernel<896, 4864, 896, true>)
+          : reinterpret_cast<const void *>(&resident_decode_kernel<896, 4864, 896, false>);
+  return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kBlock), params, 0, s);
 }
 
 int resident_max_grid(int device) {
@@ -488,7 +528,7 @@ int resident_max_grid(int device) {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     return 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &per_cu, reinterpret_cast<const void *>(&resident_decode_kernel<896, 4864, 896>),
+          &per_cu, reinterpret_cast<const void *>(&resident_decode_kernel<896, 4864, 896, true>),
           kBlock, 0) != hipSuccess)
     return 0;
   return cus * per_cu;

@@ -10,6 +10,8 @@
 namespace qd {
 
 constexpr int kResidentMaxChunks = 80;  // split-KV chunks the merge holds in LDS
+// Profiled stages: QKV, attention, O-proj, gate/up, down, LM head, argmax.
+constexpr int kResidentStages = 7;
 
 // Arguments of one resident generation on one sequence slot.
 struct ResidentArgs {
@@ -37,6 +39,7 @@ struct ResidentArgs {
   uint32_t *out_tokens;         // [max_tokens]
   SeqState *st;
   uint32_t *error;              // zero at launch; nonzero: a barrier gave up
+  uint64_t *stage_ticks;        // nullptr, or [kResidentStages] 100 MHz ticks
   int history;
   int capacity;
   int vocab;

@@ -82,6 +82,7 @@ _SIGNATURES = {
     "qd_write_kv": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _F, _F]),
     "qd_read_kv": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _F, _F]),
     "qd_read_decode_state": (C.c_int, [_E, C.c_uint32, C.POINTER(DecodeState)]),
+    "qd_read_activation": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F, C.c_size_t]),
     "qd_layer_step": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F]),
     "qd_step": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F, _U, _F]),
     "qd_prefill": (C.c_int, [_E, C.c_uint32, _U, C.c_uint32, _F, _U, _F]),
@@ -91,6 +92,8 @@ _SIGNATURES = {
     "qd_last_timing": (C.c_int, [_E, C.POINTER(Timing)]),
     "qd_profile_kernels": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(KernelStat),
                                      C.c_uint32, _U]),
+    "qd_profile_resident": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double),
+                                      C.c_uint32, _U]),
     "qd_sync": (C.c_int, [_E]),
     "qd_bundle_write_layer": (C.c_int, [C.c_char_p, C.c_char_p, _U, C.c_float, _F]),
     "qd_bundle_read_layer": (C.c_int, [C.c_char_p, _U, _F, _F, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -234,6 +237,13 @@ class Engine:
         _check(lib().qd_read_kv(self.handle, seq, layer, start, count, _f(k), _f(v)))
         return k, v
 
+    def read_activation(self, seq: int, which: int) -> np.ndarray:
+        c = self.config
+        n = [c.hidden, c.heads * c.head_dim, c.heads * c.head_dim, c.intermediate][which]
+        out = np.empty(n, np.float32)
+        _check(lib().qd_read_activation(self.handle, seq, which, _f(out), n))
+        return out
+
     def decode_state(self, seq: int) -> DecodeState:
         s = DecodeState()
         _check(lib().qd_read_decode_state(self.handle, seq, C.byref(s)))
@@ -288,6 +298,15 @@ class Engine:
         for s in stats[:n.value]:
             out[s.name.decode()] = (int(s.launches), s.total_us / s.launches, s.bytes / s.launches)
         return out
+
+    RESIDENT_STAGES = ("qkv", "attention", "oproj", "gateup", "down", "lmhead", "argmax")
+
+    def profile_resident(self, seq: int, first_token: int, tokens: int) -> dict:
+        """Per-stage microseconds (summed over `tokens`) of the resident kernel."""
+        out = (C.c_double * 8)()
+        n = C.c_uint32()
+        _check(lib().qd_profile_resident(self.handle, seq, first_token, tokens, out, 8, C.byref(n)))
+        return {name: out[i] for i, name in enumerate(self.RESIDENT_STAGES[:n.value])}
 
     def last_timing(self) -> Timing:
         t = Timing()
