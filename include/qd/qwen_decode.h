@@ -237,9 +237,9 @@ QD_API qd_status qd_profile_kernels(qd_engine *engine, uint32_t seq,
                                     uint32_t *count);
 
 /* Runs qd_generate_resident's resident megakernel in its profiled form
- * (workgroup 0 stamps every grid-barrier exit) and reports per-stage totals
- * in microseconds: QKV, attention, O projection, gate/up, down, LM head,
- * argmax (7 entries). Advances the position like qd_generate_resident. The
+ * (workgroup 0 stamps the end of every input wait and every stage) and
+ * reports totals in microseconds as (wait, work) pairs for QKV, attention,
+ * O projection, gate/up, down, LM head and argmax (14 entries). Advances the position like qd_generate_resident. The
  * counterpart of the reference's stage profile kernel
  * (benchmarks/qwen_stateful_graph_kernel.cpp:837-865). */
 QD_API qd_status qd_profile_resident(qd_engine *engine, uint32_t seq,

@@ -11,8 +11,25 @@ constexpr int kRotary = kHeadDim / 2;  // rotate-half frequencies per head
 constexpr int kWave = 64;              // CDNA wavefront
 constexpr int kBlock = 256;            // threads per workgroup
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int kAttnChunk = 64;         // KV positions per split-KV partial
 constexpr int kMaxGroup = 16;          // query heads per KV head
+
+// Split-KV attention geometry (qd_attention.hpp): chunks are multiples of
+// kAttnPass positions, at most kAttnMaxChunks per head; a partial record is
+// (m, l, acc[64]).
+constexpr int kAttnPass = 64;
+constexpr int kAttnMaxChunks = 16;
+constexpr int kPartStride = kHeadDim + 2;
+
+__host__ __device__ inline int attn_chunk_len(int length) {
+  const int passes = (length + kAttnPass - 1) / kAttnPass;
+  const int per_chunk = (passes + kAttnMaxChunks - 1) / kAttnMaxChunks;
+  return per_chunk * kAttnPass;
+}
+
+__host__ __device__ inline int attn_chunks(int length) {
+  const int cl = attn_chunk_len(length);
+  return (length + cl - 1) / cl;
+}
 
 enum Mode : uint32_t { kModeStep = 0, kModeGenerate = 1 };
 

@@ -98,7 +98,6 @@ struct qd_engine {
   qd_config cfg{};
   size_t H = 0, I = 0, NQ = 0, NKV = 0, QD = 0, KVD = 0, QKV = 0, V = 0, L = 0,
          CAP = 0, B = 0;
-  int max_chunks = 0;
   hipStream_t stream = nullptr;
   hipEvent_t ev_begin = nullptr, ev_end = nullptr;
   std::vector<void *> allocs;
@@ -111,7 +110,7 @@ struct qd_engine {
   float *rope_cos = nullptr, *rope_sin = nullptr;
   float *hidden = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr,
         *logits = nullptr;
-  float *part_m = nullptr, *part_l = nullptr, *part_acc = nullptr;
+  float *part = nullptr;  // split-KV partials [16][heads][66]
   float *part_val = nullptr;
   uint32_t *part_idx = nullptr;
   uint32_t *tokens_dev = nullptr;  // [capacity]
@@ -121,11 +120,9 @@ struct qd_engine {
 
   // Resident megakernel state.
   qd::LayerPtrs *layer_ptrs_dev = nullptr;  // [layers]
-  float *h1 = nullptr;                      // [hidden]
-  float *top_val = nullptr;                 // [grid]
-  uint32_t *top_idx = nullptr;              // [grid]
-  uint32_t *flags = nullptr;                // [grid]
-  uint32_t *group_count = nullptr;          // [kv_heads * 64]
+  uint64_t *tagged = nullptr;               // (value, tag) arena
+  size_t tagged_elems = 0;
+  uint32_t epoch = 0;                       // last launch epoch (1..4095)
   uint32_t *resident_error = nullptr;       // [1]
   int resident_grid = 0;                    // 0: resident path unavailable
   const char *resident_off_reason = "";
@@ -221,10 +218,7 @@ struct qd_engine {
     a.act = act + seq * I;
     a.k_cache = kv_slice(k_cache, seq, layer);
     a.v_cache = kv_slice(v_cache, seq, layer);
-    a.part_m = part_m;
-    a.part_l = part_l;
-    a.part_acc = part_acc;
-    a.max_chunks = max_chunks;
+    a.part = part;
     a.capacity = static_cast<int>(CAP);
     a.nq = static_cast<int>(NQ);
     a.nkv = static_cast<int>(NKV);
@@ -267,7 +261,7 @@ struct qd_engine {
   // `length` positions: weights, KV rows and activations each moved once.
   double kernel_bytes(int kernel, double length) const {
     const double f = 4.0;
-    const double chunks = std::ceil(length / qd::kAttnChunk);
+    const double chunks = qd::attn_chunks(static_cast<int>(length));
     switch (kernel) {
       case qd::kKEmbed: return 2 * H * f;
       case qd::kKQkvRope:
@@ -284,52 +278,61 @@ struct qd_engine {
     return 0;
   }
 
-  // Resets the barrier words and launches the resident megakernel (stream
-  // ordered; no synchronisation).
+  // Launches the resident megakernel (stream ordered; no synchronisation).
+  // Each launch gets a fresh epoch so no tag of an earlier launch matches;
+  // when the epoch counter wraps the tagged arena is cleared first.
   void launch_resident(uint32_t seq, uint32_t first_token, uint32_t max_tokens,
                        uint32_t eos, float *hist, int use_hist, uint64_t *stage_ticks) {
-      qd::ResidentArgs ra{};
-      ra.layer_ptrs = layer_ptrs_dev;
-      ra.embed = embed;
-      ra.head = lm_head;
-      ra.final_norm = final_norm;
-      ra.rope_cos = rope_cos;
-      ra.rope_sin = rope_sin;
-      ra.k_cache = kv_slice(k_cache, seq, 0);
-      ra.v_cache = kv_slice(v_cache, seq, 0);
-      ra.hidden = hidden + size_t(seq) * H;
-      ra.h1 = h1;
-      ra.q = q + size_t(seq) * QD;
-      ra.attn = attn + size_t(seq) * QD;
-      ra.act = act + size_t(seq) * I;
-      ra.part_m = part_m;
-      ra.part_l = part_l;
-      ra.part_acc = part_acc;
-      ra.group_count = group_count;
-      ra.logits = hist;
-      ra.top_val = top_val;
-      ra.top_idx = top_idx;
-      ra.flags = flags;
-      ra.out_tokens = tokens_dev;
-      ra.st = states + seq;
-      ra.error = resident_error;
-      ra.history = use_hist;
-      ra.capacity = static_cast<int>(CAP);
-      ra.vocab = static_cast<int>(V);
-      ra.layers = static_cast<int>(L);
-      ra.nq = static_cast<int>(NQ);
-      ra.nkv = static_cast<int>(NKV);
-      ra.max_chunks = max_chunks;
-      ra.eps = cfg.rms_eps;
-      ra.first_token = first_token;
-      ra.start_position = positions[seq];
-      ra.max_tokens = max_tokens;
-      ra.eos = eos;
-      check(hipMemsetAsync(flags, 0, size_t(resident_grid) * 4, stream), "memset");
-      check(hipMemsetAsync(group_count, 0, NKV * 64 * 4, stream), "memset");
-      check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
-      ra.stage_ticks = stage_ticks;
-      check(qd::launch_resident(stream, ra, resident_grid), "resident launch");
+    epoch = epoch % 4095u + 1u;
+    if (epoch == 1u)
+      check(hipMemsetAsync(tagged, 0, tagged_elems * 8, stream), "memset");
+    uint64_t *p = tagged;
+    auto take = [&](size_t n) {
+      uint64_t *r = p;
+      p += n;
+      return static_cast<void *>(r);
+    };
+    qd::ResidentArgs ra{};
+    ra.layer_ptrs = layer_ptrs_dev;
+    ra.embed = embed;
+    ra.head = lm_head;
+    ra.final_norm = final_norm;
+    ra.rope_cos = rope_cos;
+    ra.rope_sin = rope_sin;
+    ra.k_cache = kv_slice(k_cache, seq, 0);
+    ra.v_cache = kv_slice(v_cache, seq, 0);
+    ra.q = take(QD);
+    ra.kvnew = take(2 * KVD);
+    ra.part = take(size_t(qd::kAttnMaxChunks) * NQ * qd::kPartStride);
+    ra.attn = take(QD);
+    ra.h1 = take(H);
+    ra.act = take(I);
+    ra.hidden = take(H);
+    ra.top = take(2 * size_t(resident_grid));
+    ra.logits = hist;
+    ra.out_tokens = tokens_dev;
+    ra.st = states + seq;
+    ra.error = resident_error;
+    ra.stage_ticks = stage_ticks;
+    ra.history = use_hist;
+    ra.capacity = static_cast<int>(CAP);
+    ra.vocab = static_cast<int>(V);
+    ra.layers = static_cast<int>(L);
+    ra.nq = static_cast<int>(NQ);
+    ra.nkv = static_cast<int>(NKV);
+    ra.eps = cfg.rms_eps;
+    ra.first_token = first_token;
+    ra.start_position = positions[seq];
+    ra.max_tokens = max_tokens;
+    ra.eos = eos;
+    ra.epoch = epoch << qd::kTagSeqBits;
+    check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
+    check(qd::launch_resident(stream, ra, resident_grid), "resident launch");
+  }
+
+  // Resident launches name (token, stage) pairs in kTagSeqBits bits.
+  bool resident_fits(uint32_t max_tokens) const {
+    return uint64_t(max_tokens) * (6 * L + 1) + 1 < (uint64_t(1) << qd::kTagSeqBits);
   }
 
   void sync() { check(hipStreamSynchronize(stream), "hipStreamSynchronize"); }
@@ -439,7 +442,6 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     e->L = c.layers;
     e->CAP = c.capacity;
     e->B = c.max_batch;
-    e->max_chunks = static_cast<int>((e->CAP + qd::kAttnChunk - 1) / qd::kAttnChunk);
     e->set_device();
     check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
     check(hipEventCreate(&e->ev_begin), "hipEventCreate");
@@ -476,9 +478,7 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     e->attn = e->alloc<float>(e->B * e->QD);
     e->act = e->alloc<float>(e->B * e->I);
     e->logits = e->alloc<float>(e->B * e->V);
-    e->part_m = e->alloc<float>(size_t(e->max_chunks) * e->NQ);
-    e->part_l = e->alloc<float>(size_t(e->max_chunks) * e->NQ);
-    e->part_acc = e->alloc<float>(size_t(e->max_chunks) * e->NQ * qd::kHeadDim);
+    e->part = e->alloc<float>(size_t(qd::kAttnMaxChunks) * e->NQ * qd::kPartStride);
     e->part_val = e->alloc<float>(kLmHeadParts);
     e->part_idx = e->alloc<uint32_t>(kLmHeadParts);
     e->tokens_dev = e->alloc<uint32_t>(e->CAP);
@@ -503,27 +503,25 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     const char *env = std::getenv("QD_RESIDENT");
     if (env && std::strcmp(env, "0") == 0) {
       e->resident_off_reason = "QD_RESIDENT=0";
-    } else if (e->max_chunks > qd::kResidentMaxChunks) {
-      e->resident_off_reason = "capacity beyond the resident split-KV table";
-    } else if (cus <= 0 || max_grid < cus) {
+    } else if (cus < 64 || max_grid < cus) {
       e->resident_off_reason = "device cannot co-schedule one workgroup per CU";
     } else {
-      e->resident_grid = cus;
+      // Two workgroups per CU when they fit: twice the waves in flight.
+      e->resident_grid = std::min({max_grid, 2 * cus, qd::kMaxResidentGrid});
       // Diagnostic override of the resident grid (1..max co-resident).
       if (const char *g = std::getenv("QD_RESIDENT_GRID")) {
         const int want = std::atoi(g);
-        if (want >= 1 && want <= max_grid) e->resident_grid = want;
+        if (want >= 64 && want <= std::min(max_grid, qd::kMaxResidentGrid)) e->resident_grid = want;
       }
     }
     const int grid_alloc = std::max({cus, max_grid, 1});
     e->layer_ptrs_dev = e->alloc<qd::LayerPtrs>(e->L);
     check(hipMemcpyAsync(e->layer_ptrs_dev, e->layers.data(), e->L * sizeof(qd::LayerPtrs),
                          hipMemcpyHostToDevice, e->stream), "layer table upload");
-    e->h1 = e->alloc<float>(e->H);
-    e->top_val = e->alloc<float>(grid_alloc);
-    e->top_idx = e->alloc<uint32_t>(grid_alloc);
-    e->flags = e->alloc<uint32_t>(grid_alloc);
-    e->group_count = e->alloc<uint32_t>(e->NKV * 64);
+    e->tagged_elems = qd::resident_tagged_elems(int(e->H), int(e->NQ), int(e->NKV), int(e->I),
+                                                grid_alloc);
+    e->tagged = e->alloc<uint64_t>(e->tagged_elems);
+    check(hipMemsetAsync(e->tagged, 0, e->tagged_elems * 8, e->stream), "memset");
     e->resident_error = e->alloc<uint32_t>(1);
     e->sync();
     *out = e.release();
@@ -946,7 +944,8 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
       use_hist = 1;
     }
     e->push_state(seq, first_token, qd::kModeGenerate, eos, max_tokens);
-    if (e->resident_grid > 0) {
+    const bool resident = e->resident_grid > 0 && e->resident_fits(max_tokens);
+    if (resident) {
       check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
       e->launch_resident(seq, first_token, max_tokens, eos, hist, use_hist, nullptr);
     } else {
@@ -957,7 +956,7 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
                          e->stream), "D2H");
     e->sync();
-    if (e->resident_grid > 0) {
+    if (resident) {
       uint32_t err = 0;
       check(hipMemcpy(&err, e->resident_error, 4, hipMemcpyDeviceToHost), "D2H");
       if (err) fail(QD_ERROR_RUNTIME, "resident kernel barrier wait timed out");
@@ -1066,6 +1065,7 @@ qd_status qd_profile_resident(qd_engine *e, uint32_t seq, uint32_t first_token, 
     if (first_token >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", first_token);
     if (size_t(e->positions[seq]) + tokens > e->CAP)
       fail(QD_ERROR_INVALID_ARGUMENT, "profiling %u tokens overflows capacity", tokens);
+    if (!e->resident_fits(tokens)) fail(QD_ERROR_INVALID_ARGUMENT, "too many tokens for one resident launch");
     e->set_device();
     uint64_t *ticks = e->alloc<uint64_t>(qd::kResidentStages);
     e->launch_resident(seq, first_token, tokens, UINT32_MAX, e->logits + size_t(seq) * e->V, 0, ticks);

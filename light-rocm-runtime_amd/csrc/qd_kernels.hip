@@ -21,6 +21,7 @@
 #include <cstdint>
 
 #include "qd_device.hpp"
+#include "qd_attention.hpp"
 #include "qd_device_math.hpp"
 #include "qd_kernels.hpp"
 
@@ -96,123 +97,56 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
   }
 }
 
-// Split-KV decode attention: workgroup (chunk, kv head) scores the chunk's
-// positions against every query head of the group (the KV tile is read once
-// for all of them) and writes an online-softmax partial (max, sum, acc[64]).
-// Thread t owns position t/4 of the chunk and dims [16*(t%4), +16).
+// Split-KV decode attention partials (qd_attention.hpp): workgroup
+// (chunk, KV head) writes one record (m, l, acc[64]) per query head of the
+// group into part[chunk][head][66].
 __global__ __launch_bounds__(kBlock) void attn_partial_kernel(
     const float *__restrict__ q, const float *__restrict__ k_cache,
     const float *__restrict__ v_cache, const SeqState *__restrict__ st,
-    int nq, int nkv, float *__restrict__ part_m, float *__restrict__ part_l,
-    float *__restrict__ part_acc, int capacity) {
-  __shared__ float qs[kMaxGroup * kHeadDim];
-  __shared__ float red[kWavesPerBlock];
-  __shared__ float acc_red[kWavesPerBlock][kHeadDim];
+    int nq, int nkv, float *__restrict__ part, int capacity) {
+  __shared__ AttnLds sh;
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
-  const int length = static_cast<int>(st->position) + 1;
+  const int position = static_cast<int>(st->position);
+  const int length = position + 1;
   const int chunk = blockIdx.x;
-  if (chunk * kAttnChunk >= length) return;
-  const int kvh = blockIdx.y;
+  if (chunk >= attn_chunks(length)) return;
+  const int chunk_len = attn_chunk_len(length);
+  const int g = blockIdx.y;
   const int group = nq / nkv;
   const int kv_dim = nkv * kHeadDim;
-  const int t = threadIdx.x;
-  const int lane = lane_id();
-  const int quarter = t & 3;
-  const int j = chunk * kAttnChunk + (t >> 2);
-  const bool valid = j < length;
-
-  for (int e = t; e < group * kHeadDim; e += kBlock)
-    qs[e] = q[kvh * group * kHeadDim + e];
-
-  float4 kr[4], vr[4];
-  const size_t row = static_cast<size_t>(valid ? j : 0) * kv_dim +
-                     kvh * kHeadDim + quarter * 16;
-  const float4 *k4 = reinterpret_cast<const float4 *>(k_cache + row);
-  const float4 *v4 = reinterpret_cast<const float4 *>(v_cache + row);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    kr[e] = k4[e];
-    vr[e] = v4[e];
-  }
-  __syncthreads();
-
-  for (int g = 0; g < group; ++g) {
-    const float4 *q4 =
-        reinterpret_cast<const float4 *>(qs + g * kHeadDim + quarter * 16);
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) s = fma4(kr[e], q4[e], s);
-    s += __shfl_xor(s, 1, kWave);
-    s += __shfl_xor(s, 2, kWave);
-    s = valid ? s * rsqrtf(static_cast<float>(kHeadDim)) : -INFINITY;
-
-    float m = s;
-#pragma unroll
-    for (int o = 4; o < kWave; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
-    if (lane == 0) red[wave_id()] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-
-    const float p = valid ? expf(s - m) : 0.f;
-    float l = p;
-#pragma unroll
-    for (int o = 4; o < kWave; o <<= 1) l += __shfl_xor(l, o, kWave);
-    if (lane == 0) red[wave_id()] = l;
-
-    float a[16];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      a[4 * e + 0] = p * vr[e].x;
-      a[4 * e + 1] = p * vr[e].y;
-      a[4 * e + 2] = p * vr[e].z;
-      a[4 * e + 3] = p * vr[e].w;
-    }
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-#pragma unroll
-      for (int o = 4; o < kWave; o <<= 1) a[e] += __shfl_xor(a[e], o, kWave);
-    }
-    if (lane < 4) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc_red[wave_id()][quarter * 16 + e] = a[e];
-    }
-    __syncthreads();
-    const int h = kvh * group + g;
-    if (t < kHeadDim) {
-      float sum = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWavesPerBlock; ++w) sum += acc_red[w][t];
-      part_acc[(static_cast<size_t>(chunk) * nq + h) * kHeadDim + t] = sum;
-    }
-    if (t == 0) {
-      part_m[chunk * nq + h] = m;
-      part_l[chunk * nq + h] = red[0] + red[1] + red[2] + red[3];
-    }
-    __syncthreads();
-  }
+  const int begin = chunk * chunk_len;
+  const int end = min(length, begin + chunk_len);
+  const Plain kc(k_cache), vc(v_cache);
+  const Plain knew(k_cache + static_cast<size_t>(position) * kv_dim);
+  const Plain vnew(v_cache + static_cast<size_t>(position) * kv_dim);
+  attn_partial_unit(kc, vc, knew, vnew, position, g, group, kv_dim, begin, end, sh,
+                    [&]() {
+                      for (int e = threadIdx.x; e < group * kHeadDim; e += kBlock)
+                        sh.qs[e] = q[g * group * kHeadDim + e];
+                      __syncthreads();
+                    },
+                    [&](int hl, float m, float l, float acc, int d) {
+                      float *rec =
+                          part + ((g * group + hl) * kAttnMaxChunks + chunk) * kPartStride;
+                      rec[2 + d] = acc;
+                      if (d == 0) {
+                        rec[0] = m;
+                        rec[1] = l;
+                      }
+                    });
 }
 
-// Merges the split-KV partials of each query head into attn[h*64 + d].
+// Merges each head's partials into attn[h*64 + d].
 __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(
-    const float *__restrict__ part_m, const float *__restrict__ part_l,
-    const float *__restrict__ part_acc, const SeqState *__restrict__ st,
-    int nq, float *__restrict__ attn, int capacity) {
+    const float *__restrict__ part, const SeqState *__restrict__ st, int nq,
+    float *__restrict__ attn, int capacity) {
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
-  const int length = static_cast<int>(st->position) + 1;
-  const int chunks = (length + kAttnChunk - 1) / kAttnChunk;
+  const int chunks = attn_chunks(static_cast<int>(st->position) + 1);
   const int h = blockIdx.x;
   const int d = threadIdx.x;
-  float m = -INFINITY;
-  for (int c = 0; c < chunks; ++c) m = fmaxf(m, part_m[c * nq + h]);
-  float num = 0.f, den = 0.f;
-  for (int c = 0; c < chunks; ++c) {
-    const float scale = expf(part_m[c * nq + h] - m);
-    den = fmaf(scale, part_l[c * nq + h], den);
-    num = fmaf(scale, part_acc[(static_cast<size_t>(c) * nq + h) * kHeadDim + d],
-               num);
-  }
-  attn[h * kHeadDim + d] = num / den;
+  attn[h * kHeadDim + d] = attn_merge(
+      [&](int c, int k) { return part[(h * kAttnMaxChunks + c) * kPartStride + k]; }, chunks,
+      d);
 }
 
 // hidden[r] += Wo[r,:] . attn; unit u = rows (2u, 2u+1), contiguous.
@@ -437,15 +371,13 @@ hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
   }
   {
     Scope scope(m, kKAttnPartial);
-    attn_partial_kernel<<<dim3(p.max_chunks, p.nkv), kBlock, 0, s>>>(
-        p.q, p.k_cache, p.v_cache, p.st, p.nq, p.nkv, p.part_m, p.part_l,
-        p.part_acc, p.capacity);
+    attn_partial_kernel<<<dim3(kAttnMaxChunks, p.nkv), kBlock, 0, s>>>(
+        p.q, p.k_cache, p.v_cache, p.st, p.nq, p.nkv, p.part, p.capacity);
   }
   {
     Scope scope(m, kKAttnCombine);
-    attn_combine_kernel<<<p.nq, kHeadDim, 0, s>>>(p.part_m, p.part_l,
-                                                  p.part_acc, p.st, p.nq,
-                                                  p.attn, p.capacity);
+    attn_combine_kernel<<<p.nq, kHeadDim, 0, s>>>(p.part, p.st, p.nq, p.attn,
+                                                  p.capacity);
   }
   {
     Scope scope(m, kKOproj);

@@ -21,10 +21,7 @@ struct LayerLaunch {
   float *act;      // [intermediate]
   float *k_cache;  // this layer's [capacity, kv_heads*64]
   float *v_cache;
-  float *part_m;   // [max_chunks, heads]
-  float *part_l;
-  float *part_acc; // [max_chunks, heads, 64]
-  int max_chunks;
+  float *part;     // split-KV partials [16][heads][66]
   int capacity;  // KV positions of the slot; kernels skip positions beyond
   int nq;
   int nkv;

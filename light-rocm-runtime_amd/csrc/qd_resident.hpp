@@ -9,11 +9,15 @@
 
 namespace qd {
 
-constexpr int kResidentMaxChunks = 80;  // split-KV chunks the merge holds in LDS
-// Profiled stages: QKV, attention, O-proj, gate/up, down, LM head, argmax.
-constexpr int kResidentStages = 7;
+// Profiled intervals of workgroup 0, each stage split into waiting for its
+// input and working: QKV, attention, O-proj (with merge), gate/up, down,
+// LM head, argmax -> 14 entries (wait, work) per stage.
+constexpr int kResidentStages = 14;
+// Largest resident grid (the argmax partials are staged in LDS).
+constexpr int kMaxResidentGrid = 1024;
 
-// Arguments of one resident generation on one sequence slot.
+// Arguments of one resident generation on one sequence slot. The tagged
+// vectors hold 8-byte (value, tag) elements; see qd_resident.hip.
 struct ResidentArgs {
   const LayerPtrs *layer_ptrs;  // device array [layers]
   const float *embed;           // [vocab, hidden]
@@ -23,22 +27,18 @@ struct ResidentArgs {
   const float *rope_sin;
   float *k_cache;               // slot base [layers][capacity][kv_heads*64]
   float *v_cache;
-  float *hidden;                // [hidden] residual after each layer
-  float *h1;                    // [hidden] residual after the attention block
-  float *q;                     // [heads*64]
-  float *attn;                  // [heads*64]
-  float *act;                   // [intermediate]
-  float *part_m;                // [max_chunks, heads]
-  float *part_l;
-  float *part_acc;              // [max_chunks, heads, 64]
-  uint32_t *group_count;        // [kv_heads * 64], zero at launch
+  void *q;                      // tagged [heads*64]
+  void *kvnew;                  // tagged [2 * kv_heads*64]: this step's K | V
+  void *part;                   // tagged [heads][kAttnMaxChunks][66]
+  void *attn;                   // tagged [heads*64] merged attention
+  void *h1;                     // tagged [hidden]
+  void *act;                    // tagged [intermediate]
+  void *hidden;                 // tagged [hidden]
+  void *top;                    // tagged [2 * grid]
   float *logits;                // [vocab] or [max_tokens][vocab]
-  float *top_val;               // [grid]
-  uint32_t *top_idx;            // [grid]
-  uint32_t *flags;              // [grid], zero at launch
   uint32_t *out_tokens;         // [max_tokens]
   SeqState *st;
-  uint32_t *error;              // zero at launch; nonzero: a barrier gave up
+  uint32_t *error;              // zero at launch; nonzero: a wait gave up
   uint64_t *stage_ticks;        // nullptr, or [kResidentStages] 100 MHz ticks
   int history;
   int capacity;
@@ -46,13 +46,21 @@ struct ResidentArgs {
   int layers;
   int nq;
   int nkv;
-  int max_chunks;
   float eps;
   uint32_t first_token;
   uint32_t start_position;
   uint32_t max_tokens;
   uint32_t eos;
+  uint32_t epoch;               // launch epoch << kTagSeqBits, never 0
 };
+
+// Tags: epoch << kTagSeqBits | (token * (6 * layers + 1) + stage + 1).
+constexpr int kTagSeqBits = 20;
+// Elements of the tagged arena for a given grid.
+inline size_t resident_tagged_elems(int hidden, int heads, int kv_heads, int inter, int grid) {
+  return 2 * size_t(heads) * 64 + 2 * size_t(kv_heads) * 64 + 16 * size_t(heads) * 66 +
+         3 * size_t(hidden) + inter + 2 * size_t(grid);
+}
 
 hipError_t launch_resident(hipStream_t s, const ResidentArgs &args, int grid);
 // Largest co-resident grid on `device` (0 if the query fails).

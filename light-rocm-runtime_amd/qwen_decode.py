@@ -299,13 +299,14 @@ class Engine:
             out[s.name.decode()] = (int(s.launches), s.total_us / s.launches, s.bytes / s.launches)
         return out
 
-    RESIDENT_STAGES = ("qkv", "attention", "oproj", "gateup", "down", "lmhead", "argmax")
+    RESIDENT_STAGES = tuple(f"{s}.{k}" for s in ("qkv", "attention", "oproj", "gateup", "down",
+                                                  "lmhead", "argmax") for k in ("wait", "work"))
 
     def profile_resident(self, seq: int, first_token: int, tokens: int) -> dict:
         """Per-stage microseconds (summed over `tokens`) of the resident kernel."""
-        out = (C.c_double * 8)()
+        out = (C.c_double * 16)()
         n = C.c_uint32()
-        _check(lib().qd_profile_resident(self.handle, seq, first_token, tokens, out, 8, C.byref(n)))
+        _check(lib().qd_profile_resident(self.handle, seq, first_token, tokens, out, 16, C.byref(n)))
         return {name: out[i] for i, name in enumerate(self.RESIDENT_STAGES[:n.value])}
 
     def last_timing(self) -> Timing:
