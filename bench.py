@@ -33,6 +33,14 @@ PROMPT_STREAM = 0x300000
 WEIGHT_BYTES = 1_976_131_072
 
 
+# HBM bytes per decode token of the resident kernel, measured with rocprofv3
+# FETCH_SIZE (x2.000) + WRITE_SIZE (x1.000) on the 64-token launch of this
+# workload; the factors come from a 1 GiB device copy in the same profile
+# (profiles/resident_decode_kernel_config2.md). Re-measured when the kernel
+# changes; None where no measurement exists.
+RESIDENT_TRAFFIC_PER_TOKEN = 2_024_293_558
+
+
 def step_bytes(length: int) -> int:
     return WEIGHT_BYTES + 24_576 * length + 24_576 + 607_744 + 3_584
 
@@ -68,12 +76,35 @@ def cpu_baseline(budget_s: float = 12.0):
                       f"24 layers + 151936-row LM head, oracle/libqwen_oracle.so FP32 OpenMP"}
 
 
+def copy_probe(mib: int):
+    """Copies `mib` MiB device-to-device through the HIP runtime: a plain copy
+    kernel of known size whose FETCH_SIZE / WRITE_SIZE counters calibrate the
+    per-dispatch HBM traffic of the decode kernel in the same profile."""
+    import ctypes as C
+
+    hip = C.CDLL("libamdhip64.so")
+    n = mib << 20
+    src, dst = C.c_void_p(), C.c_void_p()
+    for p in (src, dst):
+        if hip.hipMalloc(C.byref(p), C.c_size_t(n)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    hip.hipMemset(src, 1, C.c_size_t(n))
+    for _ in range(3):
+        hip.hipMemcpy(dst, src, C.c_size_t(n), 3)  # device to device
+    hip.hipDeviceSynchronize()
+    hip.hipFree(src)
+    hip.hipFree(dst)
+    log(f"copy probe: 3 x {mib} MiB device-to-device")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); the decode path "
@@ -112,14 +143,18 @@ def main():
         # One resident launch runs all K tokens: its HIP-event duration on the
         # engine stream is the kernel time, its algorithmic bytes the K steps'.
         dom_name, avg_us, avg_bytes = "resident_decode_kernel", timing.total_us, float(total_bytes)
+        traffic = RESIDENT_TRAFFIC_PER_TOKEN * K if RESIDENT_TRAFFIC_PER_TOKEN else None
     else:
         eng.kv_reset(0, PROMPT)
         prof = eng.profile_kernels(0, first, min(K, 16))
         dom_name, (launches, avg_us, avg_bytes) = max(prof.items(), key=lambda kv: kv[1][0] * kv[1][1])
+        traffic = None
         log("kernel profile: " + ", ".join(f"{n}={v[1]:.1f}us" for n, v in prof.items()))
     achieved = avg_bytes / (avg_us * 1e-6) / 1e9
     eng.close()
 
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
     cpu = None if args.no_cpu else cpu_baseline()
     out = {
         "metric": METRIC,
@@ -148,7 +183,7 @@ def main():
         "device_tokens_per_s": round(K / dev_s, 2),
         "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "avg_us": round(avg_us, 3),
+                     "traffic": traffic, "avg_us": round(avg_us, 3),
                      "bytes_per_launch": round(avg_bytes)},
         "cpu_baseline": cpu,
         "path": f"resident megakernel, {grid} workgroups" if grid else "stream-ordered kernels",
