@@ -1,0 +1,104 @@
+"""The qd_run command-line runner: argument handling (CPU) and its stdout
+contract on the GPU, parsed with the same patterns the reference's wrapper
+uses (tools/run_qwen_e2e.py:28-35)."""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import qwen_decode as qd
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+RUNNER = os.path.join(ROOT, "light-rocm-runtime_amd", "qd_run")
+
+GENERATED_TOKEN_IDS_RE = re.compile(r"^generated_token_ids=\[([0-9]+(?:,[0-9]+)*)\]$", re.MULTILINE)
+TOP_LOGIT_RE = re.compile(
+    r"^step ([1-9][0-9]*) top_token=([0-9]+) logit=([-+0-9.eE]+) vocab=([0-9]+)$", re.MULTILINE)
+STOP_REASON_RE = re.compile(r"^stop_reason=(eos_token|max_new_tokens)$", re.MULTILINE)
+
+needs_runner = pytest.mark.skipif(not os.path.exists(RUNNER), reason="qd_run not built")
+
+
+def run(*args, timeout=120):
+    return subprocess.run([RUNNER, *map(str, args)], capture_output=True, text=True,
+                          timeout=timeout)
+
+
+@needs_runner
+def test_help_exits_zero():
+    r = run("--help")
+    assert r.returncode == 0 and "usage: qd_run" in r.stdout
+
+
+@needs_runner
+@pytest.mark.parametrize("args,needle", [
+    ((), "exactly one of --weights-dir and --synthetic-seed"),
+    (("--synthetic-seed", "1"), "--prompt-token-ids is required"),
+    (("--weights-dir", "/nonexistent", "--prompt-token-ids", "1"), "--weights-dir requires --layers"),
+    (("--synthetic-seed", "1", "--prompt-token-ids", "1,,2"), "empty entry"),
+    (("--synthetic-seed", "x", "--prompt-token-ids", "1"), "non-negative integer"),
+    (("--synthetic-seed", "1", "--prompt-token-ids", "1", "--max-new-tokens", "0"), "must be positive"),
+    (("--synthetic-seed", "1", "--prompt-token-ids", "1,2,3", "--max-new-tokens", "4", "--keys", "2"),
+     "--keys must cover"),
+    (("--bogus",), "unknown option --bogus"),
+])
+def test_argument_errors(args, needle):
+    r = run(*args)
+    assert r.returncode == 2, r.stderr
+    assert needle in r.stderr
+
+
+@needs_runner
+def test_no_device_is_a_clear_error():
+    if qd.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    r = run("--synthetic-seed", 1, "--layers", 2, "--vocab", 4096, "--prompt-token-ids", "1,2")
+    assert r.returncode == 3 and "no HIP device" in r.stderr
+
+
+@needs_runner
+@pytest.mark.gpu
+@pytest.mark.parametrize("resident", [False, True])
+def test_stdout_contract_matches_engine(resident):
+    print(f"[gpu-case] qd_run 2 layers vocab 4096 resident={resident}", flush=True)
+    prompt = [5, 17, 400, 9]
+    n = 6
+    args = ["--synthetic-seed", 3, "--layers", 2, "--vocab", 4096,
+            "--prompt-token-ids", ",".join(map(str, prompt)), "--max-new-tokens", n, "--e2e-check"]
+    if resident:
+        args.append("--resident")
+    r = run(*args)
+    assert r.returncode == 0, r.stderr
+    ids = [int(x) for x in GENERATED_TOKEN_IDS_RE.search(r.stdout).group(1).split(",")]
+    steps = TOP_LOGIT_RE.findall(r.stdout)
+    assert STOP_REASON_RE.search(r.stdout).group(1) == "max_new_tokens"
+    assert len(ids) == n and [int(s[0]) for s in steps] == list(range(1, n + 1))
+    assert [int(s[1]) for s in steps] == ids
+    assert all(int(s[3]) == 4096 for s in steps)
+
+    with qd.Engine(layers=2, vocab=4096, capacity=64, max_batch=1) as eng:
+        eng.load_synthetic(3)
+        tok, logits, _ = eng.prefill(0, np.array(prompt, np.uint32), want_logits=True)
+        want = [tok]
+        for _ in range(n - 1):
+            tok, _, _ = eng.step(0, tok, want_logits=False)
+            want.append(tok)
+    assert ids == want
+    assert abs(float(steps[0][2]) - float(logits.max())) <= 1e-5 * abs(float(logits.max())) + 1e-6
+
+
+@needs_runner
+@pytest.mark.gpu
+def test_eos_stops_runner():
+    print("[gpu-case] qd_run eos", flush=True)
+    base = ["--synthetic-seed", 3, "--layers", 2, "--vocab", 4096, "--prompt-token-ids", "5,17"]
+    first = run(*base, "--max-new-tokens", 3)
+    assert first.returncode == 0, first.stderr
+    ids = [int(x) for x in GENERATED_TOKEN_IDS_RE.search(first.stdout).group(1).split(",")]
+    r = run(*base, "--max-new-tokens", 3, "--eos-token-id", ids[1], "--resident", "--e2e-check")
+    assert r.returncode == 0, r.stderr
+    got = [int(x) for x in GENERATED_TOKEN_IDS_RE.search(r.stdout).group(1).split(",")]
+    assert got == ids[:2]
+    assert STOP_REASON_RE.search(r.stdout).group(1) == "eos_token"
