@@ -239,13 +239,30 @@ QD_API qd_status qd_profile_kernels(qd_engine *engine, uint32_t seq,
 /* Runs qd_generate_resident's resident megakernel in its profiled form
  * (workgroup 0 stamps the end of every input wait and every stage) and
  * reports totals in microseconds as (wait, work) pairs for QKV, attention,
- * O projection, gate/up, down, LM head and argmax (14 entries). Advances the position like qd_generate_resident. The
+ * O projection, gate/up, down, LM head and argmax (14 entries), then three
+ * sub-phases of the attention work (K/V staging, softmax math, emit) that
+ * the attention "work" entry excludes (17 entries). Advances the position
+ * like qd_generate_resident. The
  * counterpart of the reference's stage profile kernel
  * (benchmarks/qwen_stateful_graph_kernel.cpp:837-865). */
 QD_API qd_status qd_profile_resident(qd_engine *engine, uint32_t seq,
                                      uint32_t first_token, uint32_t tokens,
                                      double *stage_us, uint32_t capacity,
                                      uint32_t *count);
+
+/* Diagnostic timeline of the resident megakernel: runs like
+ * qd_profile_resident and records, for token `trace_token` of the launch,
+ * the 100 MHz timestamp at which every workgroup ended every stage:
+ * timeline[workgroup][row][stage] with rows = layers + 1 (the last row holds
+ * the LM head / argmax stages) and stages = the qd_profile_resident entries.
+ * capacity is in entries; the dimensions are returned (also on a capacity
+ * error). No counterpart in the reference; it locates the critical path
+ * between the stages' producers and consumers. */
+QD_API qd_status qd_trace_resident(qd_engine *engine, uint32_t seq,
+                                   uint32_t first_token, uint32_t tokens,
+                                   uint32_t trace_token, uint64_t *timeline,
+                                   size_t capacity, uint32_t *workgroups,
+                                   uint32_t *rows, uint32_t *stages);
 
 /* Timing of the last qd_generate_resident call. */
 QD_API qd_status qd_last_timing(const qd_engine *engine, qd_timing *timing);

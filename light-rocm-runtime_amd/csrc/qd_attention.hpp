@@ -3,9 +3,9 @@
 //
 // Split-KV: the attended positions 0..L-1 are cut into chunks of
 // attn_chunk_len(L) positions (a multiple of 64, at most kAttnMaxChunks
-// chunks). A workgroup owns one (KV head, chunk) unit and produces, for each
-// of the group's query heads, an online-softmax partial (max m, sum l,
-// acc[64]); the chunk is walked in passes of 64 positions. A merge combines
+// chunks). A workgroup owns one (query head, chunk) unit and produces an
+// online-softmax partial (max m, sum l, acc[64]); the heads of a group read
+// the same K/V rows, the repeats served by the caches. A merge combines
 // the partials of a head: out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.
 // Semantics: benchmarks/qwen_stateful_graph_kernel.cpp:554-600 (scale
 // 1/sqrt(64), query head h reads KV head h / (heads / kv_heads), positions
@@ -23,130 +23,161 @@ namespace qd {
 
 namespace dev {
 
+// Positions of a pass owned by one wave (lane l: position 16*wave + l/4,
+// dims [16*(l%4), +16)).
+constexpr int kWavePositions = kAttnPass / kWavesPerBlock;
+
 struct AttnLds {
-  float qs[kMaxGroup * kHeadDim];      // the group's query heads
-  float vs[kAttnPass][kHeadDim];       // V rows of the current pass
-  float ps[kMaxGroup][kAttnPass];      // scores, then probabilities
-  float m[kMaxGroup];                  // running max per head
-  float l[kMaxGroup];                  // running sum per head
-  float scale[kMaxGroup];              // e^(m_old - m_new) of the pass
+  float qkv[3 * kHeadDim];                  // the unit's query head, then this step's K, V row
+  float vs[kAttnPass][kHeadDim];            // V rows of the current pass
+  float ps[kAttnPass];                      // probabilities of the current pass
+  float wp[kWavesPerBlock][kPartStride];    // per-wave partials (m, l, acc)
 };
 
-// One (KV head g, chunk) unit: 256 threads; thread t scores position t/4 of
-// the pass on dims [16*(t%4), +16) and owns outputs o = t and t + 256 of the
-// group's heads*64 accumulators. wait_q() (whole workgroup) must leave the
-// group's queries in lds.qs and make knew/vnew readable; it runs once, after
-// the first pass's cached rows were requested. kcache/vcache
-// load cached K/V rows ([position][kv_heads*64], float4 index); knew/vnew
-// supply the row at `new_pos` (the position this step writes, whose values
-// may not be in the cache yet) with the same row-relative indexing. Results
-// leave through emit(h_local, m, l, acc_d, d), called once per output
-// (head, d); m and l are the head's softmax max and sum.
-template <typename KvSrc, typename NewSrc, typename WaitQ, typename Emit>
+struct NoProbe {
+  __device__ void operator()(int) const {}
+};
+
+// One (query head, chunk) unit, 256 threads; g is the head's KV head. The
+// chunk is walked in passes of 16 * kWaves positions split over the first
+// kWaves waves (any further wave only joins the barriers):
+// thread t holds position t/4 of the pass with dims [16*(t%4), +16) of its
+// K and V rows in registers (requested one pass ahead) and the matching 16
+// query dims. Per pass each wave scores its 16 positions (16-dim partial dot
+// per lane, summed over the quad), keeps an online softmax over its own
+// positions (running max m, sum l) and accumulates P.V with lane = output
+// dim from the pass's V rows staged in LDS. After the last pass wave 0
+// merges the kWaves wave partials (out = sum_w e^(m_w - M) acc_w,
+// l = sum_w e^(m_w - M) l_w) and emits them.
+//
+// wait_q(request) (whole workgroup, ends with a workgroup barrier) must
+// call request() once -- it asks for the first pass's cached rows -- and
+// leave the query head in lds.qkv[0, 64) and knew/vnew readable. kcache/vcache load
+// cached K/V rows ([position][kv_heads*64], float4 index); knew/vnew supply
+// the row at `new_pos` (the position this step writes, whose values may not
+// be in the cache yet) with the same row-relative indexing. Results leave
+// through emit(m, l, acc_d, d), called by wave 0 with d = lane. probe(k)
+// marks phases for profiling: 3 query arrived, 0 first pass staged and
+// scored, 1 passes done, 2 emitted.
+template <int kWaves, typename KvSrc, typename NewSrc, typename WaitQ, typename Emit,
+          typename Probe = NoProbe>
 __device__ void attn_partial_unit(const KvSrc &kcache, const KvSrc &vcache,
                                   const NewSrc &knew, const NewSrc &vnew,
-                                  int new_pos, int g, int group, int kv_dim,
-                                  int begin, int end, AttnLds &sh, WaitQ wait_q,
-                                  Emit emit) {
+                                  int new_pos, int g, int kv_dim, int begin, int end,
+                                  AttnLds &sh, WaitQ wait_q, Emit emit,
+                                  Probe probe = Probe()) {
   const int t = threadIdx.x;
   const int quarter = t & 3;
-  const int jl = t >> 2;
-  const int outs = group * kHeadDim;
-  float acc0 = 0.f, acc1 = 0.f;
-  if (t < kMaxGroup) {
-    sh.m[t] = -INFINITY;
-    sh.l[t] = 0.f;
-  }
-  for (int base = begin; base < end; base += kAttnPass) {
+  const int jl = t >> 2;  // position within the pass
+  const int w = wave_id();
+  const int lane = lane_id();
+  // Waves past kWaves (a caller's helper wave) only join the barriers.
+  static_assert(kWaves >= 1 && kWaves <= kWavesPerBlock, "unit waves");
+  constexpr int kPass = kWaves * kWavePositions;
+  const bool active = w < kWaves;
+  const float scale = rsqrtf(static_cast<float>(kHeadDim));
+  float m = -INFINITY, l = 0.f, acc = 0.f;
+  float4 kr[4], vr[4];
+  auto request = [&](int base) {
     const int j = base + jl;
-    const bool valid = j < end;
-    float4 kr[4], vr[4];
-    const bool is_new = valid && j == new_pos;
-    if (!is_new) {
-      const uint32_t row4 =
-          static_cast<uint32_t>((valid ? j : 0) * kv_dim + g * kHeadDim + quarter * 16) / 4;
+    if (active && j < end && j != new_pos) {
+      const uint32_t row4 = static_cast<uint32_t>(j * kv_dim + g * kHeadDim + quarter * 16) / 4;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         kr[e] = kcache.ld4(row4 + e);
         vr[e] = vcache.ld4(row4 + e);
       }
     }
-    // The cached rows of the first pass are in flight while the query (and
-    // this step's K/V row) are awaited.
-    if (base == begin) wait_q();
-    if (is_new) {
+  };
+  // The first pass's cached rows are requested before the query poll and
+  // are in flight while the query (and this step's K/V row) are awaited.
+  wait_q([&] { request(begin); });
+  probe(3);
+  float4 qv[4];
+  {
+    const float4 *q4 = reinterpret_cast<const float4 *>(sh.qkv);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[e] = q4[quarter * 4 + e];
+  }
+  for (int base = begin; base < end; base += kPass) {
+    const int j = base + jl;
+    const bool in = active && j < end;
+    if (active && j == new_pos) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         kr[e] = knew.ld4((g * kHeadDim + quarter * 16) / 4 + e);
         vr[e] = vnew.ld4((g * kHeadDim + quarter * 16) / 4 + e);
       }
     }
-    __syncthreads();  // previous pass finished reading vs / ps
+    float corr = 1.f;
+    if (active) {
+      const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 *vdst = reinterpret_cast<float4 *>(&sh.vs[jl][quarter * 16]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float *dst = &sh.vs[jl][quarter * 16 + 4 * e];
-      dst[0] = valid ? vr[e].x : 0.f;
-      dst[1] = valid ? vr[e].y : 0.f;
-      dst[2] = valid ? vr[e].z : 0.f;
-      dst[3] = valid ? vr[e].w : 0.f;
-    }
-    for (int hl = 0; hl < group; ++hl) {
-      const float4 *q4 =
-          reinterpret_cast<const float4 *>(sh.qs + hl * kHeadDim + quarter * 16);
+      for (int e = 0; e < 4; ++e) {
+        float4 b = vr[e];
+        if (!in) b = zero;
+        vdst[e] = b;
+      }
       float s = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s = fma4(kr[e], q4[e], s);
-      s += __shfl_xor(s, 1, kWave);
-      s += __shfl_xor(s, 2, kWave);
-      if (quarter == 0)
-        sh.ps[hl][jl] = valid ? s * rsqrtf(static_cast<float>(kHeadDim)) : -INFINITY;
+      for (int e = 0; e < 4; ++e) s = fma4(kr[e], qv[e], s);
+      s = quad_sum(s);
+      const float sv = in ? s * scale : -INFINITY;
+      const float m_new = fmaxf(m, wave_max(sv));
+      // Every position appears in the four lanes of its quad: its first lane
+      // contributes it to the sum.
+      const float p = m_new == -INFINITY ? 0.f : expf(sv - m_new);
+      corr = m_new == -INFINITY ? 1.f : expf(m - m_new);
+      l = fmaf(l, corr, wave_sum(quarter == 0 ? p : 0.f));
+      m = m_new;
+      if (quarter == 0) sh.ps[jl] = p;
     }
-    __syncthreads();
-    // Wave w updates heads w, w+4, ...: lane = position of the pass.
-    for (int hl = wave_id(); hl < group; hl += kWavesPerBlock) {
-      const int lane = lane_id();
-      const float s = sh.ps[hl][lane];
-      float mx = s;
+    if (base + kPass < end) request(base + kPass);
+    __syncthreads();  // vs and ps complete
+    if (base == begin) probe(0);
+    // P.V over this wave's 16 positions, lane = output dim.
+    if (active) {
+      const float4 *p4 = reinterpret_cast<const float4 *>(&sh.ps[w * kWavePositions]);
+      float a = acc * corr;
 #pragma unroll
-      for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-      const float m_old = sh.m[hl];
-      const float m_new = fmaxf(m_old, mx);
-      const float p = expf(s - m_new);
-      float sum = p;
-#pragma unroll
-      for (int o = kWave / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, kWave);
-      sh.ps[hl][lane] = p;
-      if (lane == 0) {
-        const float sc = expf(m_old - m_new);
-        sh.scale[hl] = sc;
-        sh.l[hl] = sh.l[hl] * sc + sum;
-        sh.m[hl] = m_new;
+      for (int i = 0; i < kWavePositions / 4; ++i) {
+        const float4 pp = p4[i];
+        const int r = w * kWavePositions + 4 * i;
+        a = fmaf(pp.x, sh.vs[r][lane], a);
+        a = fmaf(pp.y, sh.vs[r + 1][lane], a);
+        a = fmaf(pp.z, sh.vs[r + 2][lane], a);
+        a = fmaf(pp.w, sh.vs[r + 3][lane], a);
       }
+      acc = a;
     }
-    __syncthreads();
-    // P.V for the pass.
-    if (t < outs) {
-      const int hl = t / kHeadDim, d = t % kHeadDim;
-      float a = 0.f;
-#pragma unroll 8
-      for (int jj = 0; jj < kAttnPass; ++jj) a = fmaf(sh.ps[hl][jj], sh.vs[jj][d], a);
-      acc0 = acc0 * sh.scale[hl] + a;
-    }
-    if (t + kBlock < outs) {
-      const int o = t + kBlock;
-      const int hl = o / kHeadDim, d = o % kHeadDim;
-      float a = 0.f;
-#pragma unroll 8
-      for (int jj = 0; jj < kAttnPass; ++jj) a = fmaf(sh.ps[hl][jj], sh.vs[jj][d], a);
-      acc1 = acc1 * sh.scale[hl] + a;
+    __syncthreads();  // the next pass overwrites vs / ps
+  }
+  probe(1);
+  // Merge the four wave partials.
+  if (active) {
+    sh.wp[w][2 + lane] = acc;
+    if (lane == 0) {
+      sh.wp[w][0] = m;
+      sh.wp[w][1] = l;
     }
   }
   __syncthreads();
-  if (t < outs) emit(t / kHeadDim, sh.m[t / kHeadDim], sh.l[t / kHeadDim], acc0, t % kHeadDim);
-  if (t + kBlock < outs) {
-    const int o = t + kBlock;
-    emit(o / kHeadDim, sh.m[o / kHeadDim], sh.l[o / kHeadDim], acc1, o % kHeadDim);
+  if (w == 0) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) mx = fmaxf(mx, sh.wp[v][0]);
+    float lsum = 0.f, a = 0.f;
+#pragma unroll
+    for (int v = 0; v < kWaves; ++v) {
+      const float mv = sh.wp[v][0];
+      const float f = mv == -INFINITY ? 0.f : expf(mv - mx);
+      lsum = fmaf(f, sh.wp[v][1], lsum);
+      a = fmaf(f, sh.wp[v][2 + lane], a);
+    }
+    emit(mx, lsum, a, lane);
   }
+  probe(2);
 }
 
 // Merge of one head's partials for output dim d; part(c, k) returns element

@@ -14,20 +14,20 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kMaxGroup = 16;          // query heads per KV head
 
 // Split-KV attention geometry (qd_attention.hpp): chunks are multiples of
-// kAttnPass positions, at most kAttnMaxChunks per head; a partial record is
-// (m, l, acc[64]).
+// the pass length (16 positions per wave of the unit: 64 with four waves),
+// at most kAttnMaxChunks per head; a partial record is (m, l, acc[64]).
 constexpr int kAttnPass = 64;
 constexpr int kAttnMaxChunks = 16;
 constexpr int kPartStride = kHeadDim + 2;
 
-__host__ __device__ inline int attn_chunk_len(int length) {
-  const int passes = (length + kAttnPass - 1) / kAttnPass;
+__host__ __device__ inline int attn_chunk_len(int length, int pass = kAttnPass) {
+  const int passes = (length + pass - 1) / pass;
   const int per_chunk = (passes + kAttnMaxChunks - 1) / kAttnMaxChunks;
-  return per_chunk * kAttnPass;
+  return per_chunk * pass;
 }
 
-__host__ __device__ inline int attn_chunks(int length) {
-  const int cl = attn_chunk_len(length);
+__host__ __device__ inline int attn_chunks(int length, int pass = kAttnPass) {
+  const int cl = attn_chunk_len(length, pass);
   return (length + cl - 1) / cl;
 }
 

@@ -15,9 +15,47 @@ namespace dev {
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
 
+// Cross-lane moves inside a 16-lane row (DPP), fused by the compiler into
+// the consuming VALU op.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- lane 7-i of its 8-lane half
+constexpr int kDppMirror = 0x140;     // lane i <- lane 15-i of its row
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float read_lane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Wave64 sum and max with the result in every lane (a wave-uniform value).
+// The whole wave must be active. Rows reduce through DPP (xor 1, xor 2,
+// half-row mirror, row mirror), then the four row results are combined in a
+// fixed order: (r0 + r1) + (r2 + r3).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  return fmaxf(fmaxf(read_lane(v, 0), read_lane(v, 16)), fmaxf(read_lane(v, 32), read_lane(v, 48)));
+}
+
+// Sum over the four lanes of a quad (lanes 4k..4k+3), in every lane of it.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
   return v;
 }
 
@@ -129,11 +167,25 @@ struct PairSlots {
   static constexpr int NJ = (2 * K4 + kWave - 1) / kWave;
 };
 
-// xv[j] = x[c] (optionally * inv * gain[c]) for the column c of slot j.
-template <int K, bool kNorm, typename Src>
-__device__ __forceinline__ void load_pair_operand(
-    const Src &x, float inv, const float *gain,
-    float4 (&xv)[PairSlots<K>::NJ]) {
+// xv[j] = x[c] for the column c of slot j.
+template <int K, typename Src>
+__device__ __forceinline__ void load_pair_operand(const Src &x,
+                                                  float4 (&xv)[PairSlots<K>::NJ]) {
+  constexpr int K4 = PairSlots<K>::K4;
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = 0; j < PairSlots<K>::NJ; ++j) {
+    const int f = j * kWave + lane;
+    const int c = f < K4 ? f : f - K4;
+    xv[j] = f < 2 * K4 ? x.ld4(c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+// RMSNorm gains in the slot layout (gv[j] = gain[c]); loaded ahead of the
+// activation so the normalised operand needs no global load.
+template <int K>
+__device__ __forceinline__ void load_pair_gain(const float *gain,
+                                               float4 (&gv)[PairSlots<K>::NJ]) {
   constexpr int K4 = PairSlots<K>::K4;
   const float4 *g4 = reinterpret_cast<const float4 *>(gain);
   const int lane = lane_id();
@@ -141,18 +193,22 @@ __device__ __forceinline__ void load_pair_operand(
   for (int j = 0; j < PairSlots<K>::NJ; ++j) {
     const int f = j * kWave + lane;
     const int c = f < K4 ? f : f - K4;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (f < 2 * K4) {
-      v = x.ld4(c);
-      if (kNorm) {
-        const float4 g = g4[c];
-        v.x = v.x * inv * g.x;
-        v.y = v.y * inv * g.y;
-        v.z = v.z * inv * g.z;
-        v.w = v.w * inv * g.w;
-      }
-    }
-    xv[j] = v;
+    gv[j] = f < 2 * K4 ? g4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+// xv[j] = x[c] * inv * gain[c]: the RMSNorm output in the slot layout.
+template <int K, typename Src>
+__device__ __forceinline__ void load_pair_operand_norm(
+    const Src &x, float inv, const float4 (&gv)[PairSlots<K>::NJ],
+    float4 (&xv)[PairSlots<K>::NJ]) {
+  load_pair_operand<K>(x, xv);
+#pragma unroll
+  for (int j = 0; j < PairSlots<K>::NJ; ++j) {
+    xv[j].x = xv[j].x * inv * gv[j].x;
+    xv[j].y = xv[j].y * inv * gv[j].y;
+    xv[j].z = xv[j].z * inv * gv[j].z;
+    xv[j].w = xv[j].w * inv * gv[j].w;
   }
 }
 
@@ -217,6 +273,54 @@ __device__ __forceinline__ void dot_pair(const float *a, const float *b,
   pair_dot<K>(w, xv, sa, sb);
 }
 
+// pair_dot with the operand read from LDS (x[0..K)) slot by slot instead of
+// held in registers.
+template <int K>
+__device__ __forceinline__ void pair_dot_lds(const float4 (&w)[PairSlots<K>::NJ],
+                                             const float *x, float &sa, float &sb) {
+  constexpr int K4 = PairSlots<K>::K4;
+  constexpr int NJ = PairSlots<K>::NJ;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const int lane = lane_id();
+  float accA = 0.f, accB = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int f = j * kWave + lane;
+    const int c = f < K4 ? f : f - K4;
+    const float4 xv = f < 2 * K4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (j * kWave + kWave <= K4) {
+      accA = fma4(w[j], xv, accA);
+    } else if (j * kWave >= K4) {
+      accB = fma4(w[j], xv, accB);
+    } else {
+      const float d = fma4(w[j], xv, 0.f);
+      if (f < K4) {
+        accA += d;
+      } else {
+        accB += d;
+      }
+    }
+  }
+  sa = wave_sum(accA);
+  sb = wave_sum(accB);
+}
+
+// y[c] = x[c] * inv * gain[c] for c < N (float4 c4 = thread index, loaded
+// ahead into g), written by the whole workgroup; the caller synchronises.
+template <int N>
+__device__ __forceinline__ void norm_to_lds(const float *x, float inv, float4 g, float *y) {
+  const int c4 = threadIdx.x;
+  if (c4 < N / 4) {
+    const float4 v = reinterpret_cast<const float4 *>(x)[c4];
+    float4 o;
+    o.x = v.x * inv * g.x;
+    o.y = v.y * inv * g.y;
+    o.z = v.z * inv * g.z;
+    o.w = v.w * inv * g.w;
+    reinterpret_cast<float4 *>(y)[c4] = o;
+  }
+}
+
 // Single-row dot for K a multiple of 256 floats: lane l loads float4 slots
 // 64*j + l; xv[j] is the matching operand.
 template <int K>
@@ -248,6 +352,22 @@ __device__ __forceinline__ float row_dot(const float4 (&w)[RowSlots<K>::NJ],
   float acc = 0.f;
 #pragma unroll
   for (int j = 0; j < RowSlots<K>::NJ; ++j) acc = fma4(w[j], xv[j], acc);
+  return wave_sum(acc);
+}
+
+// row_dot with the operand read from LDS.
+template <int K>
+__device__ __forceinline__ float row_dot_lds(const float4 (&w)[RowSlots<K>::NJ],
+                                             const float *x) {
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const int lane = lane_id();
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < RowSlots<K>::NJ; ++j) {
+    // Bounds the operand reads the scheduler hoists (register pressure).
+    if (j % 4 == 0) __builtin_amdgcn_sched_barrier(0);
+    acc = fma4(w[j], x4[j * kWave + lane], acc);
+  }
   return wave_sum(acc);
 }
 

@@ -125,7 +125,7 @@ struct qd_engine {
   uint32_t epoch = 0;                       // last launch epoch (1..4095)
   uint32_t *resident_error = nullptr;       // [1]
   int resident_grid = 0;                    // 0: resident path unavailable
-  const char *resident_off_reason = "";
+  std::string resident_off_reason;
 
   qd::SeqState *h_states = nullptr;  // pinned [max_batch]
   uint32_t *h_tokens = nullptr;      // pinned [capacity]
@@ -281,8 +281,11 @@ struct qd_engine {
   // Launches the resident megakernel (stream ordered; no synchronisation).
   // Each launch gets a fresh epoch so no tag of an earlier launch matches;
   // when the epoch counter wraps the tagged arena is cleared first.
-  void launch_resident(uint32_t seq, uint32_t first_token, uint32_t max_tokens,
-                       uint32_t eos, float *hist, int use_hist, uint64_t *stage_ticks) {
+  // Returns the launch status; the caller decides how to handle a refused
+  // cooperative launch.
+  hipError_t launch_resident(uint32_t seq, uint32_t first_token, uint32_t max_tokens,
+                             uint32_t eos, float *hist, int use_hist, uint64_t *stage_ticks,
+                             uint64_t *trace = nullptr, uint32_t trace_token = 0) {
     epoch = epoch % 4095u + 1u;
     if (epoch == 1u)
       check(hipMemsetAsync(tagged, 0, tagged_elems * 8, stream), "memset");
@@ -301,8 +304,7 @@ struct qd_engine {
     ra.rope_sin = rope_sin;
     ra.k_cache = kv_slice(k_cache, seq, 0);
     ra.v_cache = kv_slice(v_cache, seq, 0);
-    ra.q = take(QD);
-    ra.kvnew = take(2 * KVD);
+    ra.qkv = take(3 * QD);
     ra.part = take(size_t(qd::kAttnMaxChunks) * NQ * qd::kPartStride);
     ra.attn = take(QD);
     ra.h1 = take(H);
@@ -314,6 +316,8 @@ struct qd_engine {
     ra.st = states + seq;
     ra.error = resident_error;
     ra.stage_ticks = stage_ticks;
+    ra.trace = trace;
+    ra.trace_token = trace_token;
     ra.history = use_hist;
     ra.capacity = static_cast<int>(CAP);
     ra.vocab = static_cast<int>(V);
@@ -327,7 +331,18 @@ struct qd_engine {
     ra.eos = eos;
     ra.epoch = epoch << qd::kTagSeqBits;
     check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
-    check(qd::launch_resident(stream, ra, resident_grid), "resident launch");
+    return qd::launch_resident(stream, ra, resident_grid);
+  }
+
+  // A cooperative launch can be refused while another process holds the
+  // device's cooperative-launch resources. The engine then generates with
+  // the stream-ordered kernels (same results) from here on, and says why.
+  bool resident_refused(hipError_t err) {
+    if (err != hipErrorIllegalState && err != hipErrorCooperativeLaunchTooLarge) return false;
+    (void)hipGetLastError();
+    resident_grid = 0;
+    resident_off_reason = std::string("cooperative launch refused: ") + hipGetErrorString(err);
+    return true;
   }
 
   // Resident launches name (token, stage) pairs in kTagSeqBits bits.
@@ -944,14 +959,17 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
       use_hist = 1;
     }
     e->push_state(seq, first_token, qd::kModeGenerate, eos, max_tokens);
-    const bool resident = e->resident_grid > 0 && e->resident_fits(max_tokens);
+    bool resident = e->resident_grid > 0 && e->resident_fits(max_tokens);
+    check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
     if (resident) {
-      check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
-      e->launch_resident(seq, first_token, max_tokens, eos, hist, use_hist, nullptr);
-    } else {
-      check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
-      for (uint32_t t = 0; t < max_tokens; ++t) e->enqueue_step(seq, hist, use_hist, e->tokens_dev);
+      const hipError_t err = e->launch_resident(seq, first_token, max_tokens, eos, hist, use_hist, nullptr);
+      if (err != hipSuccess) {
+        if (!e->resident_refused(err)) check(err, "resident launch");
+        resident = false;
+      }
     }
+    if (!resident)
+      for (uint32_t t = 0; t < max_tokens; ++t) e->enqueue_step(seq, hist, use_hist, e->tokens_dev);
     check(hipEventRecord(e->ev_end, e->stream), "hipEventRecord");
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
                          e->stream), "D2H");
@@ -1054,36 +1072,96 @@ qd_status qd_profile_kernels(qd_engine *e, uint32_t seq, uint32_t first_token, u
   });
 }
 
-qd_status qd_profile_resident(qd_engine *e, uint32_t seq, uint32_t first_token, uint32_t tokens,
-                              double *stage_us, uint32_t capacity, uint32_t *count) {
-  return guard([&] {
-    if (!e || !stage_us || !count) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
-    e->check_seq(seq);
-    e->check_loaded();
-    if (e->resident_grid == 0) fail(QD_ERROR_NOT_SUPPORTED, "resident path disabled: %s", e->resident_off_reason);
-    if (tokens == 0) fail(QD_ERROR_INVALID_ARGUMENT, "tokens must be positive");
-    if (first_token >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", first_token);
-    if (size_t(e->positions[seq]) + tokens > e->CAP)
-      fail(QD_ERROR_INVALID_ARGUMENT, "profiling %u tokens overflows capacity", tokens);
-    if (!e->resident_fits(tokens)) fail(QD_ERROR_INVALID_ARGUMENT, "too many tokens for one resident launch");
-    e->set_device();
-    uint64_t *ticks = e->alloc<uint64_t>(qd::kResidentStages);
-    e->launch_resident(seq, first_token, tokens, UINT32_MAX, e->logits + size_t(seq) * e->V, 0, ticks);
-    uint64_t h[qd::kResidentStages] = {};
-    check(hipMemcpyAsync(h, ticks, sizeof(h), hipMemcpyDeviceToHost, e->stream), "D2H");
-    check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
-                         e->stream), "D2H");
+namespace {
+
+// One profiled resident launch of `tokens` tokens: stage totals of
+// workgroup 0 into ticks_out[kResidentStages] and, when trace_out is set,
+// every workgroup's timeline of token trace_token.
+void profiled_resident_launch(qd_engine *e, uint32_t seq, uint32_t first_token, uint32_t tokens,
+                              uint64_t *ticks_out, uint64_t *trace_out, uint32_t trace_token) {
+  e->check_seq(seq);
+  e->check_loaded();
+  if (e->resident_grid == 0)
+    fail(QD_ERROR_NOT_SUPPORTED, "resident path disabled: %s", e->resident_off_reason.c_str());
+  if (tokens == 0) fail(QD_ERROR_INVALID_ARGUMENT, "tokens must be positive");
+  if (first_token >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", first_token);
+  if (size_t(e->positions[seq]) + tokens > e->CAP)
+    fail(QD_ERROR_INVALID_ARGUMENT, "profiling %u tokens overflows capacity", tokens);
+  if (!e->resident_fits(tokens)) fail(QD_ERROR_INVALID_ARGUMENT, "too many tokens for one resident launch");
+  e->set_device();
+  const size_t trace_elems =
+      trace_out ? size_t(e->resident_grid) * (e->L + 1) * qd::kResidentStages : 0;
+  // Temporary buffers of a diagnostic call, released before returning.
+  uint64_t *ticks = nullptr, *trace = nullptr;
+  check(hipMalloc(&ticks, qd::kResidentStages * sizeof(uint64_t)), "hipMalloc");
+  if (trace_elems && hipMalloc(&trace, trace_elems * sizeof(uint64_t)) != hipSuccess) {
+    (void)hipFree(ticks);
+    fail(QD_ERROR_RUNTIME, "hipMalloc of the trace buffer failed");
+  }
+  auto release = [&] {
+    (void)hipFree(ticks);
+    if (trace) (void)hipFree(trace);
+  };
+  try {
+    check(hipMemsetAsync(ticks, 0, qd::kResidentStages * sizeof(uint64_t), e->stream), "memset");
+    if (trace) check(hipMemsetAsync(trace, 0, trace_elems * sizeof(uint64_t), e->stream), "memset");
+    const hipError_t launched = e->launch_resident(seq, first_token, tokens, UINT32_MAX,
+                                                   e->logits + size_t(seq) * e->V, 0, ticks, trace,
+                                                   trace_token);
+    if (launched != hipSuccess) {
+      if (e->resident_refused(launched))
+        fail(QD_ERROR_NOT_SUPPORTED, "%s", e->resident_off_reason.c_str());
+      check(launched, "resident launch");
+    }
+    check(hipMemcpyAsync(ticks_out, ticks, qd::kResidentStages * sizeof(uint64_t),
+                         hipMemcpyDeviceToHost, e->stream), "D2H");
+    if (trace)
+      check(hipMemcpyAsync(trace_out, trace, trace_elems * sizeof(uint64_t), hipMemcpyDeviceToHost,
+                           e->stream), "D2H");
+    check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState),
+                         hipMemcpyDeviceToHost, e->stream), "D2H");
     e->sync();
-    check(hipFree(ticks), "hipFree");
-    e->allocs.pop_back();
-    e->device_bytes -= 256;
     uint32_t err = 0;
     check(hipMemcpy(&err, e->resident_error, 4, hipMemcpyDeviceToHost), "D2H");
     if (err) fail(QD_ERROR_RUNTIME, "resident kernel barrier wait timed out");
     e->positions[seq] = e->h_states[seq].position;
+  } catch (...) {
+    release();
+    throw;
+  }
+  release();
+}
+
+}  // namespace
+
+qd_status qd_profile_resident(qd_engine *e, uint32_t seq, uint32_t first_token, uint32_t tokens,
+                              double *stage_us, uint32_t capacity, uint32_t *count) {
+  return guard([&] {
+    if (!e || !stage_us || !count) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    uint64_t h[qd::kResidentStages] = {};
+    profiled_resident_launch(e, seq, first_token, tokens, h, nullptr, 0);
     const uint32_t n = std::min<uint32_t>(capacity, qd::kResidentStages);
     for (uint32_t s = 0; s < n; ++s) stage_us[s] = double(h[s]) / 100.0;  // 100 MHz
     *count = n;
+  });
+}
+
+qd_status qd_trace_resident(qd_engine *e, uint32_t seq, uint32_t first_token, uint32_t tokens,
+                            uint32_t trace_token, uint64_t *timeline, size_t capacity,
+                            uint32_t *workgroups, uint32_t *rows, uint32_t *stages) {
+  return guard([&] {
+    if (!e || !timeline || !workgroups || !rows || !stages)
+      fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    if (trace_token >= tokens) fail(QD_ERROR_INVALID_ARGUMENT, "trace_token must be below tokens");
+    const size_t need = size_t(e->resident_grid) * (e->L + 1) * qd::kResidentStages;
+    *workgroups = e->resident_grid;
+    *rows = uint32_t(e->L + 1);
+    *stages = qd::kResidentStages;
+    if (e->resident_grid == 0)
+      fail(QD_ERROR_NOT_SUPPORTED, "resident path disabled: %s", e->resident_off_reason.c_str());
+    if (capacity < need) fail(QD_ERROR_INVALID_ARGUMENT, "timeline needs %zu entries", need);
+    uint64_t h[qd::kResidentStages] = {};
+    profiled_resident_launch(e, seq, first_token, tokens, h, timeline, trace_token);
   });
 }
 

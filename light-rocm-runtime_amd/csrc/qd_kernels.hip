@@ -19,6 +19,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 
 #include "qd_device.hpp"
 #include "qd_attention.hpp"
@@ -55,9 +56,11 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
     float eps, int capacity) {
   __shared__ float red[kWavesPerBlock];
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
+  float4 gv[PairSlots<H>::NJ];
+  load_pair_gain<H>(gain, gv);
   const float inv = block_inv_rms<H>(Plain(hidden), eps, red);
   float4 xv[PairSlots<H>::NJ];
-  load_pair_operand<H, true>(Plain(hidden), inv, gain, xv);
+  load_pair_operand_norm<H>(Plain(hidden), inv, gv, xv);
   const int position = static_cast<int>(st->position);
   const int kv_dim = nkv * kHeadDim;
   const int units = (nq + 2 * nkv) * kRotary;
@@ -98,8 +101,8 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
 }
 
 // Split-KV decode attention partials (qd_attention.hpp): workgroup
-// (chunk, KV head) writes one record (m, l, acc[64]) per query head of the
-// group into part[chunk][head][66].
+// (chunk, query head) writes one record (m, l, acc[64]) into
+// part[head][chunk][66].
 __global__ __launch_bounds__(kBlock) void attn_partial_kernel(
     const float *__restrict__ q, const float *__restrict__ k_cache,
     const float *__restrict__ v_cache, const SeqState *__restrict__ st,
@@ -111,29 +114,29 @@ __global__ __launch_bounds__(kBlock) void attn_partial_kernel(
   const int chunk = blockIdx.x;
   if (chunk >= attn_chunks(length)) return;
   const int chunk_len = attn_chunk_len(length);
-  const int g = blockIdx.y;
-  const int group = nq / nkv;
+  const int h = blockIdx.y;
+  const int g = h / (nq / nkv);
   const int kv_dim = nkv * kHeadDim;
   const int begin = chunk * chunk_len;
   const int end = min(length, begin + chunk_len);
   const Plain kc(k_cache), vc(v_cache);
   const Plain knew(k_cache + static_cast<size_t>(position) * kv_dim);
   const Plain vnew(v_cache + static_cast<size_t>(position) * kv_dim);
-  attn_partial_unit(kc, vc, knew, vnew, position, g, group, kv_dim, begin, end, sh,
-                    [&]() {
-                      for (int e = threadIdx.x; e < group * kHeadDim; e += kBlock)
-                        sh.qs[e] = q[g * group * kHeadDim + e];
-                      __syncthreads();
-                    },
-                    [&](int hl, float m, float l, float acc, int d) {
-                      float *rec =
-                          part + ((g * group + hl) * kAttnMaxChunks + chunk) * kPartStride;
-                      rec[2 + d] = acc;
-                      if (d == 0) {
-                        rec[0] = m;
-                        rec[1] = l;
-                      }
-                    });
+  attn_partial_unit<kWavesPerBlock>(
+      kc, vc, knew, vnew, position, g, kv_dim, begin, end, sh,
+      [&](auto request_rows) {
+        request_rows();
+        if (threadIdx.x < kHeadDim) sh.qkv[threadIdx.x] = q[h * kHeadDim + threadIdx.x];
+        __syncthreads();
+      },
+      [&](float m, float l, float acc, int d) {
+        float *rec = part + (h * kAttnMaxChunks + chunk) * kPartStride;
+        rec[2 + d] = acc;
+        if (d == 0) {
+          rec[0] = m;
+          rec[1] = l;
+        }
+      });
 }
 
 // Merges each head's partials into attn[h*64 + d].
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(kBlock) void oproj_residual_kernel(
     const SeqState *__restrict__ st, float *__restrict__ hidden) {
   if (st->stopped) return;
   float4 xv[PairSlots<QD>::NJ];
-  load_pair_operand<QD, false>(Plain(attn), 1.f, nullptr, xv);
+  load_pair_operand<QD>(Plain(attn), xv);
   constexpr int units = H / 2;
   for (int u = blockIdx.x * kWavesPerBlock + wave_id(); u < units;
        u += gridDim.x * kWavesPerBlock) {
@@ -179,9 +182,11 @@ __global__ __launch_bounds__(kBlock) void gateup_silu_kernel(
     float eps) {
   __shared__ float red[kWavesPerBlock];
   if (st->stopped) return;
+  float4 gv[PairSlots<H>::NJ];
+  load_pair_gain<H>(gain, gv);
   const float inv = block_inv_rms<H>(Plain(hidden), eps, red);
   float4 xv[PairSlots<H>::NJ];
-  load_pair_operand<H, true>(Plain(hidden), inv, gain, xv);
+  load_pair_operand_norm<H>(Plain(hidden), inv, gv, xv);
   for (int r = blockIdx.x * kWavesPerBlock + wave_id(); r < inter;
        r += gridDim.x * kWavesPerBlock) {
     float g, up;
@@ -218,9 +223,11 @@ __global__ __launch_bounds__(kBlock) void lmhead_kernel(
   __shared__ float bv[kWavesPerBlock];
   __shared__ uint32_t bi[kWavesPerBlock];
   if (st->stopped) return;
+  float4 gv[PairSlots<H>::NJ];
+  load_pair_gain<H>(gain, gv);
   const float inv = block_inv_rms<H>(Plain(hidden), eps, red);
   float4 xv[PairSlots<H>::NJ];
-  load_pair_operand<H, true>(Plain(hidden), inv, gain, xv);
+  load_pair_operand_norm<H>(Plain(hidden), inv, gv, xv);
   float *out = logits + (history ? static_cast<size_t>(st->generated) * vocab : 0);
   float best = -INFINITY;
   uint32_t best_i = UINT32_MAX;
@@ -371,7 +378,7 @@ hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
   }
   {
     Scope scope(m, kKAttnPartial);
-    attn_partial_kernel<<<dim3(kAttnMaxChunks, p.nkv), kBlock, 0, s>>>(
+    attn_partial_kernel<<<dim3(kAttnMaxChunks, p.nq), kBlock, 0, s>>>(
         p.q, p.k_cache, p.v_cache, p.st, p.nq, p.nkv, p.part, p.capacity);
   }
   {

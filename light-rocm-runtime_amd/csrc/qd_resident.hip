@@ -19,8 +19,9 @@
 // Stage map per layer (whole output rows per wave, rows spread over every
 // wave of the grid):
 //   A  attention RMSNorm + packed QKV + bias + RoPE -> q, new K/V (+ cache)
-//   B  split-KV GQA attention partials per (KV head, chunk)
-//   C  merge of the partials + O projection + residual -> h1
+//   B  split-KV GQA attention per (query head, chunk); the unit of a head's
+//      last chunk merges the head's partials -> attn
+//   C  O projection + residual -> h1
 //   D  MLP RMSNorm + gate/up + SiLU -> act      (every workgroup takes part)
 //   E  down projection + residual -> hidden
 // Tail: final RMSNorm + LM head + per-workgroup top-1 -> every workgroup
@@ -33,6 +34,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 
 #include "qd_attention.hpp"
 #include "qd_device.hpp"
@@ -70,68 +72,6 @@ struct TagVec {
   }
 };
 
-// Waits until elements [first, first + n) of src (n even, first even) all
-// carry `tag` and copies their values to dst[0..n). Whole workgroup; returns
-// false when the wait gave up (error word raised).
-template <int kMaxPer>
-__device__ bool gather(const TagVec &src, uint32_t first, int n, uint32_t tag,
-                       float *dst, uint32_t *error) {
-  const int pairs = n / 2;
-  const int t = threadIdx.x;
-  uint32_t pending = 0;
-#pragma unroll
-  for (int k = 0; k < kMaxPer; ++k)
-    if (t + k * kBlock < pairs) pending |= 1u << k;
-  for (uint32_t spin = 0;; ++spin) {
-    Pair2 got[kMaxPer];
-#pragma unroll
-    for (int k = 0; k < kMaxPer; ++k)
-      if ((pending >> k) & 1u) got[k] = src.get2(first / 2 + t + k * kBlock);
-#pragma unroll
-    for (int k = 0; k < kMaxPer; ++k) {
-      if (((pending >> k) & 1u) && got[k].t0 == tag && got[k].t1 == tag) {
-        const int p = t + k * kBlock;
-        dst[2 * p] = got[k].v0;
-        dst[2 * p + 1] = got[k].v1;
-        pending &= ~(1u << k);
-      }
-    }
-    if (__syncthreads_and(pending == 0)) return true;
-    if (spin > kSpinLimit) {
-      if (t == 0) atomicOr(error, 1u);
-      return false;
-    }
-  }
-}
-
-// Polls elements [first, first + n) (n even, first even) until every tag
-// matches, copying nothing: a cheap wait on the elements its producers write
-// last, so a large vector is fetched only once it is nearly complete.
-template <int kMaxPer>
-__device__ bool await_tags(const TagVec &src, uint32_t first, int n, uint32_t tag,
-                           uint32_t *error) {
-  const int pairs = n / 2;
-  const int t = threadIdx.x;
-  uint32_t pending = 0;
-#pragma unroll
-  for (int k = 0; k < kMaxPer; ++k)
-    if (t + k * kBlock < pairs) pending |= 1u << k;
-  for (uint32_t spin = 0;; ++spin) {
-    Pair2 got[kMaxPer];
-#pragma unroll
-    for (int k = 0; k < kMaxPer; ++k)
-      if ((pending >> k) & 1u) got[k] = src.get2(first / 2 + t + k * kBlock);
-#pragma unroll
-    for (int k = 0; k < kMaxPer; ++k)
-      if (((pending >> k) & 1u) && got[k].t0 == tag && got[k].t1 == tag) pending &= ~(1u << k);
-    if (__syncthreads_and(pending == 0)) return true;
-    if (spin > kSpinLimit) {
-      if (t == 0) atomicOr(error, 1u);
-      return false;
-    }
-  }
-}
-
 struct Lds {
   const float *p;
   __device__ float ld(uint32_t i) const { return p[i]; }
@@ -148,17 +88,27 @@ struct LdsHeadRow {
   }
 };
 
+// This thread's float4 of an RMSNorm gain vector (threads past N/4 get 0),
+// loaded ahead of the activation it scales.
+template <int N>
+__device__ __forceinline__ float4 load_gain4(const float *gain) {
+  return threadIdx.x < N / 4 ? reinterpret_cast<const float4 *>(gain)[threadIdx.x]
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 // "Row pairs over all waves" loop with a 4-deep weight pipeline: while a
-// unit is reduced, the wave's next three units are already loading.
-// rows(u, a, b) gives unit u's two row pointers; epi(u, sa, sb) consumes the
-// sums (every lane holds them). w0 must hold the weights of unit `first`
-// when first < units.
+// unit is reduced, the wave's next three units are already loading; the
+// operand x (K floats in LDS) is held in registers in the slot layout. rows(u, a, b) gives unit u's two
+// row pointers; epi(u, sa, sb) consumes the sums (every lane holds them).
+// w0 must hold the weights of unit `first` when first < units.
 template <int K, typename Rows, typename Epi>
-__device__ __forceinline__ void run_pairs(int first, int stride, int units,
-                                          const float4 (&xv)[PairSlots<K>::NJ],
+__device__ __forceinline__ void run_pairs(int first, int stride, int units, const float *x,
                                           float4 (&w0)[PairSlots<K>::NJ], Rows rows,
                                           Epi epi) {
   constexpr int NJ = PairSlots<K>::NJ;
+  if (first >= units) return;
+  float4 xv[NJ];
+  load_pair_operand<K>(Lds{x}, xv);
   float4 w1[NJ], w2[NJ], w3[NJ];
   auto load = [&](int u, float4 (&w)[NJ]) {
     if (u < units) {
@@ -189,18 +139,38 @@ __device__ __forceinline__ void run_pairs(int first, int stride, int units,
   }
 }
 
+// Profiling clock (profiled kernel variant only), kept by thread 0 of each
+// workgroup in LDS: per-stage totals (published for workgroup 0), and
+// optionally a timeline of every workgroup for one token
+// (row[layer * kResidentStages + stage] = time the stage ended; the tail
+// stages use layer = layers).
 template <bool kProfile>
 struct StageClock {
-  uint64_t ticks[kResidentStages] = {};
+  uint64_t *ticks = nullptr;  // LDS [kResidentStages]
   uint64_t prev = 0;
-  __device__ void start() {
-    if (kProfile) prev = wall_clock64();
+  uint64_t *row = nullptr;
+  bool tracing = false;
+  int layer = 0;
+  __device__ void start(uint64_t *lds_ticks, uint64_t *trace, int layers) {
+    if (kProfile && threadIdx.x == 0) {
+      ticks = lds_ticks;
+      for (int s = 0; s < kResidentStages; ++s) ticks[s] = 0;
+      prev = wall_clock64();
+      if (trace) row = trace + static_cast<size_t>(blockIdx.x) * (layers + 1) * kResidentStages;
+    }
   }
   __device__ void lap(int stage) {
-    if (kProfile) {
+    if (kProfile && threadIdx.x == 0) {
       const uint64_t now = wall_clock64();
       ticks[stage] += now - prev;
       prev = now;
+      if (tracing) row[layer * kResidentStages + stage] = now;
+    }
+  }
+  __device__ void at(uint32_t token, uint32_t trace_token, int l) {
+    if (kProfile) {
+      tracing = row != nullptr && token == trace_token;
+      layer = l;
     }
   }
   __device__ void publish(uint64_t *out) const {
@@ -212,14 +182,60 @@ struct StageClock {
 struct Shared {
   float xs[4864];                              // staged activation vector
   float hs[1024];                              // residual vector
-  float parts[kAttnMaxChunks * kPartStride];   // one head's partials (mergers)
+  float hid[1024];                             // the layer's input hidden vector
+  float xn[1024];                              // RMSNorm output (GEMV operand)
+  float parts[kAttnMaxChunks * kPartStride];   // a head's partials at its owner unit
   AttnLds attn;
-  float kvn[2 * kHeadDim];                     // this step's K/V row of one head
   float red[kWavesPerBlock];
   float bv[kWavesPerBlock];
   uint32_t bi[kWavesPerBlock];
   float top[2 * kMaxResidentGrid];
+  uint64_t ticks[kResidentStages];             // profiling totals (thread 0)
 };
+
+// Whole-workgroup gather: waits until elements [first, first + n) of src
+// (n even, first even) all carry `tag` and copies their values to dst[0..n).
+// ahead() runs first: the stage's weight prefetch, which then streams while
+// the inputs are awaited. Returns false when the wait gave up (error word
+// raised).
+template <int kMaxPer, typename Ahead>
+__device__ bool gather(const TagVec &src, uint32_t first, int n, uint32_t tag, float *dst,
+                       uint32_t *error, Ahead ahead) {
+  const int pairs = n / 2;
+  const int t = threadIdx.x;
+  uint32_t pending = 0;
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k)
+    if (t + k * kBlock < pairs) pending |= 1u << k;
+  ahead();
+  __builtin_amdgcn_sched_barrier(0);
+  for (uint32_t spin = 0;; ++spin) {
+    Pair2 got[kMaxPer];
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k)
+      if ((pending >> k) & 1u) got[k] = src.get2(first / 2 + t + k * kBlock);
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+      if (((pending >> k) & 1u) && got[k].t0 == tag && got[k].t1 == tag) {
+        const int p = t + k * kBlock;
+        dst[2 * p] = got[k].v0;
+        dst[2 * p + 1] = got[k].v1;
+        pending &= ~(1u << k);
+      }
+    }
+    if (__syncthreads_and(pending == 0)) return true;
+    if (spin > kSpinLimit) {
+      if (t == 0) atomicOr(error, 1u);
+      return false;
+    }
+  }
+}
+
+template <int kMaxPer>
+__device__ bool gather(const TagVec &src, uint32_t first, int n, uint32_t tag, float *dst,
+                       uint32_t *error) {
+  return gather<kMaxPer>(src, first, n, tag, dst, error, [] {});
+}
 
 template <int H, int I, int QD, bool kProfile>
 __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs a) {
@@ -230,9 +246,12 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
   const int gw = blockIdx.x * kWavesPerBlock + wave_id();
   const int nwaves = gridDim.x * kWavesPerBlock;
   const int lane = lane_id();
+  const int wgw = static_cast<int>(blockIdx.x) * kWavesPerBlock;  // first wave of the WG
   const uint32_t per_token = 6u * a.layers + 1u;
-  const TagVec tq(a.q, QD);
-  const TagVec tkv(a.kvnew, 2 * kv_dim);
+  // Per query head h: its query, then this step's K and V rows of its KV
+  // head (repeated for every head of the group).
+  constexpr int qkv_block = 3 * kHeadDim;
+  const TagVec tqkv(a.qkv, a.nq * qkv_block);
   const TagVec tpart(a.part, kAttnMaxChunks * a.nq * kPartStride);
   const TagVec tattn(a.attn, QD);
   const TagVec th1(a.h1, H);
@@ -240,13 +259,24 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
   const TagVec thid(a.hidden, H);
   const TagVec ttop(a.top, 2 * gridDim.x);
   auto tag = [&](uint32_t seq) { return a.epoch | (seq + 1u); };
+  // The layer's input hidden vector into sh.hid (embedding row at layer 0),
+  // with the caller's prefetch queued behind the first poll.
+  auto fetch_hidden = [&](int l, uint32_t tag_prev, const float *embed_row, auto ahead) {
+    if (l == 0) {
+      ahead();
+      for (int c = threadIdx.x; c < H; c += kBlock) sh.hid[c] = embed_row[c];
+      __syncthreads();
+      return true;
+    }
+    return gather<(H / 2 + kBlock - 1) / kBlock>(thid, 0, H, tag_prev, sh.hid, a.error, ahead);
+  };
 
   uint32_t token = a.first_token;
   uint32_t generated = 0;
   uint32_t stop_reason = 0;
   float top = 0.f;
   StageClock<kProfile> clock;
-  clock.start();
+  clock.start(sh.ticks, a.trace, a.layers);
 
   for (uint32_t t = 0; t < a.max_tokens; ++t) {
     const int position = static_cast<int>(a.start_position + t);
@@ -258,6 +288,7 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
     const uint32_t s0 = t * per_token;
 
     for (int l = 0; l < a.layers; ++l) {
+      clock.at(t, a.trace_token, l);
       const LayerPtrs w = a.layer_ptrs[l];
       float *kc = a.k_cache + static_cast<size_t>(l) * a.capacity * kv_dim;
       float *vc = a.v_cache + static_cast<size_t>(l) * a.capacity * kv_dim;
@@ -268,11 +299,12 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
       const uint32_t tag_act = tag(s0 + 6 * l + 4);
       const uint32_t tag_hid = tag(s0 + 6 * l + 5);
       const uint32_t tag_prev = l ? tag(s0 + 6 * (l - 1) + 5) : 0u;
+      bool have_hidden = false;
 
       // ---- A: RMSNorm + QKV + bias + RoPE ------------------------------------
       {
         const int units = (a.nq + 2 * a.nkv) * kRotary;
-        if (static_cast<int>(blockIdx.x) * kWavesPerBlock < units) {
+        if (wgw < units) {
           auto rows = [&](int u, const float *&ra, const float *&rb) {
             const int row = (u / kRotary) * kHeadDim + u % kRotary;
             ra = w.wqkv + static_cast<size_t>(row) * H;
@@ -290,141 +322,156 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
           };
           float4 w0[PairSlots<H>::NJ];
           float4 c0 = make_float4(0.f, 0.f, 1.f, 0.f);
-          if (gw < units) {
-            const float *ra, *rb;
-            rows(gw, ra, rb);
-            load_pair_weights<H>(ra, rb, w0);
-            consts(gw, c0);
-          }
-          if (l == 0) {
-            for (int c = threadIdx.x; c < H; c += kBlock) sh.xs[c] = embed_row[c];
-            __syncthreads();
-          } else if (!gather<2>(thid, 0, H, tag_prev, sh.xs, a.error)) {
+          float4 g;
+          if (!fetch_hidden(l, tag_prev, embed_row, [&] {
+                if (gw < units) {
+                  const float *ra, *rb;
+                  rows(gw, ra, rb);
+                  load_pair_weights<H>(ra, rb, w0);
+                  consts(gw, c0);
+                }
+                g = load_gain4<H>(w.attn_norm);
+              }))
             return;
-          }
+          have_hidden = true;
           clock.lap(0);
-          const float inv = block_inv_rms<H>(Lds{sh.xs}, a.eps, sh.red);
-          float4 xv[PairSlots<H>::NJ];
-          load_pair_operand<H, true>(Lds{sh.xs}, inv, w.attn_norm, xv);
-          const Coherent kcache(kc, static_cast<uint32_t>(a.capacity) * kv_dim * 4u);
-          const Coherent vcache(vc, static_cast<uint32_t>(a.capacity) * kv_dim * 4u);
-          run_pairs<H>(gw, nwaves, units, xv, w0, rows, [&](int u, float sa, float sb) {
-            if (lane != 0) return;
-            float4 cv = c0;
-            if (u != gw) consts(u, cv);
-            const int head = u / kRotary, i = u % kRotary;
-            const int ra = head * kHeadDim + i, rb = ra + kRotary;
-            const float x0 = sa + cv.x;
-            const float x1 = sb + cv.y;
-            if (head < a.nq + a.nkv) {
-              const float first = x0 * cv.z - x1 * cv.w;
-              const float second = x1 * cv.z + x0 * cv.w;
-              if (head < a.nq) {
-                tq.put(ra, first, tag_q);
-                tq.put(rb, second, tag_q);
+          const float inv = block_inv_rms<H>(Lds{sh.hid}, a.eps, sh.red);
+          norm_to_lds<H>(sh.hid, inv, g, sh.xn);
+          __syncthreads();
+          {
+            const Coherent kcache(kc, static_cast<uint32_t>(a.capacity) * kv_dim * 4u);
+            const Coherent vcache(vc, static_cast<uint32_t>(a.capacity) * kv_dim * 4u);
+            run_pairs<H>(gw, nwaves, units, sh.xn, w0, rows, [&](int u, float sa, float sb) {
+              if (lane != 0) return;
+              float4 cv = c0;
+              if (u != gw) consts(u, cv);
+              const int head = u / kRotary, i = u % kRotary;
+              const float x0 = sa + cv.x;
+              const float x1 = sb + cv.y;
+              if (head < a.nq + a.nkv) {
+                const float first = x0 * cv.z - x1 * cv.w;
+                const float second = x1 * cv.z + x0 * cv.w;
+                if (head < a.nq) {
+                  tqkv.put(head * qkv_block + i, first, tag_q);
+                  tqkv.put(head * qkv_block + i + kRotary, second, tag_q);
+                } else {
+                  const int kvh = head - a.nq;
+                  const int o = kvh * kHeadDim + i;
+                  for (int h = kvh * group; h < (kvh + 1) * group; ++h) {
+                    tqkv.put(h * qkv_block + kHeadDim + i, first, tag_q);
+                    tqkv.put(h * qkv_block + kHeadDim + i + kRotary, second, tag_q);
+                  }
+                  kcache.st(position * kv_dim + o, first);
+                  kcache.st(position * kv_dim + o + kRotary, second);
+                }
               } else {
-                const int o = (head - a.nq) * kHeadDim + i;
-                tkv.put(o, first, tag_q);
-                tkv.put(o + kRotary, second, tag_q);
-                kcache.st(position * kv_dim + o, first);
-                kcache.st(position * kv_dim + o + kRotary, second);
+                const int kvh = head - a.nq - a.nkv;
+                const int o = kvh * kHeadDim + i;
+                for (int h = kvh * group; h < (kvh + 1) * group; ++h) {
+                  tqkv.put(h * qkv_block + 2 * kHeadDim + i, x0, tag_q);
+                  tqkv.put(h * qkv_block + 2 * kHeadDim + i + kRotary, x1, tag_q);
+                }
+                vcache.st(position * kv_dim + o, x0);
+                vcache.st(position * kv_dim + o + kRotary, x1);
               }
-            } else {
-              const int o = (head - a.nq - a.nkv) * kHeadDim + i;
-              tkv.put(kv_dim + o, x0, tag_q);
-              tkv.put(kv_dim + o + kRotary, x1, tag_q);
-              vcache.st(position * kv_dim + o, x0);
-              vcache.st(position * kv_dim + o + kRotary, x1);
-            }
-          });
+            });
+          }
         }
       }
       clock.lap(1);
 
-      // ---- B: split-KV attention partials -------------------------------------
+      // ---- B: split-KV attention, one (query head, chunk) per unit -----------
       {
-        const int units = a.nkv * chunks;
+        const int units = a.nq * chunks;
         const Coherent kcache(kc, static_cast<uint32_t>(a.capacity) * kv_dim * 4u);
         const Coherent vcache(vc, static_cast<uint32_t>(a.capacity) * kv_dim * 4u);
         for (int u = blockIdx.x; u < units; u += gridDim.x) {
-          const int g = u / chunks, chunk = u % chunks;
+          const int h = u / chunks, chunk = u % chunks;
+          const int g = h / group;
           const int begin = chunk * chunk_len;
           const int end = min(length, begin + chunk_len);
           const bool has_new = position >= begin && position < end;
           bool ok = true;
-          const LdsHeadRow knew{sh.kvn, g};
-          const LdsHeadRow vnew{sh.kvn + kHeadDim, g};
-          attn_partial_unit(
-              kcache, vcache, knew, vnew, has_new ? position : -1, g, group, kv_dim, begin, end,
+          // The unit holding this step's position also takes its K/V row,
+          // which follows the query in the same tagged block.
+          const LdsHeadRow knew{sh.attn.qkv + kHeadDim, g};
+          const LdsHeadRow vnew{sh.attn.qkv + 2 * kHeadDim, g};
+          attn_partial_unit<kWavesPerBlock>(
+              kcache, vcache, knew, vnew, has_new ? position : -1, g, kv_dim, begin, end,
               sh.attn,
-              [&]() {
-                ok = gather<2>(tq, g * group * kHeadDim, group * kHeadDim, tag_q, sh.attn.qs,
-                               a.error);
-                if (ok && has_new)
-                  ok = gather<1>(tkv, g * kHeadDim, kHeadDim, tag_q, sh.kvn, a.error) &&
-                       gather<1>(tkv, kv_dim + g * kHeadDim, kHeadDim, tag_q, sh.kvn + kHeadDim,
-                                 a.error);
+              [&](auto request_rows) {
+                ok = gather<1>(tqkv, h * qkv_block, has_new ? qkv_block : kHeadDim, tag_q,
+                               sh.attn.qkv, a.error, request_rows);
                 clock.lap(2);
               },
-              [&](int hl, float m, float lsum, float acc, int d) {
-                const uint32_t rec = ((g * group + hl) * kAttnMaxChunks + chunk) * kPartStride;
-                tpart.put(rec + 2 + d, acc, tag_p);
-                if (d == 0) {
-                  tpart.put(rec, m, tag_p);
-                  tpart.put(rec + 1, lsum, tag_p);
+              [&](float m, float lsum, float acc, int d) {
+                if (has_new) {
+                  // The owner keeps its own record in LDS for the merge.
+                  float *rec = sh.parts + chunk * kPartStride;
+                  rec[2 + d] = acc;
+                  if (d == 0) {
+                    rec[0] = m;
+                    rec[1] = lsum;
+                  }
+                } else {
+                  const uint32_t rec = (h * kAttnMaxChunks + chunk) * kPartStride;
+                  tpart.put(rec + 2 + d, acc, tag_p);
+                  if (d == 0) {
+                    tpart.put(rec, m, tag_p);
+                    tpart.put(rec + 1, lsum, tag_p);
+                  }
                 }
+              },
+              [&](int phase) {
+                if (phase < 3) clock.lap(kResidentStages - 3 + phase);
               });
           if (!ok) return;
+          if (has_new) {
+            // Owner of the head (its last chunk, which waits longest for this
+            // step's K/V row): merge the other chunks' partials with its own.
+            if (!gather<(kAttnMaxChunks * kPartStride / 2 + kBlock - 1) / kBlock>(
+                    tpart, h * kAttnMaxChunks * kPartStride, chunk * kPartStride, tag_p, sh.parts,
+                    a.error))
+              return;
+            if (threadIdx.x < kHeadDim) {
+              const int d = threadIdx.x;
+              tattn.put(h * kHeadDim + d,
+                        attn_merge([&](int c, int k) { return sh.parts[c * kPartStride + k]; },
+                                   chunks, d),
+                        tag_m);
+            }
+          }
           __syncthreads();
         }
       }
       clock.lap(3);
 
-      // ---- M: merge of each query head's partials (one workgroup per head) ----
-      {
-        const int h = static_cast<int>(blockIdx.x) - (static_cast<int>(gridDim.x) - a.nq);
-        if (h >= 0) {
-          if (!gather<3>(tpart, h * kAttnMaxChunks * kPartStride, chunks * kPartStride, tag_p,
-                         sh.parts, a.error))
-            return;
-          if (threadIdx.x < kHeadDim) {
-            const int d = threadIdx.x;
-            tattn.put(h * kHeadDim + d,
-                      attn_merge([&](int c, int k) { return sh.parts[c * kPartStride + k]; },
-                                 chunks, d),
-                      tag_m);
-          }
-        }
-      }
-
       // ---- C: O projection + residual -----------------------------------------
       {
         constexpr int units = H / 2;
-        if (static_cast<int>(blockIdx.x) * kWavesPerBlock < units) {
+        if (wgw < units) {
           auto rows = [&](int u, const float *&ra, const float *&rb) {
             ra = w.wo + static_cast<size_t>(2 * u) * QD;
             rb = ra + QD;
           };
           float4 w0[PairSlots<QD>::NJ];
-          if (gw < units) {
-            const float *ra, *rb;
-            rows(gw, ra, rb);
-            load_pair_weights<QD>(ra, rb, w0);
-          }
-          if (l == 0) {
-            for (int c = threadIdx.x; c < H; c += kBlock) sh.hs[c] = embed_row[c];
-          } else if (!gather<2>(thid, 0, H, tag_prev, sh.hs, a.error)) {
+          if (!have_hidden && !fetch_hidden(l, tag_prev, embed_row, [] {})) return;
+          if (!gather<(QD / 2 + kBlock - 1) / kBlock>(tattn, 0, QD, tag_m, sh.xs, a.error, [&] {
+                if (gw < units) {
+                  const float *ra, *rb;
+                  rows(gw, ra, rb);
+                  load_pair_weights<QD>(ra, rb, w0);
+                }
+              }))
             return;
-          }
-          if (!gather<2>(tattn, 0, QD, tag_m, sh.xs, a.error)) return;
           clock.lap(4);
-          float4 xv[PairSlots<QD>::NJ];
-          load_pair_operand<QD, false>(Lds{sh.xs}, 1.f, nullptr, xv);
-          run_pairs<QD>(gw, nwaves, units, xv, w0, rows, [&](int u, float sa, float sb) {
-            if (lane != 0) return;
-            th1.put(2 * u, sh.hs[2 * u] + sa, tag_h1);
-            th1.put(2 * u + 1, sh.hs[2 * u + 1] + sb, tag_h1);
-          });
+          {
+            run_pairs<QD>(gw, nwaves, units, sh.xs, w0, rows, [&](int u, float sa, float sb) {
+              if (lane != 0) return;
+              th1.put(2 * u, sh.hid[2 * u] + sa, tag_h1);
+              th1.put(2 * u + 1, sh.hid[2 * u + 1] + sb, tag_h1);
+            });
+          }
         }
       }
       clock.lap(5);
@@ -436,36 +483,41 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
           rb = w.wu + static_cast<size_t>(u) * H;
         };
         float4 w0[PairSlots<H>::NJ];
-        if (gw < I) {
-          const float *ra, *rb;
-          rows(gw, ra, rb);
-          load_pair_weights<H>(ra, rb, w0);
-        }
-        if (!gather<2>(th1, 0, H, tag_h1, sh.hs, a.error)) return;
+        float4 g;
+        if (!gather<(H / 2 + kBlock - 1) / kBlock>(th1, 0, H, tag_h1, sh.hs, a.error, [&] {
+              if (gw < I) {
+                const float *ra, *rb;
+                rows(gw, ra, rb);
+                load_pair_weights<H>(ra, rb, w0);
+              }
+              g = load_gain4<H>(w.mlp_norm);
+            }))
+          return;
         clock.lap(6);
         const float inv = block_inv_rms<H>(Lds{sh.hs}, a.eps, sh.red);
-        float4 xv[PairSlots<H>::NJ];
-        load_pair_operand<H, true>(Lds{sh.hs}, inv, w.mlp_norm, xv);
-        run_pairs<H>(gw, nwaves, I, xv, w0, rows, [&](int u, float g, float up) {
-          if (lane == 0) tact.put(u, g / (1.f + expf(-g)) * up, tag_act);
-        });
+        norm_to_lds<H>(sh.hs, inv, g, sh.xn);
+        __syncthreads();
+        {
+          run_pairs<H>(gw, nwaves, I, sh.xn, w0, rows, [&](int u, float gt, float up) {
+            if (lane == 0) tact.put(u, gt / (1.f + expf(-gt)) * up, tag_act);
+          });
+        }
       }
       clock.lap(7);
 
       // ---- E: down projection + residual --------------------------------------
       {
-        if (static_cast<int>(blockIdx.x) * kWavesPerBlock < H) {
+        if (wgw < H) {
+          // A wave's first two rows are requested before the wait.
           float4 wrow[RowSlots<I>::NJ];
-          if (gw < H) load_row_weights<I>(w.wd + static_cast<size_t>(gw) * I, wrow);
-          const int probe = min(I, nwaves);
-          if (!await_tags<4>(tact, I - probe, probe, tag_act, a.error)) return;
-          if (!gather<10>(tact, 0, I, tag_act, sh.xs, a.error)) return;
+          if (!gather<(I / 2 + kBlock - 1) / kBlock>(tact, 0, I, tag_act, sh.xs, a.error, [&] {
+                if (gw < H) load_row_weights<I>(w.wd + static_cast<size_t>(gw) * I, wrow);
+              }))
+            return;
           clock.lap(8);
-          float4 xv[RowSlots<I>::NJ];
-          load_row_operand<I>(Lds{sh.xs}, xv);
           for (int r = gw; r < H; r += nwaves) {
             if (r != gw) load_row_weights<I>(w.wd + static_cast<size_t>(r) * I, wrow);
-            const float s = row_dot<I>(wrow, xv);
+            const float s = row_dot_lds<I>(wrow, sh.xs);
             if (lane == 0) thid.put(r, sh.hs[r] + s, tag_hid);
           }
         }
@@ -474,6 +526,7 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
     }
 
     // ---- LM head + top-1 ---------------------------------------------------------
+    clock.at(t, a.trace_token, a.layers);
     const uint32_t tag_last = tag(s0 + 6 * (a.layers - 1) + 5);
     const uint32_t tag_top = tag(s0 + 6 * a.layers);
     {
@@ -483,35 +536,41 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
         rb = 2 * u + 1 < a.vocab ? ra + H : ra;
       };
       float4 w0[PairSlots<H>::NJ];
-      if (gw < units) {
-        const float *ra, *rb;
-        rows(gw, ra, rb);
-        load_pair_weights<H>(ra, rb, w0);
-      }
-      if (!gather<2>(thid, 0, H, tag_last, sh.xs, a.error)) return;
+      float4 g;
+      if (!gather<(H / 2 + kBlock - 1) / kBlock>(thid, 0, H, tag_last, sh.xs, a.error, [&] {
+            if (gw < units) {
+              const float *ra, *rb;
+              rows(gw, ra, rb);
+              load_pair_weights<H>(ra, rb, w0);
+            }
+            g = load_gain4<H>(a.final_norm);
+          }))
+        return;
       clock.lap(10);
       const float inv = block_inv_rms<H>(Lds{sh.xs}, a.eps, sh.red);
-      float4 xv[PairSlots<H>::NJ];
-      load_pair_operand<H, true>(Lds{sh.xs}, inv, a.final_norm, xv);
-      float *logits = a.logits + (a.history ? static_cast<size_t>(t) * a.vocab : 0);
+      norm_to_lds<H>(sh.xs, inv, g, sh.xn);
+      __syncthreads();
       float best = -INFINITY;
       uint32_t best_i = UINT32_MAX;
-      run_pairs<H>(gw, nwaves, units, xv, w0, rows, [&](int u, float sa, float sb) {
-        const int r0 = 2 * u;
-        const bool has1 = r0 + 1 < a.vocab;
-        if (lane == 0) {
-          logits[r0] = sa;
-          if (has1) logits[r0 + 1] = sb;
-        }
-        if (better(sa, r0, best, best_i)) {
-          best = sa;
-          best_i = r0;
-        }
-        if (has1 && better(sb, r0 + 1, best, best_i)) {
-          best = sb;
-          best_i = r0 + 1;
-        }
-      });
+      {
+        float *logits = a.logits + (a.history ? static_cast<size_t>(t) * a.vocab : 0);
+        run_pairs<H>(gw, nwaves, units, sh.xn, w0, rows, [&](int u, float sa, float sb) {
+          const int r0 = 2 * u;
+          const bool has1 = r0 + 1 < a.vocab;
+          if (lane == 0) {
+            logits[r0] = sa;
+            if (has1) logits[r0 + 1] = sb;
+          }
+          if (better(sa, r0, best, best_i)) {
+            best = sa;
+            best_i = r0;
+          }
+          if (has1 && better(sb, r0 + 1, best, best_i)) {
+            best = sb;
+            best_i = r0 + 1;
+          }
+        });
+      }
       if (lane == 0) {
         sh.bv[wave_id()] = best;
         sh.bi[wave_id()] = best_i;
@@ -532,11 +591,13 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
 
     // ---- argmax over the workgroup partials (every workgroup) ----------------
     {
-      if (!gather<4>(ttop, 0, 2 * gridDim.x, tag_top, sh.top, a.error)) return;
+      if (!gather<(kMaxResidentGrid + kBlock - 1) / kBlock>(ttop, 0, 2 * gridDim.x, tag_top,
+                                                            sh.top, a.error))
+        return;
       clock.lap(12);
       float best = -INFINITY;
       uint32_t best_i = UINT32_MAX;
-      for (uint32_t p = threadIdx.x; p < gridDim.x; p += kBlock) {
+      for (uint32_t p = threadIdx.x; p < gridDim.x; p += blockDim.x) {
         const float v = sh.top[2 * p];
         const uint32_t i = __builtin_bit_cast(uint32_t, sh.top[2 * p + 1]);
         if (better(v, i, best, best_i)) {
@@ -603,7 +664,7 @@ __global__ __launch_bounds__(kBlock, 1) void resident_decode_kernel(ResidentArgs
 hipError_t launch_resident(hipStream_t s, const ResidentArgs &args, int grid) {
   void *params[] = {const_cast<ResidentArgs *>(&args)};
   const void *fn =
-      args.stage_ticks
+      (args.stage_ticks || args.trace)
           ? reinterpret_cast<const void *>(&resident_decode_kernel<896, 4864, 896, true>)
           : reinterpret_cast<const void *>(&resident_decode_kernel<896, 4864, 896, false>);
   return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kBlock), params, 0, s);

@@ -11,8 +11,9 @@ namespace qd {
 
 // Profiled intervals of workgroup 0, each stage split into waiting for its
 // input and working: QKV, attention, O-proj (with merge), gate/up, down,
-// LM head, argmax -> 14 entries (wait, work) per stage.
-constexpr int kResidentStages = 14;
+// LM head, argmax -> 14 entries (wait, work), then the attention work's
+// sub-phases (K/V staging, math, emit) -> 17 entries.
+constexpr int kResidentStages = 17;
 // Largest resident grid (the argmax partials are staged in LDS).
 constexpr int kMaxResidentGrid = 1024;
 
@@ -27,8 +28,8 @@ struct ResidentArgs {
   const float *rope_sin;
   float *k_cache;               // slot base [layers][capacity][kv_heads*64]
   float *v_cache;
-  void *q;                      // tagged [heads*64]
-  void *kvnew;                  // tagged [2 * kv_heads*64]: this step's K | V
+  void *qkv;                    // tagged [heads][3 * 64]: per query head, its query,
+                                //   then this step's K and V rows of its KV head
   void *part;                   // tagged [heads][kAttnMaxChunks][66]
   void *attn;                   // tagged [heads*64] merged attention
   void *h1;                     // tagged [hidden]
@@ -40,6 +41,9 @@ struct ResidentArgs {
   SeqState *st;
   uint32_t *error;              // zero at launch; nonzero: a wait gave up
   uint64_t *stage_ticks;        // nullptr, or [kResidentStages] 100 MHz ticks
+  uint64_t *trace;              // nullptr, or [grid][layers + 1][kResidentStages]
+                                //   100 MHz timestamps of token trace_token
+  uint32_t trace_token;
   int history;
   int capacity;
   int vocab;
@@ -58,8 +62,9 @@ struct ResidentArgs {
 constexpr int kTagSeqBits = 20;
 // Elements of the tagged arena for a given grid.
 inline size_t resident_tagged_elems(int hidden, int heads, int kv_heads, int inter, int grid) {
-  return 2 * size_t(heads) * 64 + 2 * size_t(kv_heads) * 64 + 16 * size_t(heads) * 66 +
-         3 * size_t(hidden) + inter + 2 * size_t(grid);
+  (void)kv_heads;
+  return 4 * size_t(heads) * 64 + 16 * size_t(heads) * 66 + 3 * size_t(hidden) + inter +
+         2 * size_t(grid);
 }
 
 hipError_t launch_resident(hipStream_t s, const ResidentArgs &args, int grid);

@@ -94,6 +94,8 @@ _SIGNATURES = {
                                      C.c_uint32, _U]),
     "qd_profile_resident": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double),
                                       C.c_uint32, _U]),
+    "qd_trace_resident": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                    C.POINTER(C.c_uint64), C.c_size_t, _U, _U, _U]),
     "qd_sync": (C.c_int, [_E]),
     "qd_bundle_write_layer": (C.c_int, [C.c_char_p, C.c_char_p, _U, C.c_float, _F]),
     "qd_bundle_read_layer": (C.c_int, [C.c_char_p, _U, _F, _F, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -300,14 +302,30 @@ class Engine:
         return out
 
     RESIDENT_STAGES = tuple(f"{s}.{k}" for s in ("qkv", "attention", "oproj", "gateup", "down",
-                                                  "lmhead", "argmax") for k in ("wait", "work"))
+                                                  "lmhead", "argmax") for k in ("wait", "work")) + \
+        ("attention.stage", "attention.math", "attention.emit")
 
     def profile_resident(self, seq: int, first_token: int, tokens: int) -> dict:
         """Per-stage microseconds (summed over `tokens`) of the resident kernel."""
-        out = (C.c_double * 16)()
+        out = (C.c_double * 32)()
         n = C.c_uint32()
-        _check(lib().qd_profile_resident(self.handle, seq, first_token, tokens, out, 16, C.byref(n)))
+        _check(lib().qd_profile_resident(self.handle, seq, first_token, tokens, out, 32, C.byref(n)))
         return {name: out[i] for i, name in enumerate(self.RESIDENT_STAGES[:n.value])}
+
+    def trace_resident(self, seq: int, first_token: int, tokens: int, trace_token: int) -> np.ndarray:
+        """Timeline [workgroup, layer row, stage] (microseconds from the earliest
+        stamp) of token `trace_token` in a profiled resident launch; 0 = no stamp."""
+        g, r, st = C.c_uint32(), C.c_uint32(), C.c_uint32()
+        cap = max(self.resident_grid(), 1) * (self.config.layers + 1) * len(self.RESIDENT_STAGES)
+        buf = np.zeros(cap, np.uint64)
+        _check(lib().qd_trace_resident(self.handle, seq, first_token, tokens, trace_token,
+                                       buf.ctypes.data_as(C.POINTER(C.c_uint64)), cap,
+                                       C.byref(g), C.byref(r), C.byref(st)))
+        t = buf[: g.value * r.value * st.value].reshape(g.value, r.value, st.value).astype(np.float64)
+        stamped = t > 0
+        if stamped.any():
+            t[stamped] = (t[stamped] - t[stamped].min()) / 100.0
+        return t
 
     def last_timing(self) -> Timing:
         t = Timing()

@@ -80,7 +80,7 @@ def test_stdout_contract_matches_engine(resident):
 
     with qd.Engine(layers=2, vocab=4096, capacity=64, max_batch=1) as eng:
         eng.load_synthetic(3)
-        tok, logits, _ = eng.prefill(0, np.array(prompt, np.uint32), want_logits=True)
+        tok, _, logits = eng.prefill(0, np.array(prompt, np.uint32), want_logits=True)
         want = [tok]
         for _ in range(n - 1):
             tok, _, _ = eng.step(0, tok, want_logits=False)
@@ -94,11 +94,14 @@ def test_stdout_contract_matches_engine(resident):
 def test_eos_stops_runner():
     print("[gpu-case] qd_run eos", flush=True)
     base = ["--synthetic-seed", 3, "--layers", 2, "--vocab", 4096, "--prompt-token-ids", "5,17"]
-    first = run(*base, "--max-new-tokens", 3)
+    first = run(*base, "--max-new-tokens", 8)
     assert first.returncode == 0, first.stderr
     ids = [int(x) for x in GENERATED_TOKEN_IDS_RE.search(first.stdout).group(1).split(",")]
-    r = run(*base, "--max-new-tokens", 3, "--eos-token-id", ids[1], "--resident", "--e2e-check")
-    assert r.returncode == 0, r.stderr
-    got = [int(x) for x in GENERATED_TOKEN_IDS_RE.search(r.stdout).group(1).split(",")]
-    assert got == ids[:2]
-    assert STOP_REASON_RE.search(r.stdout).group(1) == "eos_token"
+    eos = ids[-1]
+    stop = ids.index(eos)  # generation ends at the first occurrence of eos
+    for flags in ((), ("--resident",)):
+        r = run(*base, "--max-new-tokens", 8, "--eos-token-id", eos, "--e2e-check", *flags)
+        assert r.returncode == 0, r.stderr
+        got = [int(x) for x in GENERATED_TOKEN_IDS_RE.search(r.stdout).group(1).split(",")]
+        assert got == ids[:stop + 1], flags
+        assert STOP_REASON_RE.search(r.stdout).group(1) == "eos_token"
