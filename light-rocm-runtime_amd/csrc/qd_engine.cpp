@@ -26,6 +26,7 @@
 #include "qd_bundle.hpp"
 #include "qd_device.hpp"
 #include "qd_kernels.hpp"
+#include "qd_prefill.hpp"
 #include "qd_resident.hpp"
 #include "qd_rng.hpp"
 
@@ -126,6 +127,15 @@ struct qd_engine {
   uint32_t *resident_error = nullptr;       // [1]
   int resident_grid = 0;                    // 0: resident path unavailable
   std::string resident_off_reason;
+  // Prompt workspace (allocated on the first prefill): rows of the hidden
+  // states, RMSNorm output, packed QKV, attention output, gate|up and SwiGLU
+  // activation, plus the chunk's token ids.
+  static constexpr size_t kPrefillRows = 512;
+  float *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr,
+        *pf_gu = nullptr, *pf_act = nullptr, *pf_split = nullptr;
+  // Split-K factors of the narrow GEMMs (QKV, O, down) so they fill the CUs.
+  static constexpr int kSplitQkv = 2, kSplitO = 2, kSplitDown = 4;
+  uint32_t *pf_tokens = nullptr;
 
   qd::SeqState *h_states = nullptr;  // pinned [max_batch]
   uint32_t *h_tokens = nullptr;      // pinned [capacity]
@@ -276,6 +286,56 @@ struct qd_engine {
       case qd::kKArgmax: return 2 * 1024 * f;
     }
     return 0;
+  }
+
+  bool wg_wu_adjacent() const {
+    for (const auto &w : layers)
+      if (w.wu != w.wg + I * H) return false;
+    return true;
+  }
+
+  // One chunk of a prompt (n <= kPrefillRows tokens at positions
+  // pos0 .. pos0 + n - 1 of slot seq) through every layer with the prompt
+  // kernels; leaves the final hidden rows in pf_h.
+  void prefill_chunk(uint32_t seq, const uint32_t *tokens, int n, int pos0) {
+    if (!pf_h) {
+      pf_h = alloc<float>(kPrefillRows * H);
+      pf_xn = alloc<float>(kPrefillRows * H);
+      pf_qkv = alloc<float>(kPrefillRows * QKV);
+      pf_attn = alloc<float>(kPrefillRows * QD);
+      pf_gu = alloc<float>(kPrefillRows * 2 * I);
+      pf_act = alloc<float>(kPrefillRows * I);
+      pf_tokens = alloc<uint32_t>(kPrefillRows);
+      pf_split = alloc<float>(kPrefillRows * std::max({kSplitQkv * QKV, kSplitO * H, kSplitDown * H}));
+    }
+    check(hipMemcpyAsync(pf_tokens, tokens, size_t(n) * 4, hipMemcpyHostToDevice, stream), "H2D");
+    const int h = int(H), in = int(I), qkv = int(QKV), qd = int(QD);
+    const int nq = int(NQ), nkv = int(NKV);
+    check(qd::launch_embed_rows(stream, embed, pf_tokens, n, h, pf_h), "embed rows");
+    for (size_t l = 0; l < L; ++l) {
+      const qd::LayerPtrs &w = layers[l];
+      float *kc = kv_slice(k_cache, seq, l), *vc = kv_slice(v_cache, seq, l);
+      check(qd::launch_rmsnorm_rows(stream, pf_h, w.attn_norm, cfg.rms_eps, n, pf_xn), "norm");
+      check(qd::launch_gemm_nt(stream, pf_xn, h, w.wqkv, h, pf_qkv, qkv, n, qkv, h, qd::kGemmBias,
+                               w.bqkv, kSplitQkv, pf_split),
+            "qkv gemm");
+      check(qd::launch_rope_kv_rows(stream, pf_qkv, n, pos0, nq, nkv, rope_cos, rope_sin, kc, vc),
+            "rope");
+      check(qd::launch_attention_prefill(stream, pf_qkv, n, pos0, nq, nkv, kc, vc, pf_attn),
+            "attention");
+      check(qd::launch_gemm_nt(stream, pf_attn, qd, w.wo, qd, pf_h, h, n, h, qd,
+                               qd::kGemmAccumulate, nullptr, kSplitO, pf_split),
+            "o gemm");
+      check(qd::launch_rmsnorm_rows(stream, pf_h, w.mlp_norm, cfg.rms_eps, n, pf_xn), "norm");
+      // wg and wu are adjacent in the arena: one GEMM over [gate; up] rows.
+      check(qd::launch_gemm_nt(stream, pf_xn, h, w.wg, h, pf_gu, 2 * in, n, 2 * in, h,
+                               qd::kGemmStore, nullptr),
+            "gate/up gemm");
+      check(qd::launch_silu_mul_rows(stream, pf_gu, n, in, pf_act), "swiglu");
+      check(qd::launch_gemm_nt(stream, pf_act, in, w.wd, in, pf_h, h, n, h, in,
+                               qd::kGemmAccumulate, nullptr, kSplitDown, pf_split),
+            "down gemm");
+    }
   }
 
   // Launches the resident megakernel (stream ordered; no synchronisation).
@@ -876,14 +936,25 @@ qd_status qd_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_
     for (uint32_t i = 0; i < n; ++i)
       if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u at %u >= vocab", tokens[i], i);
     e->set_device();
-    // Sequential decode steps; the argmax finaliser advances the position and
-    // the next token is pushed from the host mirror.
-    for (uint32_t i = 0; i < n; ++i) {
-      e->push_state(seq, tokens[i], qd::kModeStep, UINT32_MAX, 0);
-      e->enqueue_step(seq, e->logits + seq * e->V, 0, nullptr);
-      e->positions[seq] += 1;
-      e->sync();  // h_states[seq] is reused by the next push
+    if (!e->wg_wu_adjacent())
+      fail(QD_ERROR_NOT_SUPPORTED, "prefill needs the gate and up weights adjacent");
+    // The prompt in chunks of up to kPrefillRows positions, each through all
+    // layers at once (dense GEMMs); then the tail (final norm, LM head,
+    // argmax) on the last position, which advances the slot to pos0 + n.
+    for (uint32_t done = 0; done < n;) {
+      const uint32_t rows = std::min<uint32_t>(n - done, uint32_t(qd_engine::kPrefillRows));
+      e->prefill_chunk(seq, tokens + done, int(rows), int(e->positions[seq] + done));
+      done += rows;
+      if (done == n)
+        check(hipMemcpyAsync(e->hidden + size_t(seq) * e->H, e->pf_h + size_t(rows - 1) * e->H,
+                             e->H * 4, hipMemcpyDeviceToDevice, e->stream), "D2D");
+      e->sync();  // the next chunk's token upload reuses pf_tokens
     }
+    e->positions[seq] += n - 1;
+    e->push_state(seq, tokens[n - 1], qd::kModeStep, UINT32_MAX, 0);
+    check(qd::launch_tail(e->stream, e->tail_args(seq, e->logits + seq * e->V, 0, nullptr), nullptr),
+          "tail launch");
+    e->positions[seq] += 1;
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState),
                          hipMemcpyDeviceToHost, e->stream), "D2H");
     if (last_logits)

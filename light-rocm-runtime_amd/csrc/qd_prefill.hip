@@ -1,0 +1,456 @@
+// Prompt (prefill) kernels for gfx950: the prompt's positions go through a
+// layer together, so its projections are dense FP32 GEMMs on the matrix
+// cores (v_mfma_f32_32x32x2f32) and its attention a causal flash attention
+// (v_mfma_f32_16x16x4f32), instead of one decode step per position.
+//
+// Semantics follow the decode step per position (the reference's prompt
+// stack, benchmarks/triton_mini_decoder_layer.cpp:811-849, is P sequential
+// decode steps): RMSNorm eps, rotate-half RoPE at the absolute position,
+// K/V cache rows written post-RoPE / raw, attention over positions
+// 0..position inclusive with scale 1/sqrt(64) and query head h reading KV
+// head h / (heads / kv_heads).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <algorithm>
+#include <cstdint>
+
+#include "qd_device.hpp"
+#include "qd_device_math.hpp"
+#include "qd_prefill.hpp"
+
+namespace qd {
+namespace {
+
+using namespace dev;
+
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// ---- GEMM: C = A . W^T --------------------------------------------------------
+// 64 x 64 output tile per workgroup, four waves of 32 x 32 (one
+// v_mfma_f32_32x32x2f32 accumulator each). K is consumed in slices of 32,
+// staged in LDS k-major (padded rows, conflict-free operand reads) and
+// double-buffered: the next slice's global loads are in flight while the
+// current slice feeds the matrix cores.
+// Operand layout of v_mfma_f32_32x32x2f32: lane l supplies A[l % 32][l / 32]
+// and B[l / 32][l % 32]; accumulator register r of lane l holds
+// D[(r / 4) * 8 + (l / 32) * 4 + r % 4][l % 32].
+constexpr int kTileM = 64, kTileN = 64, kTileK = 32;
+constexpr int kLdsRow = kTileM + 32;  // floats per k-row of a staged tile
+
+// Split-K: slice z = blockIdx.z of gridDim.z covers k range [z k / Z,
+// (z + 1) k / Z) and, when Z > 1, writes its plain partial product to
+// C + z * m * ldc (the caller's workspace); gemm_reduce_kernel then sums the
+// partials in slice order and applies the epilogue.
+__global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict__ A, int lda,
+                                                         const float *__restrict__ W, int ldw,
+                                                         float *__restrict__ C, int ldc, int m,
+                                                         int n, int k, int mode,
+                                                         const float *__restrict__ bias) {
+  __shared__ float as[2][kTileK][kLdsRow];
+  __shared__ float ws[2][kTileK][kLdsRow];
+  const int t = threadIdx.x;
+  const int lane = lane_id();
+  const int w = wave_id();
+  const int wr = w >> 1, wc = w & 1;
+  const int m0 = blockIdx.y * kTileM, n0 = blockIdx.x * kTileN;
+  // Each thread stages two float4 of A and two of W per slice: float4 f =
+  // t + 256 i covers row f % 64, columns 4 (f / 64) .. +3 of the slice (the
+  // lanes of a wave take consecutive rows: conflict-free LDS writes).
+  float4 ra[2], rw[2];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int f = t + kBlock * i;
+      const int row = f & 63, c4 = f >> 6;
+      const int gm = m0 + row, gn = n0 + row;
+      ra[i] = gm < m ? *reinterpret_cast<const float4 *>(A + static_cast<size_t>(gm) * lda + k0 + 4 * c4)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      rw[i] = gn < n ? *reinterpret_cast<const float4 *>(W + static_cast<size_t>(gn) * ldw + k0 + 4 * c4)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int f = t + kBlock * i;
+      const int row = f & 63, c4 = f >> 6;
+      as[buf][4 * c4 + 0][row] = ra[i].x;
+      as[buf][4 * c4 + 1][row] = ra[i].y;
+      as[buf][4 * c4 + 2][row] = ra[i].z;
+      as[buf][4 * c4 + 3][row] = ra[i].w;
+      ws[buf][4 * c4 + 0][row] = rw[i].x;
+      ws[buf][4 * c4 + 1][row] = rw[i].y;
+      ws[buf][4 * c4 + 2][row] = rw[i].z;
+      ws[buf][4 * c4 + 3][row] = rw[i].w;
+    }
+  };
+  f16v acc = {};
+  const int split = gridDim.z;
+  const int slices_all = k / kTileK;
+  const int s_begin = static_cast<int>(blockIdx.z) * slices_all / split;
+  const int s_end = (static_cast<int>(blockIdx.z) + 1) * slices_all / split;
+  A += s_begin * kTileK;
+  W += s_begin * kTileK;
+  if (split > 1) {
+    C += static_cast<size_t>(blockIdx.z) * m * ldc;
+    mode = kGemmStore;
+  }
+  const int slices = s_end - s_begin;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int s = 0; s < slices; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < slices) fetch((s + 1) * kTileK);
+#pragma unroll
+    for (int kk = 0; kk < kTileK / 2; ++kk) {
+      const float a = as[buf][2 * kk + (lane >> 5)][wr * 32 + (lane & 31)];
+      const float b = ws[buf][2 * kk + (lane >> 5)][wc * 32 + (lane & 31)];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+    }
+    if (s + 1 < slices) stash(buf ^ 1);
+    __syncthreads();
+  }
+  const int col = n0 + wc * 32 + (lane & 31);
+  if (col >= n) return;
+  const float bv = mode == kGemmBias && split == 1 ? bias[col] : 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = m0 + wr * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+    if (row < m) {
+      float *c = C + static_cast<size_t>(row) * ldc + col;
+      if (mode == kGemmAccumulate)
+        *c += acc[r];
+      else
+        *c = acc[r] + bv;
+    }
+  }
+}
+
+// C[r][c] (op)= sum_z part[z][r][c] (+ bias[c]) for the split-K partials.
+__global__ __launch_bounds__(kBlock) void gemm_reduce_kernel(const float *__restrict__ part,
+                                                             int split, float *__restrict__ C,
+                                                             int ldc, int m, int n, int mode,
+                                                             const float *__restrict__ bias) {
+  const size_t total = static_cast<size_t>(m) * n;
+  for (size_t e = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; e < total;
+       e += static_cast<size_t>(gridDim.x) * kBlock) {
+    const int r = static_cast<int>(e / n), c = static_cast<int>(e % n);
+    float v = part[static_cast<size_t>(r) * ldc + c];
+    for (int z = 1; z < split; ++z) v += part[(static_cast<size_t>(z) * m + r) * ldc + c];
+    float *dst = C + static_cast<size_t>(r) * ldc + c;
+    if (mode == kGemmAccumulate)
+      *dst += v;
+    else
+      *dst = mode == kGemmBias ? v + bias[c] : v;
+  }
+}
+
+// ---- row-wise kernels ----------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void embed_rows_kernel(const float *__restrict__ embed,
+                                                            const uint32_t *__restrict__ tokens,
+                                                            int hidden, float *__restrict__ out) {
+  const int r = blockIdx.x;
+  const float4 *src = reinterpret_cast<const float4 *>(embed + static_cast<size_t>(tokens[r]) * hidden);
+  float4 *dst = reinterpret_cast<float4 *>(out + static_cast<size_t>(r) * hidden);
+  for (int c = threadIdx.x; c < hidden / 4; c += kBlock) dst[c] = src[c];
+}
+
+// Same arithmetic as the decode kernels' RMSNorm (block_inv_rms, then
+// x * inv * gain).
+template <int H>
+__global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float *__restrict__ x,
+                                                              const float *__restrict__ gain,
+                                                              float eps, float *__restrict__ y) {
+  __shared__ float red[kWavesPerBlock];
+  const int r = blockIdx.x;
+  const float *xr = x + static_cast<size_t>(r) * H;
+  const float inv = block_inv_rms<H>(Plain(xr), eps, red);
+  const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+  const float4 *g4 = reinterpret_cast<const float4 *>(gain);
+  float4 *y4 = reinterpret_cast<float4 *>(y + static_cast<size_t>(r) * H);
+  for (int c = threadIdx.x; c < H / 4; c += kBlock) {
+    const float4 v = x4[c], g = g4[c];
+    y4[c] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void rope_kv_rows_kernel(float *__restrict__ qkv, int pos0, int nq,
+                                                              int nkv, const float *__restrict__ rope_cos,
+                                                              const float *__restrict__ rope_sin,
+                                                              float *__restrict__ k_cache,
+                                                              float *__restrict__ v_cache) {
+  const int r = blockIdx.x;
+  const int p = pos0 + r;
+  const int qd = nq * kHeadDim, kvd = nkv * kHeadDim;
+  float *row = qkv + static_cast<size_t>(r) * (qd + 2 * kvd);
+  const int rotations = (nq + nkv) * kRotary;
+  for (int u = threadIdx.x; u < rotations + kvd; u += kBlock) {
+    if (u < rotations) {
+      const int head = u / kRotary, i = u % kRotary;
+      const int a = head * kHeadDim + i, b = a + kRotary;
+      const float c = rope_cos[p * kRotary + i], s = rope_sin[p * kRotary + i];
+      const float x0 = row[a], x1 = row[b];
+      const float first = x0 * c - x1 * s;
+      const float second = x1 * c + x0 * s;
+      row[a] = first;
+      row[b] = second;
+      if (head >= nq) {
+        const int o = (head - nq) * kHeadDim + i;
+        k_cache[static_cast<size_t>(p) * kvd + o] = first;
+        k_cache[static_cast<size_t>(p) * kvd + o + kRotary] = second;
+      }
+    } else {
+      const int o = u - rotations;
+      v_cache[static_cast<size_t>(p) * kvd + o] = row[qd + kvd + o];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void silu_mul_rows_kernel(const float *__restrict__ gu, int inter,
+                                                               float *__restrict__ act) {
+  const int r = blockIdx.x;
+  const float *g = gu + static_cast<size_t>(r) * 2 * inter;
+  float *o = act + static_cast<size_t>(r) * inter;
+  for (int i = threadIdx.x; i < inter; i += kBlock) {
+    const float gv = g[i];
+    o[i] = gv / (1.f + expf(-gv)) * g[inter + i];
+  }
+}
+
+// ---- causal GQA flash attention ---------------------------------------------------
+// Workgroup = (query head h, block of 16 prompt rows); its four waves take
+// the key blocks (32 positions) round-robin, each keeping an online softmax
+// and an output accumulator for the 16 queries, merged in LDS at the end.
+// Per key block a wave computes S = Q . K^T (two 16 x 16 tiles over 64
+// dims) and O += P . V (four 16 x 16 tiles over 32 keys) with
+// v_mfma_f32_16x16x4f32, whose lane l supplies A[l % 16][l / 16] and
+// B[l / 16][l % 16] and holds D[(l / 16) * 4 + r][l % 16] in register r.
+constexpr int kQBlock = 16;
+constexpr int kKBlock = 32;
+constexpr int kKRow = kHeadDim + 4;   // LDS K row stride (conflict-free B reads)
+constexpr int kVRow = kHeadDim + 16;  // LDS V row stride
+constexpr int kPRow = kKBlock + 4;    // LDS P row stride
+
+struct PrefillAttnLds {
+  float k[kWavesPerBlock][kKBlock][kKRow];
+  float v[kWavesPerBlock][kKBlock][kVRow];
+  float p[kWavesPerBlock][kQBlock][kPRow];
+  float ml[kWavesPerBlock][kQBlock][2];
+  float o[kWavesPerBlock][kQBlock][kHeadDim + 1];
+};
+
+// max / sum over the 16 lanes of a DPP row (lanes 16g .. 16g + 15).
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return v;
+}
+
+__global__ __launch_bounds__(kBlock) void attention_prefill_kernel(
+    const float *__restrict__ qkv, int rows, int pos0, int nq, int nkv,
+    const float *__restrict__ k_cache, const float *__restrict__ v_cache, float *__restrict__ out) {
+  __shared__ PrefillAttnLds sh;
+  const int h = blockIdx.y;
+  const int r0 = blockIdx.x * kQBlock;
+  const int g = h / (nq / nkv);
+  const int qd = nq * kHeadDim, kvd = nkv * kHeadDim;
+  const int ld = qd + 2 * kvd;
+  const int w = wave_id();
+  const int lane = lane_id();
+  const int lr = lane & 15, lg = lane >> 4;
+  const float scale = rsqrtf(static_cast<float>(kHeadDim));
+  const int last_row = min(rows, r0 + kQBlock) - 1;
+  const int keys = pos0 + last_row + 1;  // causal extent of the block
+  const int kblocks = (keys + kKBlock - 1) / kKBlock;
+
+  // Query operand: lane supplies Q[row lr][dim 4 s + lg] for s < 16.
+  float qa[kHeadDim / 4];
+  {
+    const int qrow = min(r0 + lr, rows - 1);
+    const float *q = qkv + static_cast<size_t>(qrow) * ld + h * kHeadDim;
+#pragma unroll
+    for (int s = 0; s < kHeadDim / 4; ++s) qa[s] = q[4 * s + lg];
+  }
+  // Running state of the lane's four query rows lg * 4 + r.
+  float m[4], l[4];
+  f4v o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+    o[r] = f4v{0.f, 0.f, 0.f, 0.f};
+  }
+  float (*ks)[kKRow] = sh.k[w];
+  float (*vs)[kVRow] = sh.v[w];
+  float (*ps)[kPRow] = sh.p[w];
+  for (int kb = w; kb < kblocks; kb += kWavesPerBlock) {
+    const int k0 = kb * kKBlock;
+    // Stage the block's K and V rows: lane covers rows lane / 16 + 4 i,
+    // float4 column lane % 16.
+#pragma unroll
+    for (int i = 0; i < kKBlock / 4; ++i) {
+      const int row = lg + 4 * i;
+      const int j = k0 + row;
+      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+      if (j < keys) {
+        kv = *reinterpret_cast<const float4 *>(k_cache + static_cast<size_t>(j) * kvd + g * kHeadDim + 4 * lr);
+        vv = *reinterpret_cast<const float4 *>(v_cache + static_cast<size_t>(j) * kvd + g * kHeadDim + 4 * lr);
+      }
+      ks[row][4 * lr + 0] = kv.x;
+      ks[row][4 * lr + 1] = kv.y;
+      ks[row][4 * lr + 2] = kv.z;
+      ks[row][4 * lr + 3] = kv.w;
+      vs[row][4 * lr + 0] = vv.x;
+      vs[row][4 * lr + 1] = vv.y;
+      vs[row][4 * lr + 2] = vv.z;
+      vs[row][4 * lr + 3] = vv.w;
+    }
+    // S tiles: keys k0 + 16 tt + lr.
+    f4v s[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      s[tt] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < kHeadDim / 4; ++st)
+        s[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], ks[16 * tt + lr][4 * st + lg], s[tt], 0, 0, 0);
+    }
+    // Online softmax per query row (row = lg * 4 + r, spread over the 16
+    // lanes of DPP row lg and the two tiles).
+    float corr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int qpos = pos0 + min(r0 + lg * 4 + r, rows - 1);
+      float sv[2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int key = k0 + 16 * tt + lr;
+        sv[tt] = key <= qpos ? s[tt][r] * scale : -INFINITY;
+      }
+      const float m_new = fmaxf(m[r], row16_max(fmaxf(sv[0], sv[1])));
+      float p0 = 0.f, p1 = 0.f;
+      corr[r] = 1.f;
+      if (m_new != -INFINITY) {
+        p0 = expf(sv[0] - m_new);
+        p1 = expf(sv[1] - m_new);
+        corr[r] = expf(m[r] - m_new);
+      }
+      l[r] = fmaf(l[r], corr[r], row16_sum(p0 + p1));
+      m[r] = m_new;
+      ps[lg * 4 + r][lr] = p0;
+      ps[lg * 4 + r][16 + lr] = p1;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[dt][r] *= corr[r];
+    // O += P . V: A = P[row lr][key 4 st + lg], B = V[key 4 st + lg][dim 16 dt + lr].
+#pragma unroll
+    for (int st = 0; st < kKBlock / 4; ++st) {
+      const float pa = ps[lr][4 * st + lg];
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vs[4 * st + lg][16 * dt + lr], o[dt], 0, 0, 0);
+    }
+  }
+  // Merge the four waves' partials.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int q = lg * 4 + r;
+    if (lr == 0) {
+      sh.ml[w][q][0] = m[r];
+      sh.ml[w][q][1] = l[r];
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) sh.o[w][q][16 * dt + lr] = o[dt][r];
+  }
+  __syncthreads();
+  {
+    const int q = threadIdx.x >> 4;        // 16 queries
+    const int d0 = (threadIdx.x & 15) * 4;  // 4 dims each
+    const int row = r0 + q;
+    if (row < rows) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < kWavesPerBlock; ++v) mx = fmaxf(mx, sh.ml[v][q][0]);
+      float den = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int v = 0; v < kWavesPerBlock; ++v) {
+        const float mv = sh.ml[v][q][0];
+        const float f = mv == -INFINITY ? 0.f : expf(mv - mx);
+        den = fmaf(f, sh.ml[v][q][1], den);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = fmaf(f, sh.o[v][q][d0 + e], acc[e]);
+      }
+      float *dst = out + static_cast<size_t>(row) * qd + h * kHeadDim + d0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[e] = acc[e] / den;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_nt(hipStream_t s, const float *A, int lda, const float *W, int ldw,
+                          float *C, int ldc, int m, int n, int k, GemmMode mode,
+                          const float *bias, int split, float *workspace) {
+  if (k % kTileK != 0 || m <= 0 || n <= 0 || split < 1 || split > k / kTileK ||
+      (split > 1 && !workspace))
+    return hipErrorInvalidValue;
+  const dim3 grid((n + kTileN - 1) / kTileN, (m + kTileM - 1) / kTileM, split);
+  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, W, ldw, split > 1 ? workspace : C, ldc, m, n, k,
+                                         mode, bias);
+  if (split > 1) {
+    const size_t total = static_cast<size_t>(m) * n;
+    const int blocks = static_cast<int>(std::min<size_t>((total + kBlock - 1) / kBlock, 4096));
+    gemm_reduce_kernel<<<blocks, kBlock, 0, s>>>(workspace, split, C, ldc, m, n, mode, bias);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(hipStream_t s, const float *embed, const uint32_t *tokens, int rows,
+                             int hidden, float *out) {
+  embed_rows_kernel<<<rows, kBlock, 0, s>>>(embed, tokens, hidden, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_rows(hipStream_t s, const float *x, const float *gain, float eps,
+                               int rows, float *y) {
+  rmsnorm_rows_kernel<896><<<rows, kBlock, 0, s>>>(x, gain, eps, y);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_rows(hipStream_t s, float *qkv, int rows, int pos0, int nq, int nkv,
+                               const float *rope_cos, const float *rope_sin, float *k_cache,
+                               float *v_cache) {
+  rope_kv_rows_kernel<<<rows, kBlock, 0, s>>>(qkv, pos0, nq, nkv, rope_cos, rope_sin, k_cache,
+                                              v_cache);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_prefill(hipStream_t s, const float *qkv, int rows, int pos0, int nq,
+                                    int nkv, const float *k_cache, const float *v_cache,
+                                    float *out) {
+  const dim3 grid((rows + kQBlock - 1) / kQBlock, nq);
+  attention_prefill_kernel<<<grid, kBlock, 0, s>>>(qkv, rows, pos0, nq, nkv, k_cache, v_cache, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul_rows(hipStream_t s, const float *gu, int rows, int inter, float *act) {
+  silu_mul_rows_kernel<<<rows, kBlock, 0, s>>>(gu, inter, act);
+  return hipGetLastError();
+}
+
+}  // namespace qd

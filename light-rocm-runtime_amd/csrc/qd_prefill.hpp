@@ -1,0 +1,49 @@
+// Host-side launchers of the prompt (prefill) kernels (qd_prefill.hip): the
+// prompt's positions go through each layer together, as dense FP32 GEMMs on
+// the matrix cores plus a causal GQA attention.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "qd_device.hpp"
+
+namespace qd {
+
+// GEMM epilogues: C = A . W^T (+ bias) or C += A . W^T (residual).
+enum GemmMode : int { kGemmStore = 0, kGemmBias = 1, kGemmAccumulate = 2 };
+
+// C[m][n] (row stride ldc) for A [m][k] (stride lda) and W [n][k] (stride
+// ldw), all FP32 row-major. m, n any size (edges masked); k a multiple of 32.
+// split > 1 divides k over that many workgroup slices whose partials go to
+// workspace (split * m * ldc floats) and are summed in a fixed order.
+hipError_t launch_gemm_nt(hipStream_t s, const float *A, int lda, const float *W, int ldw,
+                          float *C, int ldc, int m, int n, int k, GemmMode mode,
+                          const float *bias, int split = 1, float *workspace = nullptr);
+
+// out[r] = embed[tokens[r]] for r < rows (hidden floats each).
+hipError_t launch_embed_rows(hipStream_t s, const float *embed, const uint32_t *tokens, int rows,
+                             int hidden, float *out);
+
+// y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * gain for r < rows (hidden = 896).
+hipError_t launch_rmsnorm_rows(hipStream_t s, const float *x, const float *gain, float eps,
+                               int rows, float *y);
+
+// Rotates the query and key heads of every row of qkv ([rows][q | k | v],
+// rotate-half at position pos0 + r) in place and writes the rotated K and
+// the V rows to the cache slots pos0 + r.
+hipError_t launch_rope_kv_rows(hipStream_t s, float *qkv, int rows, int pos0, int nq, int nkv,
+                               const float *rope_cos, const float *rope_sin, float *k_cache,
+                               float *v_cache);
+
+// Causal GQA attention of rows queries at positions pos0.. over cache
+// positions 0..pos0 + r: out[r][h*64 + d] from the rotated queries in qkv.
+hipError_t launch_attention_prefill(hipStream_t s, const float *qkv, int rows, int pos0, int nq,
+                                    int nkv, const float *k_cache, const float *v_cache,
+                                    float *out);
+
+// act[r][i] = silu(gu[r][i]) * gu[r][inter + i].
+hipError_t launch_silu_mul_rows(hipStream_t s, const float *gu, int rows, int inter, float *act);
+
+}  // namespace qd

@@ -232,6 +232,49 @@ def test_batch_step_matches_oracle_per_sequence(full):
         check_logits(int(greedy[slot]), logits[slot], rtok, rlog, f"batch seq {slot}")
 
 
+def test_prefill_512_config5_matches_oracle(full):
+    """BASELINE config 5 prompt: 512 positions through the MFMA prompt path
+    (dense GEMMs + causal attention), then decode steps reusing its cache."""
+    eng, model = full
+    prompt = qo.fill_tokens(512, 4, PROMPT_STREAM, FULL.vocab)
+    say("prefill 512 (config 5) vs oracle")
+    eng.kv_reset(0, 0)
+    cache = qo.Cache(model, 520)
+    tok, _, logits = eng.prefill(0, prompt)
+    rtok, _, rlogits = cache.prefill(prompt)
+    check_logits(tok, logits, rtok, rlogits, "prefill 512")
+    assert eng.decode_state(0).token_position == 512
+    for layer in (0, 11, 23):
+        gk, gv = eng.read_kv(0, layer, 0, 512)
+        assert rel_err(gk, cache.layer(layer, False)[:512]) <= HIDDEN_RTOL, layer
+        assert rel_err(gv, cache.layer(layer, True)[:512]) <= HIDDEN_RTOL, layer
+    feed = rtok
+    for i in range(3):
+        tok, _, logits = eng.step(0, feed)
+        rtok, _, rlogits = cache.decode_step(feed, 512 + i)
+        check_logits(tok, logits, rtok, rlogits, f"decode after prefill {i}")
+        feed = rtok
+
+
+def test_prefill_in_pieces_and_over_chunks_agree(full):
+    """A prompt prefilled in two calls (the second continuing at position 300)
+    and one longer than a 512-row chunk give the one-call results."""
+    eng, _ = full
+    prompt = qo.fill_tokens(700, 4, PROMPT_STREAM + 5, FULL.vocab)
+    say("prefill 700 at once / 300 + 400")
+    eng.kv_reset(0, 0)
+    tok, _, logits = eng.prefill(0, prompt)
+    k_once, v_once = eng.read_kv(0, 5, 0, 700)
+    eng.kv_reset(1, 0)
+    eng.prefill(1, prompt[:300], want_logits=False)
+    tok2, _, logits2 = eng.prefill(1, prompt[300:])
+    assert eng.decode_state(1).token_position == 700
+    assert tok2 == tok or margin(logits) <= MARGIN
+    assert rel_err(logits2, logits) <= LOGIT_RTOL
+    k_two, v_two = eng.read_kv(1, 5, 0, 700)
+    assert rel_err(k_two, k_once) <= HIDDEN_RTOL and rel_err(v_two, v_once) <= HIDDEN_RTOL
+
+
 def test_long_context_4096(full):
     """BASELINE config 3 attention length: one step at position 4096 over a
     synthetic N(0,1) KV cache in every layer."""
