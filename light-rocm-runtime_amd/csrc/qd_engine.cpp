@@ -26,6 +26,7 @@
 #include "qd_bundle.hpp"
 #include "qd_device.hpp"
 #include "qd_kernels.hpp"
+#include "qd_batch.hpp"
 #include "qd_prefill.hpp"
 #include "qd_resident.hpp"
 #include "qd_rng.hpp"
@@ -136,6 +137,13 @@ struct qd_engine {
   // Split-K factors of the narrow GEMMs (QKV, O, down) so they fill the CUs.
   static constexpr int kSplitQkv = 2, kSplitO = 2, kSplitDown = 4;
   uint32_t *pf_tokens = nullptr;
+  // Batched-step workspace (allocated on the first batched step): rows of
+  // up to kBatchRows sequences, attention and split-K partials, arrival
+  // counters, the LM-head top-1 partials and each row's greedy result.
+  float *bt_h = nullptr, *bt_q = nullptr, *bt_attn = nullptr, *bt_act = nullptr,
+        *bt_part = nullptr, *bt_split = nullptr, *bt_val = nullptr, *bt_top = nullptr;
+  uint32_t *bt_idx = nullptr, *bt_counters = nullptr, *bt_token = nullptr;
+  uint32_t *h_bt_out = nullptr;  // pinned [max_batch] tokens then [max_batch] top logits
 
   qd::SeqState *h_states = nullptr;  // pinned [max_batch]
   uint32_t *h_tokens = nullptr;      // pinned [capacity]
@@ -150,6 +158,7 @@ struct qd_engine {
     for (void *p : allocs) (void)hipFree(p);
     if (h_states) (void)hipHostFree(h_states);
     if (h_tokens) (void)hipHostFree(h_tokens);
+    if (h_bt_out) (void)hipHostFree(h_bt_out);
     if (ev_begin) (void)hipEventDestroy(ev_begin);
     if (ev_end) (void)hipEventDestroy(ev_end);
     if (stream) (void)hipStreamDestroy(stream);
@@ -286,6 +295,79 @@ struct qd_engine {
       case qd::kKArgmax: return 2 * 1024 * f;
     }
     return 0;
+  }
+
+  // Arguments of one batched launch over rows sequences: slot ids, tokens
+  // and (host-tracked) positions of batch rows first .. first + rows - 1.
+  qd::BatchLaunch batch_args(const uint32_t *slots, const uint32_t *tokens, int rows) {
+    if (!bt_h) {
+      const size_t r = qd::kBatchRows;
+      bt_h = alloc<float>(r * H);
+      bt_q = alloc<float>(r * QD);
+      bt_attn = alloc<float>(r * QD);
+      bt_act = alloc<float>(r * I);
+      bt_part = alloc<float>(r * NQ * qd::kAttnMaxChunks * qd::kPartStride);
+      bt_split = alloc<float>(qd::kBatchSplitFloats);
+      bt_counters = alloc<uint32_t>(qd::kBatchCounters);
+      bt_val = alloc<float>(r * qd::kBatchLmParts);
+      bt_idx = alloc<uint32_t>(r * qd::kBatchLmParts);
+      bt_token = alloc<uint32_t>(B);
+      bt_top = alloc<float>(B);
+      check(hipMemsetAsync(bt_counters, 0, qd::kBatchCounters * sizeof(uint32_t), stream), "memset");
+      check(hipHostMalloc(reinterpret_cast<void **>(&h_bt_out), 2 * B * sizeof(uint32_t),
+                          hipHostMallocDefault),
+            "hipHostMalloc");
+    }
+    qd::BatchLaunch b{};
+    b.rows = rows;
+    for (int i = 0; i < rows; ++i) {
+      b.slot[i] = slots[i];
+      b.pos[i] = positions[slots[i]];
+      b.token[i] = tokens[i];
+    }
+    b.states = states;
+    b.hidden = bt_h;
+    b.q = bt_q;
+    b.attn = bt_attn;
+    b.act = bt_act;
+    b.part = bt_part;
+    b.split = bt_split;
+    b.counters = bt_counters;
+    b.k_cache = k_cache;
+    b.v_cache = v_cache;
+    b.rope_cos = rope_cos;
+    b.rope_sin = rope_sin;
+    b.layers = static_cast<int>(L);
+    b.capacity = static_cast<int>(CAP);
+    b.nq = static_cast<int>(NQ);
+    b.nkv = static_cast<int>(NKV);
+    b.eps = cfg.rms_eps;
+    return b;
+  }
+
+  // Tail arguments of the group whose first batch row is `first`: logits go
+  // to rows first.. of the logits buffer, greedy results to bt_token/bt_top.
+  qd::BatchTail batch_tail(size_t first) const {
+    qd::BatchTail t{};
+    t.final_norm = final_norm;
+    t.head = lm_head;
+    t.logits = logits + first * V;
+    t.part_val = bt_val;
+    t.part_idx = bt_idx;
+    t.out_token = bt_token + first;
+    t.out_top = bt_top + first;
+    t.vocab = static_cast<int>(V);
+    return t;
+  }
+
+  // Embedding + every layer + LM head + argmax of one batch group (states
+  // and slot list already on the device).
+  void enqueue_batch(const qd::BatchLaunch &b, size_t first, qd::Marker *m = nullptr) {
+    check(qd::launch_batch_embed(stream, b, embed, static_cast<int>(V), m), "batch embed launch");
+    for (size_t l = 0; l < L; ++l)
+      check(qd::launch_batch_layer(stream, b, layers[l], static_cast<int>(l), m),
+            "batch layer launch");
+    check(qd::launch_batch_tail(stream, b, batch_tail(first), m), "batch tail launch");
   }
 
   bool wg_wu_adjacent() const {
@@ -980,23 +1062,24 @@ qd_status qd_step_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, c
       if (e->positions[seq_ids[i]] >= e->CAP) fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full", seq_ids[i]);
     }
     e->set_device();
-    for (uint32_t i = 0; i < n_seq; ++i) {
-      const uint32_t s = seq_ids[i];
-      e->push_state(s, tokens[i], qd::kModeStep, UINT32_MAX, 0);
-      e->enqueue_step(s, e->logits + size_t(s) * e->V, 0, nullptr);
+    // Groups of up to kBatchRows sequences share every weight read; the
+    // kernels take each row's slot, token and position as arguments and
+    // leave the slot's state as a batch-1 step would.
+    for (uint32_t first = 0; first < n_seq; first += qd::kBatchRows) {
+      const int rows = static_cast<int>(std::min<uint32_t>(qd::kBatchRows, n_seq - first));
+      e->enqueue_batch(e->batch_args(seq_ids + first, tokens + first, rows), first);
     }
-    for (uint32_t i = 0; i < n_seq; ++i) {
-      const uint32_t s = seq_ids[i];
-      check(hipMemcpyAsync(&e->h_states[s], e->states + s, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
-                           e->stream), "D2H");
-      if (logits)
-        check(hipMemcpyAsync(logits + size_t(i) * e->V, e->logits + size_t(s) * e->V, e->V * 4,
-                             hipMemcpyDeviceToHost, e->stream), "D2H");
-    }
+    check(hipMemcpyAsync(e->h_bt_out, e->bt_token, n_seq * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    check(hipMemcpyAsync(e->h_bt_out + e->B, e->bt_top, n_seq * 4, hipMemcpyDeviceToHost, e->stream),
+          "D2H");
+    if (logits)
+      check(hipMemcpyAsync(logits, e->logits, size_t(n_seq) * e->V * 4, hipMemcpyDeviceToHost,
+                           e->stream),
+            "D2H");
     e->sync();
     for (uint32_t i = 0; i < n_seq; ++i) {
       e->positions[seq_ids[i]] += 1;
-      if (greedy) greedy[i] = e->h_states[seq_ids[i]].token;
+      if (greedy) greedy[i] = e->h_bt_out[i];
     }
   });
 }
