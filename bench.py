@@ -1,11 +1,19 @@
-"""Decode benchmark: batch-1 FP32 Qwen2.5-0.5B-shape greedy decode on one GPU.
+"""Decode benchmark of the Qwen2 FP32 decode path on one GPU. Prints one JSON line.
 
-Workload: 24-layer FP32 decoder + tied
-151936x896 LM head, random-init N(0, 0.02) weights (seed 1), a 512-token
-uniform random prompt, then greedy decode steps with argmax feedback on the
-device. One "step" = one decode token. Prints one JSON line.
+Workloads (synthetic random-init weights):
+  decode   (default) config 2: 24-layer FP32 decoder + tied 151936x896 LM
+           head, N(0, 0.02) weights (seed 1), a 512-token uniform random
+           prompt, then greedy decode steps with argmax feedback on the device.
+           One "step" = one decode token.
+  batch16  config 4: 16 independent sequences with contexts uniform in
+           [256, 2048] (seed 3) decoded together; one step = one token of
+           every sequence (16 tokens).
+  prefill  config 5: the 512-token prompt (seed 4) through the MFMA prompt
+           path; one step = one prefill of the 512 tokens. The 128 greedy
+           decode steps that follow it in config 5 are reported beside it.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+  python bench.py [--workload decode|batch16|prefill] [--steps K] [--warmup W]
+                  [--gpus 1] [--no-cpu]
 """
 import argparse
 import json
@@ -23,9 +31,14 @@ import qwen_decode as qd  # noqa: E402
 
 METRIC = "decode tokens/s at batch 1 (Qwen2.5-0.5B-shape FP32) + % HBM roofline"
 HBM_PEAK_GBS = 8000.0
+MFMA_FP32_PEAK_TFLOPS = 157.3
+VOCAB = 151936
 PROMPT = 512
 SEED = 1
 PROMPT_STREAM = 0x300000
+BATCH_SEED, BATCH_ROWS = 3, 16
+LEN_STREAM, BATCH_PROMPT_STREAM = 0x400000, 0x410000
+PREFILL_SEED, PREFILL_DECODE = 4, 128
 
 # Algorithmic bytes of one decode token attending over L positions:
 # all FP32 weights (24 x 59,649,536 + tied head 544,538,624 + final norm 3,584)
@@ -49,74 +62,96 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(budget_s: float = 12.0):
+def stream_tokens(n, seed, stream, vocab):
+    """Uniform random tokens from the repository's counter-based generator
+    (splitmix64 over a per-(seed, stream) key, the same stream the oracle and
+    the tests use), computed here without the oracle."""
+    m = (1 << 64) - 1
+
+    def mix(z):
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+        return z ^ (z >> 31)
+
+    key = mix((seed * 0x9E3779B97F4A7C15 + stream * 0xC2B2AE3D27D4EB4F + 0x165667B19E3779F9) & m)
+    out = np.empty(n, np.uint32)
+    for i in range(n):
+        r = mix((key + i * 0x9E3779B97F4A7C15) & m) >> 32
+        out[i] = (r * vocab) >> 32
+    return out
+
+
+def roofline_hbm(name, avg_us, avg_bytes, traffic=None):
+    achieved = avg_bytes / (avg_us * 1e-6) / 1e9
+    return {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "avg_us": round(avg_us, 3), "bytes_per_launch": round(avg_bytes)}
+
+
+def dominant(prof):
+    """The kernel with the largest total time: (name, (launches, avg_us, avg_bytes, avg_flops))."""
+    return max(prof.items(), key=lambda kv: kv[1][0] * kv[1][1])
+
+
+def mfma_summary(prof, names):
+    """Achieved FP32 matrix-core rate over the given kernels' launches."""
+    us = sum(prof[n][0] * prof[n][1] for n in names if n in prof)
+    fl = sum(prof[n][0] * prof[n][3] for n in names if n in prof)
+    tf = fl / (us * 1e-6) / 1e12 if us else 0.0
+    return {"kernels": [n for n in names if n in prof], "achieved_tflops": round(tf, 2),
+            "peak_tflops": MFMA_FP32_PEAK_TFLOPS, "frac": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
+
+
+# ---- CPU baselines (the oracle, timed on this host's cores) ---------------------
+
+def cpu_decode_baseline(seed, contexts, budget_s=12.0, max_steps=62):
     """The CPU oracle (FP32, OpenMP over host cores, KV cache) timed on decode
-    steps of the same model at the same context length (512 cached positions
-    of synthetic KV), as many steps as fit the time budget."""
+    steps of the same model, cycling through `contexts` (synthetic cached KV),
+    as many steps as fit the time budget."""
     import qwen_oracle as qo
 
     model = qo.Model(qo.QWEN25_05B)
-    model.fill_synthetic(SEED)
-    cache = qo.Cache(model, PROMPT + 64)
+    model.fill_synthetic(seed)
+    top = max(contexts)
+    cache = qo.Cache(model, top + max_steps + 2)
     for layer in range(qo.QWEN25_05B.layers):
-        cache.layer(layer, False)[:PROMPT] = 0.01
-        cache.layer(layer, True)[:PROMPT] = 0.01
-    cache.decode_step(1, PROMPT, want_logits=False)  # warm caches / threads
+        cache.layer(layer, False)[:top] = 0.01
+        cache.layer(layer, True)[:top] = 0.01
+    cache.decode_step(1, contexts[0], want_logits=False)  # warm caches / threads
     steps, t0 = 0, time.perf_counter()
     while True:
-        cache.decode_step(1 + steps, PROMPT + 1 + steps, want_logits=False)
+        cache.decode_step(1 + steps, contexts[steps % len(contexts)] + steps // len(contexts),
+                          want_logits=False)
         steps += 1
         el = time.perf_counter() - t0
-        if el > budget_s or steps >= 62:
+        if el > budget_s or steps >= max_steps:
             break
     model.close()
-    return {"value": round(steps / el, 3), "unit": "tokens/s", "cores": qo.threads(),
-            "kind": "port",
-            "sample": f"{steps} decode steps at context {PROMPT + 1}..{PROMPT + steps}, "
-                      f"24 layers + 151936-row LM head, oracle/libqwen_oracle.so FP32 OpenMP"}
+    return steps, el, qo.threads()
 
 
-def copy_probe(mib: int):
-    """Copies `mib` MiB device-to-device through the HIP runtime: a plain copy
-    kernel of known size whose FETCH_SIZE / WRITE_SIZE counters calibrate the
-    per-dispatch HBM traffic of the decode kernel in the same profile."""
-    import ctypes as C
+def cpu_prefill_baseline(seed, n):
+    import qwen_oracle as qo
 
-    hip = C.CDLL("libamdhip64.so")
-    n = mib << 20
-    src, dst = C.c_void_p(), C.c_void_p()
-    for p in (src, dst):
-        if hip.hipMalloc(C.byref(p), C.c_size_t(n)) != 0:
-            raise RuntimeError("hipMalloc failed")
-    hip.hipMemset(src, 1, C.c_size_t(n))
-    for _ in range(3):
-        hip.hipMemcpy(dst, src, C.c_size_t(n), 3)  # device to device
-    hip.hipDeviceSynchronize()
-    hip.hipFree(src)
-    hip.hipFree(dst)
-    log(f"copy probe: 3 x {mib} MiB device-to-device")
+    model = qo.Model(qo.QWEN25_05B)
+    model.fill_synthetic(seed)
+    cache = qo.Cache(model, n + 2)
+    prompt = stream_tokens(n, seed, PROMPT_STREAM, VOCAB)
+    t0 = time.perf_counter()
+    cache.prefill(prompt, want_logits=False)
+    el = time.perf_counter() - t0
+    model.close()
+    return el, qo.threads()
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
-    ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
-                    help="also run a plain device copy of MIB MiB (PMC calibration)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for {args.gpus}); the decode path "
-              "has no multi-GPU mode in this build", file=sys.stderr)
-        sys.exit(2)
-    K, W = args.steps, args.warmup
+# ---- workloads ------------------------------------------------------------------
+
+def run_decode(K, W, no_cpu):
     capacity = PROMPT + max(K, W) + 8
-
     log("engine create + synthetic weights")
     eng = qd.Engine(capacity=capacity, max_batch=1)
     eng.load_synthetic(SEED)
-    prompt = qo_tokens(PROMPT)
+    prompt = stream_tokens(PROMPT, SEED, PROMPT_STREAM, VOCAB)
     log("prefill 512")
     first, _, _ = eng.prefill(0, prompt, want_logits=False)
 
@@ -142,31 +177,28 @@ def main():
     if grid:
         # One resident launch runs all K tokens: its HIP-event duration on the
         # engine stream is the kernel time, its algorithmic bytes the K steps'.
-        dom_name, avg_us, avg_bytes = "resident_decode_kernel", timing.total_us, float(total_bytes)
         traffic = RESIDENT_TRAFFIC_PER_TOKEN * K if RESIDENT_TRAFFIC_PER_TOKEN else None
+        roof = roofline_hbm("resident_decode_kernel", timing.total_us, float(total_bytes), traffic)
     else:
         eng.kv_reset(0, PROMPT)
         prof = eng.profile_kernels(0, first, min(K, 16))
-        dom_name, (launches, avg_us, avg_bytes) = max(prof.items(), key=lambda kv: kv[1][0] * kv[1][1])
-        traffic = None
+        name, (_, avg_us, avg_bytes, _) = dominant(prof)
+        roof = roofline_hbm(name, avg_us, avg_bytes)
         log("kernel profile: " + ", ".join(f"{n}={v[1]:.1f}us" for n, v in prof.items()))
-    achieved = avg_bytes / (avg_us * 1e-6) / 1e9
     eng.close()
 
-    if args.copy_probe:
-        copy_probe(args.copy_probe)
-    cpu = None if args.no_cpu else cpu_baseline()
-    out = {
+    cpu = None
+    if not no_cpu:
+        steps, el, cores = cpu_decode_baseline(SEED, [PROMPT])
+        cpu = {"value": round(steps / el, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+               "sample": f"{steps} decode steps at context {PROMPT + 1}..{PROMPT + steps}, "
+                         f"24 layers + 151936-row LM head, oracle/libqwen_oracle.so FP32 OpenMP"}
+    return {
         "metric": METRIC,
         "value": round(tok_s, 2),
         "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": K,
-        "warmup": W,
         "ms_per_step": round(wall * 1e3 / K, 4),
         "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: random-init N(0,0.02) weights / N(0,0.01) biases, seed 1; "
                 "512 uniform random prompt tokens",
@@ -175,38 +207,218 @@ def main():
                         "151936x896 LM head, batch 1, prompt 512 then greedy decode with "
                         "device argmax feedback",
             "batch": 1, "context": f"{PROMPT + 1}..{PROMPT + K}", "layers": 24,
-            "hidden": 896, "vocab": 151936,
+            "hidden": 896, "vocab": VOCAB,
         },
         "step_hbm": {"achieved_gbs": round(step_gbs, 1), "peak_gbs": HBM_PEAK_GBS,
                      "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                      "bytes_per_token": round(total_bytes / K)},
         "device_tokens_per_s": round(K / dev_s, 2),
-        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "avg_us": round(avg_us, 3),
-                     "bytes_per_launch": round(avg_bytes)},
+        "roofline": roof,
         "cpu_baseline": cpu,
         "path": f"resident megakernel, {grid} workgroups" if grid else "stream-ordered kernels",
     }
-    print(json.dumps(out), flush=True)
 
 
-def qo_tokens(n):
-    """Uniform random prompt tokens from the shared generator specification
-    (same stream the tests use), computed here without the oracle."""
-    m = (1 << 64) - 1
+def batch_lengths():
+    return [256 + int(x) for x in stream_tokens(BATCH_ROWS, BATCH_SEED, LEN_STREAM, 2048 - 256 + 1)]
 
-    def mix(z):
-        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
-        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
-        return z ^ (z >> 31)
 
-    key = mix((SEED * 0x9E3779B97F4A7C15 + PROMPT_STREAM * 0xC2B2AE3D27D4EB4F + 0x165667B19E3779F9) & m)
-    out = np.empty(n, np.uint32)
-    for i in range(n):
-        r = mix((key + i * 0x9E3779B97F4A7C15) & m) >> 32
-        out[i] = (r * 151936) >> 32
-    return out
+def run_batch16(K, W, no_cpu):
+    lengths = batch_lengths()
+    slots = list(range(BATCH_ROWS))
+    log("engine create + synthetic weights (seed 3, 16 slots)")
+    eng = qd.Engine(capacity=max(lengths) + max(K, W) + 16, max_batch=BATCH_ROWS)
+    eng.load_synthetic(BATCH_SEED)
+    firsts = []
+    log("prefill 16 ragged prompts")
+    for s, n in enumerate(lengths):
+        eng.kv_reset(s, 0)
+        t, _, _ = eng.prefill(s, stream_tokens(n, BATCH_SEED, BATCH_PROMPT_STREAM + s, VOCAB),
+                              want_logits=False)
+        firsts.append(t)
+
+    def run(steps):
+        feeds = list(firsts)
+        for _ in range(steps):
+            g, _ = eng.step_batch(slots, feeds, want_logits=False)
+            feeds = [int(x) for x in g]
+
+    if W:
+        log(f"warmup {W}")
+        run(W)
+    for s in slots:
+        eng.kv_reset(s, lengths[s])
+    log(f"timed {K} batched steps")
+    eng.sync()
+    t0 = time.perf_counter()
+    run(K)
+    eng.sync()
+    wall = time.perf_counter() - t0
+    for s in slots:
+        eng.kv_reset(s, lengths[s])
+    prof = eng.profile_batch(slots, firsts, min(K, 8))
+    eng.close()
+    log("kernel profile: " + ", ".join(f"{n}={v[1]:.1f}us" for n, v in prof.items()))
+    name, (_, avg_us, avg_bytes, _) = dominant(prof)
+    # Algorithmic bytes of the K steps: weights once per step, every
+    # sequence's K/V rows, its new K/V row, logits and embedding row.
+    total_bytes = sum(WEIGHT_BYTES + sum(24_576 * (n + 1 + i) + 24_576 + 607_744 + 3_584
+                                         for n in lengths) for i in range(K))
+    step_gbs = total_bytes / wall / 1e9
+    cpu = None
+    if not no_cpu:
+        steps, el, cores = cpu_decode_baseline(BATCH_SEED, lengths, max_steps=32)
+        cpu = {"value": round(steps / el, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+               "sample": f"{steps} single-sequence decode steps cycling over the 16 contexts "
+                         f"(synthetic cached KV), oracle/libqwen_oracle.so FP32 OpenMP"}
+    gemms = ["batch_qkv_kernel", "batch_oproj_kernel", "batch_gateup_kernel",
+             "batch_down_kernel", "batch_lmhead_kernel"]
+    return {
+        "metric": "batched decode tokens/s (16 ragged sequences, Qwen2.5-0.5B-shape FP32) "
+                  "+ % HBM roofline",
+        "value": round(BATCH_ROWS * K / wall, 2),
+        "unit": "tokens/s",
+        "ms_per_step": round(wall * 1e3 / K, 4),
+        "higher_is_better": True,
+        "dtype": "f32",
+        "data": "synthetic: random-init N(0,0.02) weights / N(0,0.01) biases, seed 3; "
+                "16 uniform random prompts of uniform [256, 2048] lengths",
+        "config": {
+            "workload": "BASELINE config 4: 24-layer FP32 model, 16 sequences with ragged "
+                        "contexts decoded together (M=16 skinny GEMMs on FP32 MFMA), greedy "
+                        "feedback",
+            "batch": BATCH_ROWS, "contexts": lengths, "layers": 24, "hidden": 896, "vocab": VOCAB,
+        },
+        "step_hbm": {"achieved_gbs": round(step_gbs, 1), "peak_gbs": HBM_PEAK_GBS,
+                     "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                     "bytes_per_step": round(total_bytes / K)},
+        "roofline": roofline_hbm(name, avg_us, avg_bytes),
+        "mfma": mfma_summary(prof, gemms),
+        "kernels_us": {n: round(v[1], 2) for n, v in prof.items()},
+        "cpu_baseline": cpu,
+        "path": "stream-ordered batched kernels",
+    }
+
+
+def run_prefill(K, W, no_cpu):
+    prompt = stream_tokens(PROMPT, PREFILL_SEED, PROMPT_STREAM, VOCAB)
+    log("engine create + synthetic weights (seed 4)")
+    eng = qd.Engine(capacity=PROMPT + PREFILL_DECODE + 8, max_batch=1)
+    eng.load_synthetic(PREFILL_SEED)
+    for _ in range(W):
+        eng.kv_reset(0, 0)
+        eng.prefill(0, prompt, want_logits=False)
+    log(f"timed {K} prefills of {PROMPT} tokens")
+    eng.sync()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        eng.kv_reset(0, 0)
+        first, _, _ = eng.prefill(0, prompt, want_logits=False)
+    eng.sync()
+    wall = time.perf_counter() - t0
+    # Config 5's decode phase: 128 greedy steps reusing the prompt's cache.
+    eng.sync()
+    t1 = time.perf_counter()
+    toks, _, _ = eng.generate(0, first, PREFILL_DECODE)
+    eng.sync()
+    dec_wall = time.perf_counter() - t1
+    eng.kv_reset(0, 0)
+    prof = eng.profile_prefill(0, prompt)
+    eng.close()
+    log("kernel profile: " + ", ".join(f"{n}={v[1]:.1f}us" for n, v in prof.items()))
+    gemms = [n for n in prof if n.startswith("gemm_nt_kernel")]
+    mf = mfma_summary(prof, gemms)
+    g_us = sum(prof[n][0] * prof[n][1] for n in gemms)
+    g_fl = sum(prof[n][0] * prof[n][3] for n in gemms)
+    flops = sum(v[0] * v[3] for v in prof.values())
+    cpu = None
+    if not no_cpu:
+        el, cores = cpu_prefill_baseline(PREFILL_SEED, 256)
+        cpu = {"value": round(256 / el, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+               "sample": "one 256-token prefill (same model and prompt stream), "
+                         "oracle/libqwen_oracle.so FP32 OpenMP"}
+    return {
+        "metric": "prefill tokens/s (512-token prompt, Qwen2.5-0.5B-shape FP32) "
+                  "+ % FP32 MFMA roofline",
+        "value": round(PROMPT * K / wall, 2),
+        "unit": "tokens/s",
+        "ms_per_step": round(wall * 1e3 / K, 4),
+        "higher_is_better": True,
+        "dtype": "f32",
+        "data": "synthetic: random-init N(0,0.02) weights / N(0,0.01) biases, seed 4; "
+                "512 uniform random prompt tokens",
+        "config": {
+            "workload": "BASELINE config 5: 512-token prefill (dense M=512 GEMMs on FP32 MFMA + "
+                        "causal GQA attention), then 128 greedy decode steps",
+            "prompt": PROMPT, "layers": 24, "hidden": 896, "vocab": VOCAB,
+        },
+        "roofline": {"bound": "mfma", "kernel": "gemm_nt_kernel (all projections)",
+                     "achieved": round(g_fl / (g_us * 1e-6) / 1e12, 2),
+                     "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": mf["frac"], "traffic": None,
+                     "avg_us": round(g_us / sum(prof[n][0] for n in gemms), 3),
+                     "flops_per_prefill": round(g_fl)},
+        "prefill_flops": round(flops),
+        "kernels_us": {n: round(v[1], 2) for n, v in prof.items()},
+        "decode_after_prefill": {"steps": len(toks),
+                                 "tokens_per_s": round(len(toks) / dec_wall, 2)},
+        "cpu_baseline": cpu,
+        "path": "MFMA prompt path",
+    }
+
+
+def copy_probe(mib: int):
+    """Copies `mib` MiB device-to-device through the HIP runtime: a plain copy
+    kernel of known size whose FETCH_SIZE / WRITE_SIZE counters calibrate the
+    per-dispatch HBM traffic of the decode kernel in the same profile."""
+    import ctypes as C
+
+    hip = C.CDLL("libamdhip64.so")
+    n = mib << 20
+    src, dst = C.c_void_p(), C.c_void_p()
+    for p in (src, dst):
+        if hip.hipMalloc(C.byref(p), C.c_size_t(n)) != 0:
+            raise RuntimeError("hipMalloc failed")
+    hip.hipMemset(src, 1, C.c_size_t(n))
+    for _ in range(3):
+        hip.hipMemcpy(dst, src, C.c_size_t(n), 3)  # device to device
+    hip.hipDeviceSynchronize()
+    hip.hipFree(src)
+    hip.hipFree(dst)
+    log(f"copy probe: 3 x {mib} MiB device-to-device")
+
+
+DEFAULTS = {"decode": (64, 8), "batch16": (32, 4), "prefill": (20, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", choices=sorted(DEFAULTS), default="decode")
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB (PMC calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for {args.gpus}); the decode path "
+              "has no multi-GPU mode in this build", file=sys.stderr)
+        sys.exit(2)
+    K = args.steps if args.steps is not None else DEFAULTS[args.workload][0]
+    W = args.warmup if args.warmup is not None else DEFAULTS[args.workload][1]
+    if K <= 0:
+        sys.exit("--steps must be positive")
+    run = {"decode": run_decode, "batch16": run_batch16, "prefill": run_prefill}[args.workload]
+    out = run(K, W, args.no_cpu)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+    line = {"metric": out.pop("metric"), "value": out.pop("value"), "unit": out.pop("unit"),
+            "n_gpus": 1, "steps": K, "warmup": W, "ms_per_step": out.pop("ms_per_step"),
+            "higher_is_better": out.pop("higher_is_better"), "scaling": "weak",
+            "vs_baseline": None}
+    line.update(out)
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

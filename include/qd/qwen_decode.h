@@ -101,8 +101,9 @@ typedef struct qd_timing {
   uint32_t reserved;
 } qd_timing;
 
-/* Per-kernel totals from qd_profile_kernels: summed HIP-event durations and
- * summed algorithmic bytes (bytes the kernel must move at minimum) of its
+/* Per-kernel totals from the qd_profile_* calls: summed HIP-event durations,
+ * summed algorithmic bytes (bytes the kernel must move at minimum) and
+ * summed floating-point operations (a multiply-add counts 2) of its
  * launches. */
 typedef struct qd_kernel_stat {
   char name[48];
@@ -110,6 +111,7 @@ typedef struct qd_kernel_stat {
   uint32_t reserved;
   double total_us;
   double bytes;
+  double flops;
 } qd_kernel_stat;
 
 typedef struct qd_engine qd_engine;
@@ -233,6 +235,25 @@ QD_API qd_status qd_generate_resident(qd_engine *engine, uint32_t seq,
  * byte model, qwen_stateful_graph_kernel.cpp:837-865 stage timing). */
 QD_API qd_status qd_profile_kernels(qd_engine *engine, uint32_t seq,
                                     uint32_t first_token, uint32_t tokens,
+                                    qd_kernel_stat *stats, uint32_t capacity,
+                                    uint32_t *count);
+
+/* Runs `steps` qd_step_batch steps of the n_seq listed slots (greedy
+ * tokens fed back between steps, starting from `tokens`) with a HIP event
+ * pair around every kernel launch, and reports per-kernel totals. Advances
+ * each slot by `steps` positions. No reference counterpart: the reference
+ * decodes one sequence at a time (examples/qwen/README.md:431-432). */
+QD_API qd_status qd_profile_batch(qd_engine *engine, uint32_t n_seq,
+                                  const uint32_t *seq_ids, const uint32_t *tokens,
+                                  uint32_t steps, qd_kernel_stat *stats,
+                                  uint32_t capacity, uint32_t *count);
+
+/* Runs qd_prefill of the n tokens with a HIP event pair around every kernel
+ * launch (the prompt GEMMs by projection) and reports per-kernel totals;
+ * leaves the slot as qd_prefill does. The reference's Triton prompt path
+ * (benchmarks/triton_mini_decoder_layer.cpp:817-834) has no profile. */
+QD_API qd_status qd_profile_prefill(qd_engine *engine, uint32_t seq,
+                                    const uint32_t *tokens, uint32_t n,
                                     qd_kernel_stat *stats, uint32_t capacity,
                                     uint32_t *count);
 

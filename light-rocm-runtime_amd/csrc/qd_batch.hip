@@ -73,18 +73,25 @@ __device__ __forceinline__ void load_operand(const float *__restrict__ x, int ro
   for (int s = 0; s < kSteps; ++s) xa[s] = ld4(row + k0 + kStep * s);
 }
 
+// The gain slice matching load_operand's k offsets.
+template <int kSteps>
+__device__ __forceinline__ void load_gain(int kbase, const float *__restrict__ gain,
+                                          float4 (&gv)[kSteps]) {
+  const int k0 = kbase + k_quad();
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) gv[s] = ld4(gain + k0 + kStep * s);
+}
+
 // RMSNorm folded into the GEMM: y = x * inv * g gives W.y = inv * W.(x g),
 // so the matrix cores take x * g and the epilogue scales by the row's inv.
 // Returns this lane's contribution to the sum of squares of its row and
 // scales the slice by the gain in place.
 template <int kSteps>
-__device__ __forceinline__ float gain_operand(int kbase, const float *__restrict__ gain,
-                                              float4 (&xa)[kSteps]) {
-  const int k0 = kbase + k_quad();
+__device__ __forceinline__ float gain_operand(const float4 (&gv)[kSteps], float4 (&xa)[kSteps]) {
   float ss = 0.f;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    const float4 g = ld4(gain + k0 + kStep * s);
+    const float4 g = gv[s];
     float4 &x = xa[s];
     ss = fmaf(x.x, x.x, ss);
     ss = fmaf(x.y, x.y, ss);
@@ -112,20 +119,29 @@ __device__ __forceinline__ void rows_sum_squares(float part, float (*wss)[16], f
   __syncthreads();
 }
 
-// acc += X[:, kbase..] . W[row, kbase..]^T over kSteps steps (row = this
-// lane's weight row, K floats per row).
+// This lane's weight slice for kSteps k-steps from kbase of row wrow (K
+// floats per row): float4 s at k = kbase + 16 s + 4 (lane / 16).
 template <int kSteps>
-__device__ __forceinline__ f4v tile_mfma(const float *__restrict__ wrow, int kbase,
-                                         const float4 (&xa)[kSteps], f4v acc) {
-  float4 wv[kSteps];
+__device__ __forceinline__ void load_weights(const float *__restrict__ wrow, int kbase,
+                                             float4 (&wv)[kSteps]) {
   const int k0 = kbase + k_quad();
 #pragma unroll
   for (int s = 0; s < kSteps; ++s)
     wv[s] = ld_weight(reinterpret_cast<const float4 *>(wrow + k0 + kStep * s));
+}
+
+// acc += X[:, k slice] . W[row, k slice]^T from the loaded slices.
+template <int kSteps>
+__device__ __forceinline__ f4v tile_mfma(const float4 (&xa)[kSteps], const float4 (&wv)[kSteps],
+                                         f4v acc) {
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) acc = mfma4(xa[s], wv[s], acc);
   return acc;
 }
+
+// Keeps the compiler from moving any instruction across this point: placed
+// after a kernel's loads so all of them are in flight before the first wait.
+__device__ __forceinline__ void issue_fence() { __builtin_amdgcn_sched_barrier(0); }
 
 // Sums the waves' partial tiles: red is [waves][4][64]; thread t < 256
 // returns element (register t / 64, lane t % 64), i.e. sequence
@@ -162,10 +178,10 @@ __device__ __forceinline__ void wait_vm_stores() { __builtin_amdgcn_s_waitcnt(0x
 // XCDs' L2s without an L2 writeback or invalidate; each depositing thread
 // waits for its stores to complete before the workgroup's arrival is counted.
 constexpr int kSplitRec = 256 + 16;
-template <bool kSsq>
-__device__ bool split_gather(float &v, float *ss, float *__restrict__ ws, uint32_t *cnt, int tile,
-                             int splits) {
+template <int kSplits, bool kSsq>
+__device__ bool split_gather(float &v, float *ss, float *__restrict__ ws, uint32_t *cnt, int tile) {
   __shared__ uint32_t last;
+  constexpr int splits = kSplits;
   const int t = threadIdx.x;
   if (splits == 1) return true;
   const Coherent dep(ws + static_cast<size_t>(tile) * splits * kSplitRec,
@@ -178,10 +194,18 @@ __device__ bool split_gather(float &v, float *ss, float *__restrict__ ws, uint32
   if (t == 0) last = atomicAdd(cnt + tile, 1u) == static_cast<uint32_t>(splits - 1);
   __syncthreads();
   if (!last) return false;
+  // All deposits are requested before any is summed (one round trip).
+  float pv[kSplits], pq[kSplits];
+#pragma unroll
+  for (int s = 0; s < kSplits; ++s) {
+    pv[s] = t < 256 ? dep.ld(s * kSplitRec + t) : 0.f;
+    pq[s] = kSsq && t < 16 ? dep.ld(s * kSplitRec + 256 + t) : 0.f;
+  }
   float sum = 0.f, sq = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    if (t < 256) sum += dep.ld(s * kSplitRec + t);
-    if (kSsq && t < 16) sq += dep.ld(s * kSplitRec + 256 + t);
+#pragma unroll
+  for (int s = 0; s < kSplits; ++s) {
+    sum += pv[s];
+    sq += pq[s];
   }
   v = sum;
   if (kSsq) {
@@ -219,7 +243,7 @@ __global__ __launch_bounds__(kBlock) void batch_embed_kernel(BatchLaunch p,
 // j + 8: the rotate-half partners sit in lanes l and l ^ 8. Heads [0, nq)
 // are queries, then nkv keys, then nkv values (not rotated). K = 896 is
 // split over kSplit workgroups of four waves.
-constexpr int kQkvSplit = 2;
+constexpr int kQkvSplit = 1;
 __global__ __launch_bounds__(kBlock) void batch_qkv_kernel(BatchLaunch p, const float *__restrict__ gain,
                                                            const float *__restrict__ wqkv,
                                                            const float *__restrict__ bqkv, int layer) {
@@ -231,32 +255,40 @@ __global__ __launch_bounds__(kBlock) void batch_qkv_kernel(BatchLaunch p, const 
   const int head = tile >> 2;
   const int i0 = (tile & 3) * 8;
   const int kbase = (blockIdx.y * kWavesPerBlock + wave_id()) * kSteps * kStep;
-  float4 xa[kSteps];
-  load_operand<kSteps, kH>(p.hidden, p.rows, kbase, xa);
-  const float part = gain_operand<kSteps>(kbase, gain, xa);
   const int j = tile_col();
   const int wrow = head * kHeadDim + (j < 8 ? i0 + j : kRotary + i0 + j - 8);
-  f4v acc = {0.f, 0.f, 0.f, 0.f};
-  acc = tile_mfma<kSteps>(wqkv + static_cast<size_t>(wrow) * kH, kbase, xa, acc);
-  rows_sum_squares(part, wss, ss);
-  float v = tile_reduce<kWavesPerBlock>(acc, red);
-  if (!split_gather<true>(v, ss, p.split, p.counters + kCntQkv, tile, kQkvSplit)) return;
-  // Epilogue over the 256 tile elements.
+  // Epilogue element of this thread: its bias and rotation are requested
+  // with the weights.
   const int t = threadIdx.x;
   const int seq = tile_seq(t);
   const int jt = t & 15;
   const int i = i0 + (jt & 7);
   const int row = head * kHeadDim + (jt < 8 ? i : kRotary + i);
-  v = v * rsqrtf(ss[seq] / static_cast<float>(kH) + p.eps) + bqkv[row];
+  const int pos = static_cast<int>(p.pos[min(seq, p.rows - 1)]);
+  const float bias = bqkv[row];
+  const float c = p.rope_cos[pos * kRotary + i];
+  const float s = p.rope_sin[pos * kRotary + i];
+  float4 wv[kSteps], xa[kSteps];
+  load_weights<kSteps>(wqkv + static_cast<size_t>(wrow) * kH, kbase, wv);
+  float4 gv[kSteps];
+  load_operand<kSteps, kH>(p.hidden, p.rows, kbase, xa);
+  load_gain<kSteps>(kbase, gain, gv);
+  issue_fence();
+  const float part = gain_operand<kSteps>(gv, xa);
+  f4v acc = {0.f, 0.f, 0.f, 0.f};
+  acc = tile_mfma<kSteps>(xa, wv, acc);
+  rows_sum_squares(part, wss, ss);
+  float v = tile_reduce<kWavesPerBlock>(acc, red);
+  if (!split_gather<kQkvSplit, true>(v, ss, p.split, p.counters + kCntQkv, tile)) return;
+  // Epilogue over the 256 tile elements.
+  const float v0 = v;
+  v = v0 * rsqrtf(ss[seq] / static_cast<float>(kH) + p.eps) + bias;
   const float other = __shfl_xor(v, 8, kWave);
   if (seq >= p.rows) return;
   const uint32_t slot = p.slot[seq];
-  const int pos = static_cast<int>(p.pos[seq]);
   const int kv_dim = p.nkv * kHeadDim;
   const int d = row - head * kHeadDim;
   if (head < p.nq + p.nkv) {
-    const float c = p.rope_cos[pos * kRotary + i];
-    const float s = p.rope_sin[pos * kRotary + i];
     // (a, b) = (row i, row i + 32): a' = a c - b s, b' = b c + a s.
     const float out = jt < 8 ? v * c - other * s : v * c + other * s;
     if (head < p.nq) {
@@ -271,66 +303,210 @@ __global__ __launch_bounds__(kBlock) void batch_qkv_kernel(BatchLaunch p, const 
   }
 }
 
-// Split-KV attention: workgroup (chunk, query head, batch row) computes its
-// chunk's online-softmax partial; the last chunk of a (row, head) to finish
-// merges every chunk's partial into attn[b][h*64 + d].
+// Sum / max over the 16 lanes of a DPP row (lanes 16q .. 16q+15); every
+// lane of the row receives the result.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  return v;
+}
+
+// GQA decode attention on the matrix cores: workgroup (chunk, KV group g,
+// batch row b) serves all query heads of the group (up to 16), so every K/V
+// row of the chunk is read once. Waves take 16-position tiles (wave w: tile
+// w of each 64-position pass). Per tile:
+//   S[head][pos] = (Q / 8) . K^T    16x16x4 MFMAs, lane l supplies
+//                                   Q[head l%16] and K[pos l%16] at dims
+//                                   16 s + 4 (l/16) + c (float4 loads)
+//   online softmax per head row     (S register r of lane l is head
+//                                   4 (l/16) + r, position l%16: row
+//                                   reductions over the 16-lane DPP rows)
+//   O[head][d] += P . V             P and the V tile go through the wave's
+//                                   LDS to become MFMA A / B operands.
+// The four wave partials are merged into one record (m, l, acc[64]) per
+// head; the last chunk of (b, g) to finish merges all chunks (the same
+// merge as attn_merge) into attn[b][h*64 + d]. Scaling Q by 1/8 is exact,
+// so scores equal (q . k) / sqrt(64).
+struct GqaLds {
+  float ps[kWavesPerBlock][16][17];   // P tile [head][pos]
+  float vs[kWavesPerBlock][16][68];   // V tile [pos][dim]
+  float wm[kWavesPerBlock][16];
+  float wl[kWavesPerBlock][16];
+  float wo[kWavesPerBlock][16][65];   // wave partial O [head][dim]
+};
+
 __global__ __launch_bounds__(kBlock) void batch_attn_kernel(BatchLaunch p, int layer) {
-  __shared__ AttnLds sh;
+  __shared__ GqaLds sh;
   __shared__ uint32_t last;
-  const int b = blockIdx.z;
+  const int b = blockIdx.z, g = blockIdx.y, chunk = blockIdx.x;
   const uint32_t slot = p.slot[b];
   const int position = static_cast<int>(p.pos[b]);
   const int length = position + 1;
-  const int chunk = blockIdx.x;
   const int chunks = attn_chunks(length);
   if (chunk >= chunks) return;
   const int chunk_len = attn_chunk_len(length);
-  const int h = blockIdx.y;
-  const int g = h / (p.nq / p.nkv);
-  const int kv_dim = p.nkv * kHeadDim;
   const int begin = chunk * chunk_len;
   const int end = min(length, begin + chunk_len);
-  const float *kbase = kv_rows(p.k_cache, slot, layer, p.layers, p.capacity, kv_dim);
-  const float *vbase = kv_rows(p.v_cache, slot, layer, p.layers, p.capacity, kv_dim);
-  const Plain kc(kbase), vc(vbase);
-  const Plain knew(kbase + static_cast<size_t>(position) * kv_dim);
-  const Plain vnew(vbase + static_cast<size_t>(position) * kv_dim);
-  const float *q = p.q + b * (p.nq * kHeadDim) + h * kHeadDim;
-  // Chunk records of this (row, head), written and read at device scope.
-  const Coherent recs(p.part + (static_cast<size_t>(b) * p.nq + h) * kAttnMaxChunks * kPartStride,
-                      kAttnMaxChunks * kPartStride * sizeof(float));
-  attn_partial_unit<kWavesPerBlock>(
-      kc, vc, knew, vnew, position, g, kv_dim, begin, end, sh,
-      [&](auto request_rows) {
-        request_rows();
-        if (threadIdx.x < kHeadDim) sh.qkv[threadIdx.x] = q[threadIdx.x];
-        __syncthreads();
-      },
-      [&](float m, float l, float acc, int d) {
-        const uint32_t rec = chunk * kPartStride;
-        recs.st(rec + 2 + d, acc);
-        if (d == 0) {
-          recs.st(rec, m);
-          recs.st(rec + 1, l);
-        }
-        wait_vm_stores();
-      });
+  const int group = p.nq / p.nkv;
+  const int kv_dim = p.nkv * kHeadDim;
+  const float *kb = kv_rows(p.k_cache, slot, layer, p.layers, p.capacity, kv_dim) + g * kHeadDim;
+  const float *vb = kv_rows(p.v_cache, slot, layer, p.layers, p.capacity, kv_dim) + g * kHeadDim;
+  const int w = wave_id(), col = tile_col(), quad = lane_id() >> 4;
+  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+
+  float4 qa[4];
+  if (col < group) {
+    const float *qr = p.q + b * (p.nq * kHeadDim) + (g * group + col) * kHeadDim + 4 * quad;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float4 v = ld4(qr + 16 * s);
+      qa[s] = make_float4(v.x * 0.125f, v.y * 0.125f, v.z * 0.125f, v.w * 0.125f);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qa[s] = zero;
+  }
+  auto load_tile = [&](int p0, float4 (&kr)[4], float4 (&vr)[4]) {
+    const int pos = p0 + col;
+    if (pos < end) {
+      const size_t off = static_cast<size_t>(pos) * kv_dim + 4 * quad;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        kr[s] = ld4(kb + off + 16 * s);
+        vr[s] = ld4(vb + off + 16 * s);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kr[s] = vr[s] = zero;
+    }
+  };
+
+  float m[4], lsum[4];
+  f4v o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m[r] = -INFINITY;
+    lsum[r] = 0.f;
+    o[r] = f4v{0.f, 0.f, 0.f, 0.f};
+  }
+  float4 kc[4], vc[4];
+  load_tile(begin + 16 * w, kc, vc);
+  for (int base = begin; base < end; base += kAttnPass) {
+    const int p0 = base + 16 * w;
+    float4 kn[4], vn[4];
+    if (base + kAttnPass < end) load_tile(p0 + kAttnPass, kn, vn);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      *reinterpret_cast<float4 *>(&sh.vs[w][col][16 * s + 4 * quad]) = vc[s];
+    f4v sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) sacc = mfma4(qa[s], kc[s], sacc);
+    const bool valid = p0 + col < end;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float sv = valid ? sacc[r] : -INFINITY;
+      const float mn = fmaxf(m[r], row16_max(sv));
+      const float pv = mn == -INFINITY ? 0.f : expf(sv - mn);
+      const float corr = mn == -INFINITY ? 1.f : expf(m[r] - mn);
+      lsum[r] = fmaf(lsum[r], corr, row16_sum(pv));
+      m[r] = mn;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) o[n][r] *= corr;
+      sh.ps[w][4 * quad + r][col] = pv;
+    }
+    // The wave's own LDS tiles: LDS operations of a wave complete in order.
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float a = sh.ps[w][col][4 * s + quad];
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, sh.vs[w][4 * s + quad][16 * n + col], o[n],
+                                                     0, 0, 0);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      kc[s] = kn[s];
+      vc[s] = vn[s];
+    }
+  }
+  // Wave partials -> one record per head of the group.
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (col == 0) {
+      sh.wm[w][4 * quad + r] = m[r];
+      sh.wl[w][4 * quad + r] = lsum[r];
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) sh.wo[w][4 * quad + r][16 * n + col] = o[n][r];
+  }
   __syncthreads();
-  uint32_t *cnt = p.counters + kCntAttn + b * p.nq + h;
+  const Coherent recs(p.part + (static_cast<size_t>(b) * p.nq + g * group) * kAttnMaxChunks * kPartStride,
+                      group * kAttnMaxChunks * kPartStride * sizeof(float));
+  for (int i = threadIdx.x; i < group * kHeadDim; i += kBlock) {
+    const int h = i / kHeadDim, d = i % kHeadDim;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kWavesPerBlock; ++v) mx = fmaxf(mx, sh.wm[v][h]);
+    float lt = 0.f, a = 0.f;
+#pragma unroll
+    for (int v = 0; v < kWavesPerBlock; ++v) {
+      const float f = sh.wm[v][h] == -INFINITY ? 0.f : expf(sh.wm[v][h] - mx);
+      lt = fmaf(f, sh.wl[v][h], lt);
+      a = fmaf(f, sh.wo[v][h][d], a);
+    }
+    const uint32_t rec = (h * kAttnMaxChunks + chunk) * kPartStride;
+    recs.st(rec + 2 + d, a);
+    if (d == 0) {
+      recs.st(rec, mx);
+      recs.st(rec + 1, lt);
+    }
+  }
+  wait_vm_stores();
+  __syncthreads();
+  uint32_t *cnt = p.counters + kCntAttn + b * p.nkv + g;
   if (threadIdx.x == 0) last = atomicAdd(cnt, 1u) == static_cast<uint32_t>(chunks - 1);
   __syncthreads();
   if (!last) return;
-  if (threadIdx.x < kHeadDim) {
-    const int d = threadIdx.x;
-    p.attn[b * (p.nq * kHeadDim) + h * kHeadDim + d] =
-        attn_merge([&](int c, int k) { return recs.ld(c * kPartStride + k); }, chunks, d);
+  for (int i = threadIdx.x; i < group * kHeadDim; i += kBlock) {
+    const int h = i / kHeadDim, d = i % kHeadDim;
+    const uint32_t head_rec = h * kAttnMaxChunks * kPartStride;
+    // Every chunk's (m, l, acc_d) is requested before any is used.
+    float cm[kAttnMaxChunks], cl[kAttnMaxChunks], ca[kAttnMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kAttnMaxChunks; ++c) {
+      const uint32_t rec = head_rec + c * kPartStride;
+      const bool in = c < chunks;
+      cm[c] = in ? recs.ld(rec) : -INFINITY;
+      cl[c] = in ? recs.ld(rec + 1) : 0.f;
+      ca[c] = in ? recs.ld(rec + 2 + d) : 0.f;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kAttnMaxChunks; ++c) mx = fmaxf(mx, cm[c]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int c = 0; c < kAttnMaxChunks; ++c) {
+      const float f = c < chunks ? expf(cm[c] - mx) : 0.f;
+      den = fmaf(f, cl[c], den);
+      num = fmaf(f, ca[c], num);
+    }
+    p.attn[b * (p.nq * kHeadDim) + (g * group + h) * kHeadDim + d] = num / den;
   }
   if (threadIdx.x == 0) *cnt = 0u;
 }
 
 // hidden[b][row] += Wo[row] . attn[b] for the 16 rows of tile blockIdx.x;
 // K = 896 split over kOSplit workgroups.
-constexpr int kOSplit = 2;
+constexpr int kOSplit = 1;
 __global__ __launch_bounds__(kBlock) void batch_oproj_kernel(BatchLaunch p,
                                                              const float *__restrict__ wo) {
   constexpr int kSteps = kH / kStep / kWavesPerBlock / kOSplit;  // 7
@@ -338,12 +514,14 @@ __global__ __launch_bounds__(kBlock) void batch_oproj_kernel(BatchLaunch p,
   const int tile = blockIdx.x;
   const int n0 = tile * 16;
   const int kbase = (blockIdx.y * kWavesPerBlock + wave_id()) * kSteps * kStep;
-  float4 xa[kSteps];
+  float4 wv[kSteps], xa[kSteps];
+  load_weights<kSteps>(wo + static_cast<size_t>(n0 + tile_col()) * kH, kbase, wv);
   load_operand<kSteps, kH>(p.attn, p.rows, kbase, xa);
+  issue_fence();
   f4v acc = {0.f, 0.f, 0.f, 0.f};
-  acc = tile_mfma<kSteps>(wo + static_cast<size_t>(n0 + tile_col()) * kH, kbase, xa, acc);
+  acc = tile_mfma<kSteps>(xa, wv, acc);
   float v = tile_reduce<kWavesPerBlock>(acc, red);
-  if (!split_gather<false>(v, nullptr, p.split, p.counters + kCntO, tile, kOSplit)) return;
+  if (!split_gather<kOSplit, false>(v, nullptr, p.split, p.counters + kCntO, tile)) return;
   const int t = threadIdx.x;
   const int seq = tile_seq(t);
   if (seq < p.rows) p.hidden[seq * kH + n0 + (t & 15)] += v;
@@ -360,13 +538,18 @@ __global__ __launch_bounds__(kBlock) void batch_gateup_kernel(BatchLaunch p,
   __shared__ float red[kWavesPerBlock][4][kWave];
   const int n0 = blockIdx.x * 16;
   const int kbase = wave_id() * kSteps * kStep;
-  float4 xa[kSteps];
-  load_operand<kSteps, kH>(p.hidden, p.rows, kbase, xa);
-  const float part = gain_operand<kSteps>(kbase, gain, xa);
   const size_t wrow = static_cast<size_t>(n0 + tile_col()) * kH;
+  float4 wgv[kSteps], wuv[kSteps], xa[kSteps];
+  load_weights<kSteps>(wg + wrow, kbase, wgv);
+  load_weights<kSteps>(wu + wrow, kbase, wuv);
+  float4 gv[kSteps];
+  load_operand<kSteps, kH>(p.hidden, p.rows, kbase, xa);
+  load_gain<kSteps>(kbase, gain, gv);
+  issue_fence();
+  const float part = gain_operand<kSteps>(gv, xa);
   f4v ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-  ag = tile_mfma<kSteps>(wg + wrow, kbase, xa, ag);
-  au = tile_mfma<kSteps>(wu + wrow, kbase, xa, au);
+  ag = tile_mfma<kSteps>(xa, wgv, ag);
+  au = tile_mfma<kSteps>(xa, wuv, au);
   rows_sum_squares(part, wss, ss);
   const float g0 = tile_reduce<kWavesPerBlock>(ag, red);
   const float u0 = tile_reduce<kWavesPerBlock>(au, red);
@@ -387,12 +570,14 @@ __global__ __launch_bounds__(kBlock) void batch_down_kernel(BatchLaunch p,
   const int tile = blockIdx.x;
   const int n0 = tile * 16;
   const int kbase = (blockIdx.y * kWavesPerBlock + wave_id()) * kSteps * kStep;
-  float4 xa[kSteps];
+  float4 wv[kSteps], xa[kSteps];
+  load_weights<kSteps>(wd + static_cast<size_t>(n0 + tile_col()) * kI, kbase, wv);
   load_operand<kSteps, kI>(p.act, p.rows, kbase, xa);
+  issue_fence();
   f4v acc = {0.f, 0.f, 0.f, 0.f};
-  acc = tile_mfma<kSteps>(wd + static_cast<size_t>(n0 + tile_col()) * kI, kbase, xa, acc);
+  acc = tile_mfma<kSteps>(xa, wv, acc);
   float v = tile_reduce<kWavesPerBlock>(acc, red);
-  if (!split_gather<false>(v, nullptr, p.split, p.counters + kCntDown, tile, kDownSplit)) return;
+  if (!split_gather<kDownSplit, false>(v, nullptr, p.split, p.counters + kCntDown, tile)) return;
   const int t = threadIdx.x;
   const int seq = tile_seq(t);
   if (seq < p.rows) p.hidden[seq * kH + n0 + (t & 15)] += v;
@@ -419,9 +604,10 @@ __global__ __launch_bounds__(kBlock) void batch_lmhead_kernel(BatchLaunch p, Bat
   float4 wcur[kSteps];
   int tile = blockIdx.x;
   if (tile < tiles) load_tile(tile, wcur);
-  float4 xa[kSteps];
+  float4 xa[kSteps], gv[kSteps];
   load_operand<kSteps, kH>(p.hidden, p.rows, kbase, xa);
-  const float part = gain_operand<kSteps>(kbase, tl.final_norm, xa);
+  load_gain<kSteps>(kbase, tl.final_norm, gv);
+  const float part = gain_operand<kSteps>(gv, xa);
   rows_sum_squares(part, wss, ss);
   const int t = threadIdx.x;
   const int seq = tile_seq(t);
@@ -570,7 +756,7 @@ hipError_t launch_batch_layer(hipStream_t s, const BatchLaunch &b, const LayerPt
   }
   {
     Scope scope(m, kBAttn);
-    batch_attn_kernel<<<dim3(kAttnMaxChunks, b.nq, b.rows), kBlock, 0, s>>>(b, layer);
+    batch_attn_kernel<<<dim3(kAttnMaxChunks, b.nkv, b.rows), kBlock, 0, s>>>(b, layer);
   }
   {
     Scope scope(m, kBOproj);

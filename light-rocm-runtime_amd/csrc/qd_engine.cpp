@@ -33,7 +33,7 @@
 
 namespace {
 
-constexpr uint32_t kAbiVersion = 1;
+constexpr uint32_t kAbiVersion = 2;
 constexpr int kLmHeadParts = 1024;  // LM-head workgroups = top-1 partials
 
 thread_local std::string g_error;
@@ -370,6 +370,73 @@ struct qd_engine {
     check(qd::launch_batch_tail(stream, b, batch_tail(first), m), "batch tail launch");
   }
 
+  // Floating-point operations of one launch of `kernel` (multiply-add = 2).
+  double kernel_flops(int kernel, double length) const {
+    switch (kernel) {
+      case qd::kKQkvRope: return 2.0 * QKV * H;
+      case qd::kKAttnPartial: return 4.0 * NQ * qd::kHeadDim * length;
+      case qd::kKOproj: return 2.0 * H * QD;
+      case qd::kKGateUp: return 4.0 * I * H;
+      case qd::kKDown: return 2.0 * H * I;
+      case qd::kKLmHead: return 2.0 * V * H;
+    }
+    return 0;
+  }
+
+  // Algorithmic bytes and flops of one batched-step launch over `rows`
+  // sequences attending over `attended` positions in total.
+  std::pair<double, double> batch_cost(int kernel, double rows, double attended) const {
+    const double f = 4.0;
+    switch (kernel) {
+      case qd::kBEmbed: return {2 * rows * H * f, 0};
+      case qd::kBQkvRope: return {(QKV * H + QKV + H + rows * (H + QD + 2 * KVD)) * f, 2 * rows * QKV * H};
+      case qd::kBAttn:
+        return {(2 * attended * KVD + 2 * rows * QD) * f, 4 * NQ * qd::kHeadDim * attended};
+      case qd::kBOproj: return {(H * QD + rows * (QD + 2 * H)) * f, 2 * rows * H * QD};
+      case qd::kBGateUp: return {(2 * I * H + H + rows * (H + I)) * f, 4 * rows * I * H};
+      case qd::kBDown: return {(H * I + rows * (I + 2 * H)) * f, 2 * rows * H * I};
+      case qd::kBLmHead: return {(V * H + H + rows * (H + V)) * f, 2 * rows * V * H};
+      case qd::kBArgmax: return {rows * 2 * qd::kBatchLmParts * f, 0};
+    }
+    return {0, 0};
+  }
+
+  // Kernels of the prompt path, for per-kernel event timing.
+  enum PrefillKernel : int {
+    kPEmbed = 0, kPNorm, kPGemmQkv, kPRope, kPAttn, kPGemmO, kPGemmGateUp, kPSilu, kPGemmDown,
+    kPTail, kPrefillKernels
+  };
+  static const char *prefill_kernel_name(int id) {
+    static const char *const names[kPrefillKernels] = {
+        "embed_rows_kernel",    "rmsnorm_rows_kernel",      "gemm_nt_kernel:qkv",
+        "rope_kv_rows_kernel",  "attention_prefill_kernel", "gemm_nt_kernel:o",
+        "gemm_nt_kernel:gateup", "silu_mul_rows_kernel",    "gemm_nt_kernel:down",
+        "lmhead_kernel+argmax"};
+    return id >= 0 && id < kPrefillKernels ? names[id] : "unknown";
+  }
+
+  // Algorithmic bytes and flops of one prompt-path launch for a chunk of n
+  // rows at positions pos0..: each operand and result moved once; GEMMs
+  // that accumulate read and write C.
+  std::pair<double, double> prefill_cost(int kernel, double n, double pos0) const {
+    const double f = 4.0;
+    switch (kernel) {
+      case kPEmbed: return {2 * n * H * f, 0};
+      case kPNorm: return {(2 * n * H + H) * f, 0};
+      case kPGemmQkv: return {(QKV * H + QKV + n * (H + QKV)) * f, 2 * n * QKV * H};
+      case kPRope: return {n * (2 * QD + 4 * KVD) * f, 0};
+      case kPAttn:
+        return {(2 * (pos0 + n) * KVD + 2 * n * QD) * f,
+                4 * NQ * qd::kHeadDim * (n * pos0 + n * (n + 1) / 2)};
+      case kPGemmO: return {(H * QD + n * (QD + 2 * H)) * f, 2 * n * H * QD};
+      case kPGemmGateUp: return {(2 * I * H + n * (H + 2 * I)) * f, 4 * n * I * H};
+      case kPSilu: return {3 * n * I * f, 0};
+      case kPGemmDown: return {(H * I + n * (I + 2 * H)) * f, 2 * n * H * I};
+      case kPTail: return {(V * H + H + V) * f, 2 * V * H};
+    }
+    return {0, 0};
+  }
+
   bool wg_wu_adjacent() const {
     for (const auto &w : layers)
       if (w.wu != w.wg + I * H) return false;
@@ -379,7 +446,7 @@ struct qd_engine {
   // One chunk of a prompt (n <= kPrefillRows tokens at positions
   // pos0 .. pos0 + n - 1 of slot seq) through every layer with the prompt
   // kernels; leaves the final hidden rows in pf_h.
-  void prefill_chunk(uint32_t seq, const uint32_t *tokens, int n, int pos0) {
+  void prefill_chunk(uint32_t seq, const uint32_t *tokens, int n, int pos0, qd::Marker *m = nullptr) {
     if (!pf_h) {
       pf_h = alloc<float>(kPrefillRows * H);
       pf_xn = alloc<float>(kPrefillRows * H);
@@ -393,30 +460,45 @@ struct qd_engine {
     check(hipMemcpyAsync(pf_tokens, tokens, size_t(n) * 4, hipMemcpyHostToDevice, stream), "H2D");
     const int h = int(H), in = int(I), qkv = int(QKV), qd = int(QD);
     const int nq = int(NQ), nkv = int(NKV);
-    check(qd::launch_embed_rows(stream, embed, pf_tokens, n, h, pf_h), "embed rows");
+    auto span = [&](int id, const char *what, auto &&launch) {
+      if (m) m->before(id);
+      check(launch(), what);
+      if (m) m->after(id);
+    };
+    span(kPEmbed, "embed rows",
+         [&] { return qd::launch_embed_rows(stream, embed, pf_tokens, n, h, pf_h); });
     for (size_t l = 0; l < L; ++l) {
       const qd::LayerPtrs &w = layers[l];
       float *kc = kv_slice(k_cache, seq, l), *vc = kv_slice(v_cache, seq, l);
-      check(qd::launch_rmsnorm_rows(stream, pf_h, w.attn_norm, cfg.rms_eps, n, pf_xn), "norm");
-      check(qd::launch_gemm_nt(stream, pf_xn, h, w.wqkv, h, pf_qkv, qkv, n, qkv, h, qd::kGemmBias,
-                               w.bqkv, kSplitQkv, pf_split),
-            "qkv gemm");
-      check(qd::launch_rope_kv_rows(stream, pf_qkv, n, pos0, nq, nkv, rope_cos, rope_sin, kc, vc),
-            "rope");
-      check(qd::launch_attention_prefill(stream, pf_qkv, n, pos0, nq, nkv, kc, vc, pf_attn),
-            "attention");
-      check(qd::launch_gemm_nt(stream, pf_attn, qd, w.wo, qd, pf_h, h, n, h, qd,
-                               qd::kGemmAccumulate, nullptr, kSplitO, pf_split),
-            "o gemm");
-      check(qd::launch_rmsnorm_rows(stream, pf_h, w.mlp_norm, cfg.rms_eps, n, pf_xn), "norm");
+      span(kPNorm, "norm",
+           [&] { return qd::launch_rmsnorm_rows(stream, pf_h, w.attn_norm, cfg.rms_eps, n, pf_xn); });
+      span(kPGemmQkv, "qkv gemm", [&] {
+        return qd::launch_gemm_nt(stream, pf_xn, h, w.wqkv, h, pf_qkv, qkv, n, qkv, h, qd::kGemmBias,
+                                  w.bqkv, kSplitQkv, pf_split);
+      });
+      span(kPRope, "rope", [&] {
+        return qd::launch_rope_kv_rows(stream, pf_qkv, n, pos0, nq, nkv, rope_cos, rope_sin, kc, vc);
+      });
+      span(kPAttn, "attention", [&] {
+        return qd::launch_attention_prefill(stream, pf_qkv, n, pos0, nq, nkv, kc, vc, pf_attn);
+      });
+      span(kPGemmO, "o gemm", [&] {
+        return qd::launch_gemm_nt(stream, pf_attn, qd, w.wo, qd, pf_h, h, n, h, qd,
+                                  qd::kGemmAccumulate, nullptr, kSplitO, pf_split);
+      });
+      span(kPNorm, "norm",
+           [&] { return qd::launch_rmsnorm_rows(stream, pf_h, w.mlp_norm, cfg.rms_eps, n, pf_xn); });
       // wg and wu are adjacent in the arena: one GEMM over [gate; up] rows.
-      check(qd::launch_gemm_nt(stream, pf_xn, h, w.wg, h, pf_gu, 2 * in, n, 2 * in, h,
-                               qd::kGemmStore, nullptr),
-            "gate/up gemm");
-      check(qd::launch_silu_mul_rows(stream, pf_gu, n, in, pf_act), "swiglu");
-      check(qd::launch_gemm_nt(stream, pf_act, in, w.wd, in, pf_h, h, n, h, in,
-                               qd::kGemmAccumulate, nullptr, kSplitDown, pf_split),
-            "down gemm");
+      span(kPGemmGateUp, "gate/up gemm", [&] {
+        return qd::launch_gemm_nt(stream, pf_xn, h, w.wg, h, pf_gu, 2 * in, n, 2 * in, h,
+                                  qd::kGemmStore, nullptr);
+      });
+      span(kPSilu, "swiglu",
+           [&] { return qd::launch_silu_mul_rows(stream, pf_gu, n, in, pf_act); });
+      span(kPGemmDown, "down gemm", [&] {
+        return qd::launch_gemm_nt(stream, pf_act, in, w.wd, in, pf_h, h, n, h, in,
+                                  qd::kGemmAccumulate, nullptr, kSplitDown, pf_split);
+      });
     }
   }
 
@@ -1005,38 +1087,154 @@ qd_status qd_step(qd_engine *e, uint32_t seq, uint32_t token, float *logits_out,
   });
 }
 
+namespace {
+
+// Event pair around every launch; durations are read after one sync.
+struct EventMarker : qd::Marker {
+  struct Span {
+    int kernel;
+    size_t begin, end;
+    double bytes, flops;
+  };
+  qd_engine *e;
+  std::vector<hipEvent_t> pool;
+  std::vector<std::pair<int, size_t>> open;  // (kernel, begin event index)
+  std::vector<Span> spans;
+  size_t used = 0;
+  double ctx_a = 0, ctx_b = 0;  // workload of the launches being recorded
+  std::function<std::pair<double, double>(int)> cost;  // (bytes, flops) of one launch
+  explicit EventMarker(qd_engine *engine) : e(engine) {}
+  ~EventMarker() override {
+    for (hipEvent_t ev : pool) (void)hipEventDestroy(ev);
+  }
+  size_t next() {
+    if (used == pool.size()) {
+      hipEvent_t ev;
+      check(hipEventCreate(&ev), "hipEventCreate");
+      pool.push_back(ev);
+    }
+    check(hipEventRecord(pool[used], e->stream), "hipEventRecord");
+    return used++;
+  }
+  void before(int kernel) override { open.emplace_back(kernel, next()); }
+  void after(int kernel) override {
+    const size_t b = open.back().second;
+    open.pop_back();
+    const std::pair<double, double> c = cost ? cost(kernel) : std::pair<double, double>{0, 0};
+    spans.push_back({kernel, b, next(), c.first, c.second});
+  }
+  // Per-kernel totals (after the stream has synchronised), at most capacity.
+  void report(const char *(*name)(int), int kernels, qd_kernel_stat *stats, uint32_t capacity,
+              uint32_t *count) const {
+    std::vector<qd_kernel_stat> agg(kernels);
+    for (int k = 0; k < kernels; ++k) {
+      std::memset(&agg[k], 0, sizeof(qd_kernel_stat));
+      std::snprintf(agg[k].name, sizeof(agg[k].name), "%s", name(k));
+    }
+    for (const Span &sp : spans) {
+      float ms = 0.f;
+      check(hipEventElapsedTime(&ms, pool[sp.begin], pool[sp.end]), "hipEventElapsedTime");
+      qd_kernel_stat &st = agg[sp.kernel];
+      st.launches += 1;
+      st.total_us += ms * 1000.0;
+      st.bytes += sp.bytes;
+      st.flops += sp.flops;
+    }
+    uint32_t n = 0;
+    for (const auto &st : agg) {
+      if (st.launches == 0) continue;
+      if (n < capacity) stats[n] = st;
+      ++n;
+    }
+    *count = std::min(n, capacity);
+  }
+};
+
+// Validates a qd_prefill request.
+void check_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t n) {
+  if (!e || (!tokens && n)) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+  e->check_seq(seq);
+  e->check_loaded();
+  if (n == 0) fail(QD_ERROR_INVALID_ARGUMENT, "empty prompt");
+  if (size_t(e->positions[seq]) + n > e->CAP)
+    fail(QD_ERROR_INVALID_ARGUMENT, "prompt of %u tokens overflows capacity %zu at position %u", n, e->CAP,
+         e->positions[seq]);
+  for (uint32_t i = 0; i < n; ++i)
+    if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u at %u >= vocab", tokens[i], i);
+  e->set_device();
+  if (!e->wg_wu_adjacent()) fail(QD_ERROR_NOT_SUPPORTED, "prefill needs the gate and up weights adjacent");
+}
+
+// The prompt in chunks of up to kPrefillRows positions, each through all
+// layers at once (dense GEMMs); then the tail (final norm, LM head, argmax)
+// on the last position, which advances the slot to pos0 + n. m (nullable)
+// times every launch.
+void run_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t n, EventMarker *m) {
+  for (uint32_t done = 0; done < n;) {
+    const uint32_t rows = std::min<uint32_t>(n - done, uint32_t(qd_engine::kPrefillRows));
+    if (m) {
+      m->ctx_a = rows;
+      m->ctx_b = e->positions[seq] + done;
+    }
+    e->prefill_chunk(seq, tokens + done, int(rows), int(e->positions[seq] + done), m);
+    done += rows;
+    if (done == n)
+      check(hipMemcpyAsync(e->hidden + size_t(seq) * e->H, e->pf_h + size_t(rows - 1) * e->H, e->H * 4,
+                           hipMemcpyDeviceToDevice, e->stream),
+            "D2D");
+    e->sync();  // the next chunk's token upload reuses pf_tokens
+  }
+  e->positions[seq] += n - 1;
+  e->push_state(seq, tokens[n - 1], qd::kModeStep, UINT32_MAX, 0);
+  if (m) m->before(qd_engine::kPTail);
+  check(qd::launch_tail(e->stream, e->tail_args(seq, e->logits + seq * e->V, 0, nullptr), nullptr),
+        "tail launch");
+  if (m) m->after(qd_engine::kPTail);
+  e->positions[seq] += 1;
+}
+
+// Validates a qd_step_batch request.
+void check_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, const uint32_t *tokens,
+                 uint32_t steps) {
+  if (!e || !seq_ids || !tokens) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+  e->check_loaded();
+  if (n_seq == 0 || n_seq > e->B) fail(QD_ERROR_INVALID_ARGUMENT, "n_seq %u out of range", n_seq);
+  std::vector<bool> seen(e->B, false);
+  for (uint32_t i = 0; i < n_seq; ++i) {
+    e->check_seq(seq_ids[i]);
+    if (seen[seq_ids[i]]) fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u listed twice", seq_ids[i]);
+    seen[seq_ids[i]] = true;
+    if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", tokens[i]);
+    if (size_t(e->positions[seq_ids[i]]) + steps > e->CAP)
+      fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full", seq_ids[i]);
+  }
+  e->set_device();
+}
+
+// Enqueues one batched step of the listed slots (groups of kBatchRows) and
+// leaves every row's greedy token and logit in bt_token / bt_top; m
+// (nullable) times every launch.
+void enqueue_step_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, const uint32_t *tokens,
+                        EventMarker *m) {
+  for (uint32_t first = 0; first < n_seq; first += qd::kBatchRows) {
+    const int rows = static_cast<int>(std::min<uint32_t>(qd::kBatchRows, n_seq - first));
+    const qd::BatchLaunch b = e->batch_args(seq_ids + first, tokens + first, rows);
+    if (m) {
+      m->ctx_a = rows;
+      m->ctx_b = 0;
+      for (int i = 0; i < rows; ++i) m->ctx_b += b.pos[i] + 1.0;
+    }
+    e->enqueue_batch(b, first, m);
+  }
+}
+
+}  // namespace
+
 qd_status qd_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t n, float *last_logits,
                      uint32_t *greedy, float *top_logit) {
   return guard([&] {
-    if (!e || (!tokens && n)) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
-    e->check_seq(seq);
-    e->check_loaded();
-    if (n == 0) fail(QD_ERROR_INVALID_ARGUMENT, "empty prompt");
-    if (size_t(e->positions[seq]) + n > e->CAP)
-      fail(QD_ERROR_INVALID_ARGUMENT, "prompt of %u tokens overflows capacity %zu at position %u", n, e->CAP,
-           e->positions[seq]);
-    for (uint32_t i = 0; i < n; ++i)
-      if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u at %u >= vocab", tokens[i], i);
-    e->set_device();
-    if (!e->wg_wu_adjacent())
-      fail(QD_ERROR_NOT_SUPPORTED, "prefill needs the gate and up weights adjacent");
-    // The prompt in chunks of up to kPrefillRows positions, each through all
-    // layers at once (dense GEMMs); then the tail (final norm, LM head,
-    // argmax) on the last position, which advances the slot to pos0 + n.
-    for (uint32_t done = 0; done < n;) {
-      const uint32_t rows = std::min<uint32_t>(n - done, uint32_t(qd_engine::kPrefillRows));
-      e->prefill_chunk(seq, tokens + done, int(rows), int(e->positions[seq] + done));
-      done += rows;
-      if (done == n)
-        check(hipMemcpyAsync(e->hidden + size_t(seq) * e->H, e->pf_h + size_t(rows - 1) * e->H,
-                             e->H * 4, hipMemcpyDeviceToDevice, e->stream), "D2D");
-      e->sync();  // the next chunk's token upload reuses pf_tokens
-    }
-    e->positions[seq] += n - 1;
-    e->push_state(seq, tokens[n - 1], qd::kModeStep, UINT32_MAX, 0);
-    check(qd::launch_tail(e->stream, e->tail_args(seq, e->logits + seq * e->V, 0, nullptr), nullptr),
-          "tail launch");
-    e->positions[seq] += 1;
+    check_prefill(e, seq, tokens, n);
+    run_prefill(e, seq, tokens, n, nullptr);
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState),
                          hipMemcpyDeviceToHost, e->stream), "D2H");
     if (last_logits)
@@ -1050,25 +1248,11 @@ qd_status qd_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_
 qd_status qd_step_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, const uint32_t *tokens,
                         float *logits, uint32_t *greedy) {
   return guard([&] {
-    if (!e || !seq_ids || !tokens) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
-    e->check_loaded();
-    if (n_seq == 0 || n_seq > e->B) fail(QD_ERROR_INVALID_ARGUMENT, "n_seq %u out of range", n_seq);
-    std::vector<bool> seen(e->B, false);
-    for (uint32_t i = 0; i < n_seq; ++i) {
-      e->check_seq(seq_ids[i]);
-      if (seen[seq_ids[i]]) fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u listed twice", seq_ids[i]);
-      seen[seq_ids[i]] = true;
-      if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", tokens[i]);
-      if (e->positions[seq_ids[i]] >= e->CAP) fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full", seq_ids[i]);
-    }
-    e->set_device();
+    check_batch(e, n_seq, seq_ids, tokens, 1);
     // Groups of up to kBatchRows sequences share every weight read; the
     // kernels take each row's slot, token and position as arguments and
     // leave the slot's state as a batch-1 step would.
-    for (uint32_t first = 0; first < n_seq; first += qd::kBatchRows) {
-      const int rows = static_cast<int>(std::min<uint32_t>(qd::kBatchRows, n_seq - first));
-      e->enqueue_batch(e->batch_args(seq_ids + first, tokens + first, rows), first);
-    }
+    enqueue_step_batch(e, n_seq, seq_ids, tokens, nullptr);
     check(hipMemcpyAsync(e->h_bt_out, e->bt_token, n_seq * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
     check(hipMemcpyAsync(e->h_bt_out + e->B, e->bt_top, n_seq * 4, hipMemcpyDeviceToHost, e->stream),
           "D2H");
@@ -1150,38 +1334,6 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
   });
 }
 
-namespace {
-
-// Event pair around every launch; durations are read after one sync.
-struct EventMarker : qd::Marker {
-  qd_engine *e;
-  std::vector<hipEvent_t> pool;
-  std::vector<std::pair<int, size_t>> open;  // (kernel, begin event index)
-  std::vector<std::tuple<int, size_t, size_t, double>> spans;  // kernel, begin, end, length
-  size_t used = 0;
-  double length = 0;
-  explicit EventMarker(qd_engine *engine) : e(engine) {}
-  ~EventMarker() override {
-    for (hipEvent_t ev : pool) (void)hipEventDestroy(ev);
-  }
-  size_t next() {
-    if (used == pool.size()) {
-      hipEvent_t ev;
-      check(hipEventCreate(&ev), "hipEventCreate");
-      pool.push_back(ev);
-    }
-    check(hipEventRecord(pool[used], e->stream), "hipEventRecord");
-    return used++;
-  }
-  void before(int kernel) override { open.emplace_back(kernel, next()); }
-  void after(int kernel) override {
-    const size_t b = open.back().second;
-    open.pop_back();
-    spans.emplace_back(kernel, b, next(), length);
-  }
-};
-
-}  // namespace
 
 qd_status qd_profile_kernels(qd_engine *e, uint32_t seq, uint32_t first_token, uint32_t tokens,
                              qd_kernel_stat *stats, uint32_t capacity, uint32_t *count) {
@@ -1195,34 +1347,53 @@ qd_status qd_profile_kernels(qd_engine *e, uint32_t seq, uint32_t first_token, u
       fail(QD_ERROR_INVALID_ARGUMENT, "profiling %u tokens overflows capacity", tokens);
     e->set_device();
     EventMarker marker(e);
+    marker.cost = [&](int k) {
+      return std::pair<double, double>{e->kernel_bytes(k, marker.ctx_a), e->kernel_flops(k, marker.ctx_a)};
+    };
     e->push_state(seq, first_token, qd::kModeGenerate, UINT32_MAX, tokens);
     for (uint32_t t = 0; t < tokens; ++t) {
-      marker.length = double(e->positions[seq]) + t + 1;
+      marker.ctx_a = double(e->positions[seq]) + t + 1;
       e->enqueue_step(seq, e->logits + size_t(seq) * e->V, 0, e->tokens_dev, &marker);
     }
     e->sync();
     e->positions[seq] += tokens;
-    std::vector<qd_kernel_stat> agg(qd::kKernelCount);
-    for (int k = 0; k < qd::kKernelCount; ++k) {
-      std::memset(&agg[k], 0, sizeof(qd_kernel_stat));
-      std::snprintf(agg[k].name, sizeof(agg[k].name), "%s", qd::kernel_name(k));
+    marker.report(qd::kernel_name, qd::kKernelCount, stats, capacity, count);
+  });
+}
+
+qd_status qd_profile_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, const uint32_t *tokens,
+                           uint32_t steps, qd_kernel_stat *stats, uint32_t capacity, uint32_t *count) {
+  return guard([&] {
+    if (!stats || !count) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    if (steps == 0) fail(QD_ERROR_INVALID_ARGUMENT, "steps must be positive");
+    check_batch(e, n_seq, seq_ids, tokens, steps);
+    EventMarker marker(e);
+    marker.cost = [&](int k) { return e->batch_cost(k, marker.ctx_a, marker.ctx_b); };
+    std::vector<uint32_t> feed(tokens, tokens + n_seq);
+    for (uint32_t step = 0; step < steps; ++step) {
+      enqueue_step_batch(e, n_seq, seq_ids, feed.data(), &marker);
+      check(hipMemcpyAsync(e->h_bt_out, e->bt_token, n_seq * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+      e->sync();
+      for (uint32_t i = 0; i < n_seq; ++i) {
+        e->positions[seq_ids[i]] += 1;
+        // A NaN row has no token to feed back: it repeats its input.
+        if (e->h_bt_out[i] < e->V) feed[i] = e->h_bt_out[i];
+      }
     }
-    for (const auto &span : marker.spans) {
-      float ms = 0.f;
-      check(hipEventElapsedTime(&ms, marker.pool[std::get<1>(span)], marker.pool[std::get<2>(span)]),
-            "hipEventElapsedTime");
-      qd_kernel_stat &s = agg[std::get<0>(span)];
-      s.launches += 1;
-      s.total_us += ms * 1000.0;
-      s.bytes += e->kernel_bytes(std::get<0>(span), std::get<3>(span));
-    }
-    uint32_t n = 0;
-    for (const auto &s : agg) {
-      if (s.launches == 0) continue;
-      if (n < capacity) stats[n] = s;
-      ++n;
-    }
-    *count = std::min(n, capacity);
+    marker.report(qd::batch_kernel_name, qd::kBatchKernelCount, stats, capacity, count);
+  });
+}
+
+qd_status qd_profile_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t n,
+                             qd_kernel_stat *stats, uint32_t capacity, uint32_t *count) {
+  return guard([&] {
+    if (!stats || !count) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    check_prefill(e, seq, tokens, n);
+    EventMarker marker(e);
+    marker.cost = [&](int k) { return e->prefill_cost(k, marker.ctx_a, marker.ctx_b); };
+    run_prefill(e, seq, tokens, n, &marker);
+    e->sync();
+    marker.report(qd_engine::prefill_kernel_name, qd_engine::kPrefillKernels, stats, capacity, count);
   });
 }
 

@@ -58,7 +58,7 @@ class Timing(C.Structure):
 
 class KernelStat(C.Structure):
     _fields_ = [("name", C.c_char * 48), ("launches", C.c_uint32), ("reserved", C.c_uint32),
-                ("total_us", C.c_double), ("bytes", C.c_double)]
+                ("total_us", C.c_double), ("bytes", C.c_double), ("flops", C.c_double)]
 
 
 _F = C.POINTER(C.c_float)
@@ -91,6 +91,10 @@ _SIGNATURES = {
                                        _U, _U, _U, _F]),
     "qd_last_timing": (C.c_int, [_E, C.POINTER(Timing)]),
     "qd_profile_kernels": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(KernelStat),
+                                     C.c_uint32, _U]),
+    "qd_profile_batch": (C.c_int, [_E, C.c_uint32, _U, _U, C.c_uint32, C.POINTER(KernelStat),
+                                   C.c_uint32, _U]),
+    "qd_profile_prefill": (C.c_int, [_E, C.c_uint32, _U, C.c_uint32, C.POINTER(KernelStat),
                                      C.c_uint32, _U]),
     "qd_profile_resident": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_double),
                                       C.c_uint32, _U]),
@@ -290,16 +294,35 @@ class Engine:
         k = int(n.value)
         return out[:k], int(reason.value), (None if logits is None else logits[:k])
 
-    def profile_kernels(self, seq: int, first_token: int, tokens: int) -> dict:
-        """Per-kernel {name: (launches, avg_us, avg_bytes)} over `tokens` steps."""
+    @staticmethod
+    def _stats(call) -> dict:
         cap = 64
         stats = (KernelStat * cap)()
         n = C.c_uint32()
-        _check(lib().qd_profile_kernels(self.handle, seq, first_token, tokens, stats, cap, C.byref(n)))
-        out = {}
-        for s in stats[:n.value]:
-            out[s.name.decode()] = (int(s.launches), s.total_us / s.launches, s.bytes / s.launches)
-        return out
+        _check(call(stats, cap, C.byref(n)))
+        return {s.name.decode(): (int(s.launches), s.total_us / s.launches, s.bytes / s.launches,
+                                  s.flops / s.launches) for s in stats[:n.value]}
+
+    def profile_kernels(self, seq: int, first_token: int, tokens: int) -> dict:
+        """Per-kernel {name: (launches, avg_us, avg_bytes, avg_flops)} over
+        `tokens` stream-ordered steps."""
+        return self._stats(lambda st, cap, n: lib().qd_profile_kernels(
+            self.handle, seq, first_token, tokens, st, cap, n))
+
+    def profile_batch(self, seq_ids, tokens, steps: int) -> dict:
+        """Per-kernel {name: (launches, avg_us, avg_bytes, avg_flops)} over
+        `steps` batched steps of the listed slots."""
+        s = np.ascontiguousarray(seq_ids, np.uint32)
+        t = np.ascontiguousarray(tokens, np.uint32)
+        return self._stats(lambda st, cap, n: lib().qd_profile_batch(
+            self.handle, s.size, _u(s), _u(t), steps, st, cap, n))
+
+    def profile_prefill(self, seq: int, tokens) -> dict:
+        """Per-kernel {name: (launches, avg_us, avg_bytes, avg_flops)} of one
+        prefill of `tokens` into the slot (which advances as qd_prefill)."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        return self._stats(lambda st, cap, n: lib().qd_profile_prefill(
+            self.handle, seq, _u(t), t.size, st, cap, n))
 
     RESIDENT_STAGES = tuple(f"{s}.{k}" for s in ("qkv", "attention", "oproj", "gateup", "down",
                                                   "lmhead", "argmax") for k in ("wait", "work")) + \

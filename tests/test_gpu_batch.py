@@ -170,3 +170,27 @@ def test_batch_subsets_order_and_two_groups(batch16):
             eng.kv_reset(s, lens[s])
             tok, _, single = eng.step(s, feed[s])
             check_logits(int(greedy[i]), logits[i], tok, single, f"{len(order)} rows: slot {s}")
+
+
+def test_profile_batch_reports_every_kernel(batch16):
+    """qd_profile_batch times every batched kernel, reports algorithmic bytes
+    and flops per launch, and advances each slot like qd_step_batch."""
+    eng, lengths, _, firsts = batch16
+    slots = list(range(ROWS))
+    for s in slots:
+        eng.kv_reset(s, lengths[s])
+    say("profile_batch: 2 steps")
+    prof = eng.profile_batch(slots, firsts, 2)
+    layers = SHAPE.layers
+    for name, per_step in (("batch_qkv_kernel", layers), ("batch_attn_kernel", layers),
+                           ("batch_oproj_kernel", layers), ("batch_gateup_kernel", layers),
+                           ("batch_down_kernel", layers), ("batch_lmhead_kernel", 1),
+                           ("batch_argmax_kernel", 1), ("batch_embed_kernel", 1)):
+        launches, avg_us, avg_bytes, _ = prof[name]
+        assert launches == 2 * per_step, name
+        assert avg_us > 0 and avg_bytes > 0, name
+    h, inter = SHAPE.hidden, SHAPE.intermediate
+    assert prof["batch_gateup_kernel"][3] == 4 * ROWS * inter * h
+    assert prof["batch_lmhead_kernel"][3] == 2 * ROWS * SHAPE.vocab * h
+    for s in slots:
+        assert eng.decode_state(s).token_position == lengths[s] + 2

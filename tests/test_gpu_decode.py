@@ -256,6 +256,31 @@ def test_prefill_512_config5_matches_oracle(full):
         feed = rtok
 
 
+def test_profile_prefill_matches_prefill(full):
+    """qd_profile_prefill times the prompt kernels by projection and leaves
+    the slot exactly as qd_prefill does (same kernels: bit-identical KV)."""
+    eng, _ = full
+    prompt = qo.fill_tokens(96, 4, PROMPT_STREAM + 3, FULL.vocab)
+    say("profile_prefill vs prefill, 96 tokens")
+    eng.kv_reset(0, 0)
+    eng.kv_reset(1, 0)
+    prof = eng.profile_prefill(0, prompt)
+    tok, _, _ = eng.prefill(1, prompt, want_logits=False)
+    assert eng.decode_state(0).token_position == 96
+    assert eng.decode_state(0).sampled_token == tok
+    for layer in (0, 23):
+        k0, v0 = eng.read_kv(0, layer, 0, 96)
+        k1, v1 = eng.read_kv(1, layer, 0, 96)
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1), layer
+    h, i, qkv = FULL.hidden, FULL.intermediate, (FULL.heads + 2 * FULL.kv_heads) * FULL.head_dim
+    expect = {"gemm_nt_kernel:qkv": 2 * 96 * qkv * h, "gemm_nt_kernel:gateup": 4 * 96 * i * h,
+              "gemm_nt_kernel:down": 2 * 96 * h * i}
+    for name, flops in expect.items():
+        launches, avg_us, _, avg_flops = prof[name]
+        assert launches == FULL.layers and avg_us > 0 and avg_flops == flops, name
+    assert prof["lmhead_kernel+argmax"][0] == 1
+
+
 def test_prefill_in_pieces_and_over_chunks_agree(full):
     """A prompt prefilled in two calls (the second continuing at position 300)
     and one longer than a 512-row chunk give the one-call results."""
