@@ -51,7 +51,7 @@ WEIGHT_BYTES = 1_976_131_072
 # workload; the factors come from a 1 GiB device copy in the same profile
 # (profiles/resident_decode_kernel_config2.md). Re-measured when the kernel
 # changes; None where no measurement exists.
-RESIDENT_TRAFFIC_PER_TOKEN = 2_024_293_558
+RESIDENT_TRAFFIC_PER_TOKEN = 2_106_996_721
 
 
 def step_bytes(length: int) -> int:
