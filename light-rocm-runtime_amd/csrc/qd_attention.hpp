@@ -180,6 +180,49 @@ __device__ void attn_partial_unit(const KvSrc &kcache, const KvSrc &vcache,
   probe(2);
 }
 
+// One query head over the positions [0, n) of a chunk, computed by one wave;
+// the resident role kernel (K/V staged in LDS) and the stream-ordered kernel
+// (K/V read from the cache) both run it, so their partials are bit-identical.
+// Passes of 64 positions: lane = position for the scores (64-dim dot in
+// order d = 0..63, scale 1/sqrt(64)), an online softmax (running max m, sum
+// l), then P.V with lane = output dim, accumulating positions in order.
+// k4(d4, j) returns float4 d4 of position j's K row and v(j, d) element d of
+// its V row; positions j >= n are never read for V and their scores are
+// masked (k4 must still return something finite-or-not for them). q holds
+// the head's 64 query values; (m, l, acc) carry the state across calls, so a
+// chunk may be walked in windows whose lengths are multiples of 64.
+template <typename K4, typename V>
+__device__ __forceinline__ void attn_head_window(K4 k4, V v, const float4 (&q)[kHeadDim / 4], int n,
+                                                 float &m, float &l, float &acc) {
+  const int lane = lane_id();
+  const float scale = rsqrtf(static_cast<float>(kHeadDim));
+  for (int base = 0; base < n; base += kWave) {
+    const int j = base + lane;
+    float s = 0.f;
+#pragma unroll
+    for (int d4 = 0; d4 < kHeadDim / 4; ++d4) s = fma4(k4(d4, j), q[d4], s);
+    const bool in = j < n;
+    const float sv = in ? s * scale : -INFINITY;
+    const float m_new = fmaxf(m, wave_max(sv));
+    const float p = m_new == -INFINITY ? 0.f : expf(sv - m_new);
+    const float corr = m_new == -INFINITY ? 1.f : expf(m - m_new);
+    l = fmaf(l, corr, wave_sum(p));
+    m = m_new;
+    float a = acc * corr;
+    // Positions in order; eight V reads in flight at a time.
+    const int cnt = min(kWave, n - base);
+    for (int j0 = 0; j0 < cnt; j0 += 8) {
+      float vv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) vv[u] = j0 + u < cnt ? v(base + j0 + u, lane) : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (j0 + u < cnt) a = fmaf(read_lane(p, j0 + u), vv[u], a);
+    }
+    acc = a;
+  }
+}
+
 // Merge of one head's partials for output dim d; part(c, k) returns element
 // k of chunk c's record (0: m, 1: l, 2 + d: acc). Records are stored head
 // major: record (h, c) at (h * kAttnMaxChunks + c) * kPartStride.

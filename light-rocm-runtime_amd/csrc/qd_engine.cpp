@@ -127,6 +127,9 @@ struct qd_engine {
   uint32_t epoch = 0;                       // last launch epoch (1..4095)
   uint32_t *resident_error = nullptr;       // [1]
   int resident_grid = 0;                    // 0: resident path unavailable
+  // Role-split resident kernel (one 512-thread workgroup per CU); when
+  // roles_grid is 0 the tagged-dataflow kernel runs with resident_grid.
+  int roles_grid = 0;
   std::string resident_off_reason;
   // Prompt workspace (allocated on the first prefill): rows of the hidden
   // states, RMSNorm output, packed QKV, attention output, gate|up and SwiGLU
@@ -534,7 +537,7 @@ struct qd_engine {
     ra.h1 = take(H);
     ra.act = take(I);
     ra.hidden = take(H);
-    ra.top = take(2 * size_t(resident_grid));
+    ra.top = take(4 * size_t(std::max(resident_grid, roles_grid)));
     ra.logits = hist;
     ra.out_tokens = tokens_dev;
     ra.st = states + seq;
@@ -555,7 +558,24 @@ struct qd_engine {
     ra.eos = eos;
     ra.epoch = epoch << qd::kTagSeqBits;
     check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
+    if (roles_grid) {
+      qd::RolePlan plan{};
+      const int reach = static_cast<int>(positions[seq] + max_tokens);
+      if (qd::plan_roles(roles_grid, int(H), int(I), int(NQ), int(NKV), reach, &plan)) {
+        for (int r = 0; r < qd::kRoleCount; ++r) ra.role_end[r] = plan.end[r];
+        return qd::launch_roles(stream, ra, roles_grid);
+      }
+    }
     return qd::launch_resident(stream, ra, resident_grid);
+  }
+
+  // Grid of the resident kernel a launch reaching `reach` positions uses.
+  int active_resident_grid(uint32_t reach) const {
+    qd::RolePlan plan{};
+    if (roles_grid &&
+        qd::plan_roles(roles_grid, int(H), int(I), int(NQ), int(NKV), int(reach), &plan))
+      return roles_grid;
+    return resident_grid;
   }
 
   // A cooperative launch can be refused while another process holds the
@@ -565,6 +585,7 @@ struct qd_engine {
     if (err != hipErrorIllegalState && err != hipErrorCooperativeLaunchTooLarge) return false;
     (void)hipGetLastError();
     resident_grid = 0;
+    roles_grid = 0;
     resident_off_reason = std::string("cooperative launch refused: ") + hipGetErrorString(err);
     return true;
   }
@@ -753,6 +774,18 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
         if (want >= 64 && want <= std::min(max_grid, qd::kMaxResidentGrid)) e->resident_grid = want;
       }
     }
+    // The role-split kernel: one 512-thread workgroup on every CU, for the
+    // model shapes it is built for; QD_RESIDENT_KERNEL=tagged keeps the
+    // tagged-dataflow kernel.
+    if (e->resident_grid > 0) {
+      const char *kind = std::getenv("QD_RESIDENT_KERNEL");
+      const int role_max = qd::roles_max_grid(c.device);
+      qd::RolePlan plan{};
+      if (!(kind && std::strcmp(kind, "tagged") == 0) && role_max >= cus &&
+          cus <= qd::kMaxRoleGrid &&
+          qd::plan_roles(cus, int(e->H), int(e->I), int(e->NQ), int(e->NKV), 1, &plan))
+        e->roles_grid = cus;
+    }
     const int grid_alloc = std::max({cus, max_grid, 1});
     e->layer_ptrs_dev = e->alloc<qd::LayerPtrs>(e->L);
     check(hipMemcpyAsync(e->layer_ptrs_dev, e->layers.data(), e->L * sizeof(qd::LayerPtrs),
@@ -792,7 +825,7 @@ qd_status qd_engine_device_bytes(const qd_engine *e, uint64_t *bytes) {
 qd_status qd_engine_resident_grid(const qd_engine *e, uint32_t *grid) {
   return guard([&] {
     if (!e || !grid) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
-    *grid = static_cast<uint32_t>(e->resident_grid);
+    *grid = static_cast<uint32_t>(e->roles_grid ? e->roles_grid : e->resident_grid);
   });
 }
 
@@ -1415,7 +1448,9 @@ void profiled_resident_launch(qd_engine *e, uint32_t seq, uint32_t first_token, 
   if (!e->resident_fits(tokens)) fail(QD_ERROR_INVALID_ARGUMENT, "too many tokens for one resident launch");
   e->set_device();
   const size_t trace_elems =
-      trace_out ? size_t(e->resident_grid) * (e->L + 1) * qd::kResidentStages : 0;
+      trace_out ? size_t(e->active_resident_grid(e->positions[seq] + tokens)) * (e->L + 1) *
+                      qd::kResidentStages
+                : 0;
   // Temporary buffers of a diagnostic call, released before returning.
   uint64_t *ticks = nullptr, *trace = nullptr;
   check(hipMalloc(&ticks, qd::kResidentStages * sizeof(uint64_t)), "hipMalloc");
@@ -1478,8 +1513,10 @@ qd_status qd_trace_resident(qd_engine *e, uint32_t seq, uint32_t first_token, ui
     if (!e || !timeline || !workgroups || !rows || !stages)
       fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
     if (trace_token >= tokens) fail(QD_ERROR_INVALID_ARGUMENT, "trace_token must be below tokens");
-    const size_t need = size_t(e->resident_grid) * (e->L + 1) * qd::kResidentStages;
-    *workgroups = e->resident_grid;
+    e->check_seq(seq);
+    const int grid = e->active_resident_grid(e->positions[seq] + tokens);
+    const size_t need = size_t(grid) * (e->L + 1) * qd::kResidentStages;
+    *workgroups = uint32_t(grid);
     *rows = uint32_t(e->L + 1);
     *stages = qd::kResidentStages;
     if (e->resident_grid == 0)

@@ -100,14 +100,14 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
   }
 }
 
-// Split-KV decode attention partials (qd_attention.hpp): workgroup
-// (chunk, query head) writes one record (m, l, acc[64]) into
-// part[head][chunk][66].
-__global__ __launch_bounds__(kBlock) void attn_partial_kernel(
+// Split-KV decode attention partials (qd_attention.hpp): one wave per
+// (chunk, query head) walks the chunk with attn_head_window, reading K/V
+// from the cache (this step's row was written by qkv_rope_kernel), and
+// writes one record (m, l, acc[64]) into part[head][chunk][66].
+__global__ __launch_bounds__(kWave) void attn_partial_kernel(
     const float *__restrict__ q, const float *__restrict__ k_cache,
     const float *__restrict__ v_cache, const SeqState *__restrict__ st,
     int nq, int nkv, float *__restrict__ part, int capacity) {
-  __shared__ AttnLds sh;
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
   const int position = static_cast<int>(st->position);
   const int length = position + 1;
@@ -118,25 +118,25 @@ __global__ __launch_bounds__(kBlock) void attn_partial_kernel(
   const int g = h / (nq / nkv);
   const int kv_dim = nkv * kHeadDim;
   const int begin = chunk * chunk_len;
-  const int end = min(length, begin + chunk_len);
-  const Plain kc(k_cache), vc(v_cache);
-  const Plain knew(k_cache + static_cast<size_t>(position) * kv_dim);
-  const Plain vnew(v_cache + static_cast<size_t>(position) * kv_dim);
-  attn_partial_unit<kWavesPerBlock>(
-      kc, vc, knew, vnew, position, g, kv_dim, begin, end, sh,
-      [&](auto request_rows) {
-        request_rows();
-        if (threadIdx.x < kHeadDim) sh.qkv[threadIdx.x] = q[h * kHeadDim + threadIdx.x];
-        __syncthreads();
+  const int n = min(length, begin + chunk_len) - begin;
+  const float *kb = k_cache + static_cast<size_t>(begin) * kv_dim + g * kHeadDim;
+  const float *vb = v_cache + static_cast<size_t>(begin) * kv_dim + g * kHeadDim;
+  float4 qv[kHeadDim / 4];
+#pragma unroll
+  for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
+    qv[d4] = reinterpret_cast<const float4 *>(q + h * kHeadDim)[d4];
+  float m = -INFINITY, l = 0.f, acc = 0.f;
+  attn_head_window(
+      [&](int d4, int j) {
+        return reinterpret_cast<const float4 *>(kb + static_cast<size_t>(min(j, n - 1)) * kv_dim)[d4];
       },
-      [&](float m, float l, float acc, int d) {
-        float *rec = part + (h * kAttnMaxChunks + chunk) * kPartStride;
-        rec[2 + d] = acc;
-        if (d == 0) {
-          rec[0] = m;
-          rec[1] = l;
-        }
-      });
+      [&](int j, int d) { return vb[static_cast<size_t>(j) * kv_dim + d]; }, qv, n, m, l, acc);
+  float *rec = part + (h * kAttnMaxChunks + chunk) * kPartStride;
+  rec[2 + threadIdx.x] = acc;
+  if (threadIdx.x == 0) {
+    rec[0] = m;
+    rec[1] = l;
+  }
 }
 
 // Merges each head's partials into attn[h*64 + d].
@@ -378,7 +378,7 @@ hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
   }
   {
     Scope scope(m, kKAttnPartial);
-    attn_partial_kernel<<<dim3(kAttnMaxChunks, p.nq), kBlock, 0, s>>>(
+    attn_partial_kernel<<<dim3(kAttnMaxChunks, p.nq), kWave, 0, s>>>(
         p.q, p.k_cache, p.v_cache, p.st, p.nq, p.nkv, p.part, p.capacity);
   }
   {

@@ -17,6 +17,16 @@ constexpr int kResidentStages = 17;
 // Largest resident grid (the argmax partials are staged in LDS).
 constexpr int kMaxResidentGrid = 1024;
 
+// Role-split resident kernel (qd_roles.hip): one 512-thread workgroup per
+// CU; workgroups [0, end[kRoleQkv]) compute QKV, [end[kRoleQkv],
+// end[kRoleAttn]) attention, then O, gate/up and down.
+constexpr int kRoleThreads = 512;
+constexpr int kMaxRoleGrid = 512;
+enum ResidentRole : int { kRoleQkv = 0, kRoleAttn, kRoleO, kRoleGate, kRoleDown, kRoleCount };
+struct RolePlan {
+  int end[kRoleCount];  // cumulative workgroup ends per role
+};
+
 // Arguments of one resident generation on one sequence slot. The tagged
 // vectors hold 8-byte (value, tag) elements; see qd_resident.hip.
 struct ResidentArgs {
@@ -56,6 +66,7 @@ struct ResidentArgs {
   uint32_t max_tokens;
   uint32_t eos;
   uint32_t epoch;               // launch epoch << kTagSeqBits, never 0
+  int role_end[kRoleCount];     // role-split kernel only (RolePlan::end)
 };
 
 // Tags: epoch << kTagSeqBits | (token * (6 * layers + 1) + stage + 1).
@@ -64,12 +75,21 @@ constexpr int kTagSeqBits = 20;
 inline size_t resident_tagged_elems(int hidden, int heads, int kv_heads, int inter, int grid) {
   (void)kv_heads;
   return 4 * size_t(heads) * 64 + 16 * size_t(heads) * 66 + 3 * size_t(hidden) + inter +
-         2 * size_t(grid);
+         4 * size_t(grid);
 }
 
 hipError_t launch_resident(hipStream_t s, const ResidentArgs &args, int grid);
 // Largest co-resident grid on `device` (0 if the query fails).
 int resident_max_grid(int device);
 int device_cu_count(int device);
+
+// Role split of `grid` CUs for generations reaching context `max_length`;
+// false when the model shape has no role kernel or the grid cannot hold one
+// layer's weights on chip.
+bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int max_length,
+                RolePlan *plan);
+hipError_t launch_roles(hipStream_t s, const ResidentArgs &args, int grid);
+// Largest co-resident grid of the role kernel on `device` (0 if the query fails).
+int roles_max_grid(int device);
 
 }  // namespace qd

@@ -1,0 +1,1296 @@
+// Resident decode megakernel, role-split form. One cooperative launch of one
+// 512-thread workgroup per CU runs every token of a greedy generation (all
+// decoder layers, the LM head, the argmax and the embedding feedback); it is
+// the MI355X counterpart of the reference's persistent-graph resident loop
+// (include/lrrt/persistent_graph/compiled_scheduler.hpp:108-217 driving
+// benchmarks/qwen_stateful_graph_kernel.cpp:661-1083).
+//
+// Why roles. A decode step is a chain of dependent hand-offs between CUs
+// (QKV -> attention -> O -> gate/up -> down -> next layer); on MI355X each
+// device-scope hand-off costs ~0.5 us idle and 1-1.6 us while HBM streams,
+// and a CU's vector memory pipe returns data in issue order, so a poll issued
+// behind a burst of weight loads waits for all of them. The grid is therefore
+// split into five roles, each owning one stage of every layer:
+//
+//   QKV   attention RMSNorm + packed QKV + bias + RoPE -> q, new K/V (+ cache)
+//   ATTN  one unit per (KV head, chunk): the group's query heads over the
+//         chunk's positions, online softmax -> partial records
+//   O     merges the partial records itself, O projection + residual -> h1
+//   GATE  MLP RMSNorm + gate/up + SiLU -> act
+//   DOWN  down projection + residual -> next layer's hidden
+//
+// Every role CU keeps one layer's share of its weights on chip (LDS, filled
+// by global_load_lds DMA, plus register slots). Right after computing layer l
+// it issues the loads of its layer l+1 share, and only then polls for its
+// next input: that input arrives about one layer later, by which time the
+// loads have landed, so polls never queue behind weight traffic while HBM
+// streams the other roles' shares. Sizing gives every role CU about the same
+// bytes per layer, so all CUs stream at the same rate.
+//
+// Hand-offs are tagged vectors: each value is an 8-byte (value, tag) pair
+// written with one device-scope (sc1) 64-bit store; the tag names the launch
+// epoch and the producing (token, layer, stage). Consumers poll until every
+// pair they need carries the expected tag. Reuse safety: a vector is
+// rewritten only by a producer whose inputs transitively required every
+// consumer of the previous version to have read it (each consumer reads
+// before it publishes, and every role's output is needed downstream); the
+// argmax partials are double-buffered by token parity because a CU with no
+// unit in a layer contributes nothing to the next token's chain.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+
+#include "qd_attention.hpp"
+#include "qd_device.hpp"
+#include "qd_device_math.hpp"
+#include "qd_resident.hpp"
+
+namespace qd {
+namespace {
+
+using namespace dev;
+
+constexpr int kT = kRoleThreads;  // threads per workgroup
+constexpr int kW = kT / kWave;    // waves per workgroup
+constexpr uint32_t kSpinLimit = 1u << 21;
+// 160 KiB of LDS per CU, less what the runtime's own block reductions use.
+constexpr int kLdsBytes = 160 * 1024 - 512;
+constexpr int kAttnCap = 256;     // positions of an attention window staged in LDS
+
+// Register slots per wave: row-pair units of the K=H roles, rows of DOWN.
+constexpr int kSlotsQ = 2, kSlotsO = 2, kSlotsG = 2, kSlotsD = 1;
+
+// Wave index as a wave-uniform (scalar) value: unit indices, slot branches
+// and row addresses derived from it stay in SGPRs.
+__device__ __forceinline__ int wave_u() { return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); }
+
+// Barriers. HIP's __syncthreads() carries a workgroup-scope fence, which on
+// this target waits for every outstanding vector memory operation (weight
+// DMA in flight, device-scope stores not yet acknowledged) before the
+// barrier, and __syncthreads_and() also re-reads the workgroup size from
+// memory. The waves of a role CU only share LDS, so their barrier waits
+// for LDS operations alone; a wave that needs its own vector memory
+// operations finished (LDS filled by its DMA) says so with vm_wait().
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+__device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Whole-workgroup AND (flags: one LDS word per wave). The ballot is taken
+// with the whole wave active, then lane 0 records it.
+__device__ __forceinline__ bool block_all(bool v, uint32_t *flags) {
+  const uint32_t wave_all = __builtin_amdgcn_ballot_w64(!v) == 0 ? 1u : 0u;
+  if (lane_id() == 0) flags[wave_u()] = wave_all;
+  lds_barrier();
+  uint32_t all = 1u;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) all &= flags[w];
+  lds_barrier();
+  return all != 0u;
+}
+
+struct Pair2 {
+  float v0;
+  uint32_t t0;
+  float v1;
+  uint32_t t1;
+};
+typedef unsigned int u32x2 __attribute__((vector_size(8)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// (value, tag) vector with device-scope access; bounds-checked by the
+// buffer descriptor.
+struct TagVec {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ TagVec(void *base, uint32_t elems)
+      : r(__builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(elems * 8u), kRsrcWord3)) {}
+  __device__ void put(uint32_t i, float v, uint32_t tag) const {
+    const u32x2 x = {__builtin_bit_cast(unsigned, v), tag};
+    __builtin_amdgcn_raw_buffer_store_b64(x, r, i * 8u, 0, kPolicySc1);
+  }
+  __device__ Pair2 get2(uint32_t pair) const {
+    return __builtin_bit_cast(Pair2,
+                              __builtin_amdgcn_raw_buffer_load_b128(r, pair * 16u, 0, kPolicySc1));
+  }
+};
+
+struct Lds {
+  const float *p;
+  __device__ float ld(uint32_t i) const { return p[i]; }
+  __device__ float4 ld4(uint32_t i4) const { return reinterpret_cast<const float4 *>(p)[i4]; }
+};
+
+// 1 KiB global -> LDS copy without registers: lane l's 16 bytes from `src`
+// land at dst + 16 l (dst wave-uniform). Counted by vmcnt like any load.
+template <int kPolicy>
+__device__ __forceinline__ void dma16(const void *src, void *dst) {
+#if __HIP_DEVICE_COMPILE__
+  __builtin_amdgcn_global_load_lds(src, (lds_void *)dst, 16, 0, kPolicy);
+#endif
+}
+
+// Profiling state in LDS (see Clock): stage totals and the traced token's
+// stamps (per layer: input arrived, outputs published; then LM head/argmax).
+constexpr int kMaxTraceLayers = 24;
+constexpr int kStampsPerLayer = 5;  // input arrived, outputs published, 3 sub-phases
+struct ClockLds {
+  uint64_t ticks[kResidentStages];
+  uint64_t stamps[kStampsPerLayer * kMaxTraceLayers + 4];
+};
+
+struct Common {
+  float vec[1024];   // gathered input vector (hidden, h1, residual rows)
+  float xn[1024];    // normalised GEMV operand / merged attention
+  float red[kW];
+  float bv[kW];
+  uint32_t bi[kW];
+  uint32_t flags[kW];                   // block_all
+  float top[2 * kMaxRoleGrid];          // argmax partials (value, index bits)
+  ClockLds clock;                       // profiling (profiled variant only)
+};
+// The kernel's one LDS block, at namespace scope so the per-role functions
+// (called from the kernel) address it as LDS.
+__shared__ __attribute__((aligned(16))) unsigned char roles_lds[kLdsBytes];
+
+constexpr int kRegionOffset = (static_cast<int>(sizeof(Common)) + 255) / 256 * 256;
+constexpr int kRegionBytes = kLdsBytes - kRegionOffset;
+
+// Whole-workgroup gather of `pairs` tagged pairs: map(p, src_pair, dst)
+// names pair p's source pair index and its destination float index (two
+// consecutive floats). Returns false when the wait gave up (error raised).
+template <int kMaxPer, typename Map>
+__device__ bool gather_map(const TagVec &src, int pairs, uint32_t tag, float *dst, uint32_t *error,
+                           uint32_t *flags, Map map) {
+  const int t = threadIdx.x;
+  uint32_t pending = 0;
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k)
+    if (t + k * kT < pairs) pending |= 1u << k;
+  for (uint32_t spin = 0;; ++spin) {
+    Pair2 got[kMaxPer];
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k)
+      if ((pending >> k) & 1u) {
+        uint32_t s;
+        int d;
+        map(t + k * kT, s, d);
+        got[k] = src.get2(s);
+      }
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+      if (((pending >> k) & 1u) && got[k].t0 == tag && got[k].t1 == tag) {
+        uint32_t s;
+        int d;
+        map(t + k * kT, s, d);
+        dst[d] = got[k].v0;
+        dst[d + 1] = got[k].v1;
+        pending &= ~(1u << k);
+      }
+    }
+    // Every wave's earlier vector memory operations (its LDS DMA above all)
+    // are complete when the gather returns.
+    vm_wait();
+    if (block_all(pending == 0, flags)) return true;
+    if (spin > kSpinLimit) {
+      if (t == 0) atomicOr(error, 1u);
+      return false;
+    }
+  }
+}
+
+// Contiguous gather: elements [first, first + n) (first and n even) -> dst.
+template <int kMaxPer>
+__device__ bool gather(const TagVec &src, uint32_t first, int n, uint32_t tag, float *dst,
+                       uint32_t *error, uint32_t *flags) {
+  return gather_map<kMaxPer>(src, n / 2, tag, dst, error, flags, [&](int p, uint32_t &s, int &d) {
+    s = first / 2 + p;
+    d = 2 * p;
+  });
+}
+
+// Profiling clock kept by thread 0 (profiled variant only). Totals and the
+// traced token's stamps live in LDS and reach global memory only when the
+// traced token ends and at exit: a global store here would make the role's
+// next LDS read wait for it (the compiler guards LDS reads behind the DMA
+// with vmcnt, which also counts stores), distorting what is measured.
+
+template <bool kProfile>
+struct Clock {
+  ClockLds *lds = nullptr;
+  uint64_t prev = 0;
+  bool tracing = false;
+  int layer = 0;
+  __device__ void start(ClockLds *c) {
+    if (kProfile && threadIdx.x == 0) {
+      lds = c;
+      for (int s = 0; s < kResidentStages; ++s) lds->ticks[s] = 0;
+      prev = wall_clock64();
+    }
+  }
+  __device__ void at(bool trace_this_token, int l) {
+    if (kProfile) {
+      tracing = trace_this_token;
+      layer = l;
+    }
+  }
+  // Role stages 2r (input arrived) and 2r+1 (outputs published) per layer;
+  // stages from 2*kRoleCount on belong to the token's LM head and argmax.
+  __device__ void lap(int stage) {
+    if (kProfile && threadIdx.x == 0) {
+      const uint64_t now = wall_clock64();
+      lds->ticks[stage] += now - prev;
+      prev = now;
+      if (tracing) {
+        if (stage < 2 * kRoleCount) {
+          if (layer < kMaxTraceLayers) lds->stamps[kStampsPerLayer * layer + (stage & 1)] = now;
+        } else {
+          lds->stamps[kStampsPerLayer * kMaxTraceLayers + (stage - 2 * kRoleCount)] = now;
+        }
+      }
+    }
+  }
+  // Sub-phase stamp k (0..2) of the traced token's current layer (trace only).
+  __device__ void mark(int k) {
+    if (kProfile && threadIdx.x == 0 && tracing && layer < kMaxTraceLayers)
+      lds->stamps[kStampsPerLayer * layer + 2 + k] = wall_clock64();
+  }
+  // Timeline of the traced token: row[l][stage] for this CU's role stages,
+  // its sub-phases in the last three stage slots, and the LM head / argmax
+  // stages.
+  __device__ void flush_trace(uint64_t *trace, int layers, int role) const {
+    if (!kProfile || !trace || threadIdx.x != 0) return;
+    uint64_t *row = trace + static_cast<size_t>(blockIdx.x) * (layers + 1) * kResidentStages;
+    for (int l = 0; l < layers && l < kMaxTraceLayers; ++l) {
+      const uint64_t *st = lds->stamps + kStampsPerLayer * l;
+      row[l * kResidentStages + 2 * role] = st[0];
+      row[l * kResidentStages + 2 * role + 1] = st[1];
+      for (int k = 0; k < 3; ++k) row[l * kResidentStages + kResidentStages - 3 + k] = st[2 + k];
+    }
+    for (int j = 0; j < 4; ++j)
+      row[layers * kResidentStages + 2 * kRoleCount + j] =
+          lds->stamps[kStampsPerLayer * kMaxTraceLayers + j];
+  }
+  // Stage totals: the first CU of each role reports its role's stages, CU 0
+  // the LM head and argmax stages.
+  __device__ void publish(uint64_t *out, int role, bool first_of_role) const {
+    if (!kProfile || !out || threadIdx.x != 0) return;
+    if (first_of_role) {
+      out[2 * role] = lds->ticks[2 * role];
+      out[2 * role + 1] = lds->ticks[2 * role + 1];
+    }
+    if (blockIdx.x == 0)
+      for (int s = 2 * kRoleCount; s < kResidentStages; ++s) out[s] = lds->ticks[s];
+  }
+};
+
+// ---- K=H row-pair roles (QKV, O, gate/up) ----------------------------------
+// A CU owns units [u0, u0 + n); local unit k belongs to wave k % kW. Units
+// k < kW*S sit in register slot k / kW of their wave; the next Lcap units in
+// LDS (unit k - kW*S, in slot-layout order); any further unit is loaded from
+// global memory when computed (only if the plan over-fills a CU).
+template <int H, int S, int Lcap>
+struct PairRole {
+  static constexpr int NJ = PairSlots<H>::NJ;
+  static constexpr int K4 = PairSlots<H>::K4;
+  static constexpr int UnitF4 = NJ * kWave;
+  float4 wv[S][NJ];
+  float4 *units = nullptr;
+  int n = 0;
+
+  template <typename Rows>
+  __device__ void prefetch_regs(Rows rows) {
+    const int w = wave_u();
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      const int k = w + kW * j;
+      if (k < n) {
+        const float *ra, *rb;
+        rows(k, ra, rb);
+        load_pair_weights<H>(ra, rb, wv[j]);
+      } else {
+        // An empty slot is still redefined, so its previous contents are
+        // not kept live across the code between two prefetches.
+#pragma unroll
+        for (int c = 0; c < NJ; ++c) wv[j][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  }
+  template <typename Rows>
+  __device__ void prefetch_lds(Rows rows) {
+    const int lane = lane_id();
+    for (int k = kW * S + wave_u(); k < n && k - kW * S < Lcap; k += kW) {
+      const float *ra, *rb;
+      rows(k, ra, rb);
+      const float4 *a4 = reinterpret_cast<const float4 *>(ra);
+      const float4 *b4 = reinterpret_cast<const float4 *>(rb);
+      float4 *dst = units + (k - kW * S) * UnitF4;
+#pragma unroll
+      for (int c = 0; c < NJ; ++c) {
+        const int f = c * kWave + lane;
+        const float4 *src = f < K4 ? a4 + f : (f < 2 * K4 ? b4 + (f - K4) : a4);
+        dma16<0>(src, dst + c * kWave);
+      }
+    }
+  }
+  // Every unit's two sums are computed before any epilogue runs: the
+  // epilogues publish with device-scope stores, and on this target vmcnt
+  // counts stores too, so an LDS read issued after a store (the compiler
+  // guards LDS reads behind the pending DMA with vmcnt(0)) would wait for
+  // the store's round trip.
+  // prep(k) returns the per-unit constants the epilogue needs from LDS; all
+  // of them are read before the first epilogue store for the same reason.
+  static constexpr int kLdsPerWave = (Lcap + kW - 1) / kW;
+  template <typename Prep, typename Epi, typename Mid>
+  __device__ void compute(const float4 (&xv)[NJ], Prep prep, Epi epi, Mid mid) const {
+    const int w = wave_u(), lane = lane_id();
+    float sa[S + kLdsPerWave], sb[S + kLdsPerWave];
+#pragma unroll
+    for (int j = 0; j < S; ++j) pair_dot<H>(wv[j], xv, sa[j], sb[j]);
+#pragma unroll
+    for (int i = 0; i < kLdsPerWave; ++i) {
+      const int k = kW * S + w + kW * i;
+      sa[S + i] = sb[S + i] = 0.f;
+      if (k < n && k - kW * S < Lcap) {
+        const float4 *src = units + (k - kW * S) * UnitF4;
+        float4 wl[NJ];
+#pragma unroll
+        for (int c = 0; c < NJ; ++c) wl[c] = src[c * kWave + lane];
+        pair_dot<H>(wl, xv, sa[S + i], sb[S + i]);
+      }
+    }
+    mid();
+    float4 cst[S + kLdsPerWave];
+#pragma unroll
+    for (int j = 0; j < S + kLdsPerWave; ++j) {
+      const int k = j < S ? w + kW * j : kW * S + w + kW * (j - S);
+      cst[j] = k < n ? prep(k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      const int k = w + kW * j;
+      if (k < n) epi(k, sa[j], sb[j], cst[j]);
+    }
+#pragma unroll
+    for (int i = 0; i < kLdsPerWave; ++i) {
+      const int k = kW * S + w + kW * i;
+      if (k < n && k - kW * S < Lcap) epi(k, sa[S + i], sb[S + i], cst[S + i]);
+    }
+  }
+  // Units this CU can hold (the host plan never assigns more).
+  static constexpr int capacity() { return kW * S + Lcap; }
+};
+
+// ---- K=I rows (down) -------------------------------------------------------
+template <int I, int S, int Lcap>
+struct RowRole {
+  static constexpr int NJ = RowSlots<I>::NJ;
+  static constexpr int RowF4 = NJ * kWave;
+  float4 wv[S][NJ];
+  float4 *rowsl = nullptr;
+  int n = 0;
+
+  template <typename Row>
+  __device__ void prefetch_regs(Row row) {
+    const int w = wave_u();
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      const int k = w + kW * j;
+      if (k < n) {
+        load_row_weights<I>(row(k), wv[j]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < NJ; ++c) wv[j][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  }
+  template <typename Row>
+  __device__ void prefetch_lds(Row row) {
+    const int lane = lane_id();
+    for (int k = kW * S + wave_u(); k < n && k - kW * S < Lcap; k += kW) {
+      const float4 *src = reinterpret_cast<const float4 *>(row(k));
+      float4 *dst = rowsl + (k - kW * S) * RowF4;
+#pragma unroll
+      for (int c = 0; c < NJ; ++c) dma16<0>(src + c * kWave + lane, dst + c * kWave);
+    }
+  }
+  // Each wave's rows (its register slots and at most kLdsPerWave LDS rows)
+  // share every operand float4 read from LDS; the operand is read in
+  // chunks of 4 float4 so the compiler cannot hoist all of it at once.
+  static constexpr int kLdsPerWave = (Lcap + kW - 1) / kW;
+  template <typename Prep, typename Epi, typename Mid>
+  __device__ void compute(const float *x, Prep prep, Epi epi, Mid mid) const {
+    const int w = wave_u(), lane = lane_id();
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    float acc[S + kLdsPerWave];
+#pragma unroll
+    for (int r = 0; r < S + kLdsPerWave; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int c0 = 0; c0 < NJ; c0 += 4) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int c = c0; c < c0 + 4 && c < NJ; ++c) {
+        const float4 xc = x4[c * kWave + lane];
+#pragma unroll
+        for (int j = 0; j < S; ++j) acc[j] = fma4(wv[j][c], xc, acc[j]);
+#pragma unroll
+        for (int i = 0; i < kLdsPerWave; ++i) {
+          const int k = kW * S + w + kW * i;
+          if (k < n && k - kW * S < Lcap)
+            acc[S + i] = fma4(rowsl[(k - kW * S) * RowF4 + c * kWave + lane], xc, acc[S + i]);
+        }
+      }
+    }
+    mid();
+    float res[S + kLdsPerWave];
+#pragma unroll
+    for (int j = 0; j < S + kLdsPerWave; ++j) {
+      const int k = j < S ? w + kW * j : kW * S + w + kW * (j - S);
+      res[j] = k < n ? prep(k) : 0.f;
+      acc[j] = wave_sum(acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      const int k = w + kW * j;
+      if (k < n) epi(k, acc[j], res[j]);
+    }
+#pragma unroll
+    for (int i = 0; i < kLdsPerWave; ++i) {
+      const int k = kW * S + w + kW * i;
+      if (k < n && k - kW * S < Lcap) epi(k, acc[S + i], res[S + i]);
+    }
+  }
+  static constexpr int capacity() { return kW * S + Lcap; }
+};
+
+// 1/rms of x[0..N) over the workgroup: the arithmetic of block_inv_rms
+// (per-thread float4 sums, wave sums, then the wave totals in order; the
+// extra waves add zeros) with the barrier above and the thread count known.
+template <int N>
+__device__ float inv_rms(const float *x, float eps, float *red) {
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  float s = 0.f;
+  for (int c = threadIdx.x; c < N / 4; c += kT) {
+    const float4 v = x4[c];
+    s = fmaf(v.x, v.x, s);
+    s = fmaf(v.y, v.y, s);
+    s = fmaf(v.z, v.z, s);
+    s = fmaf(v.w, v.w, s);
+  }
+  s = wave_sum(s);
+  if (lane_id() == 0) red[wave_u()] = s;
+  lds_barrier();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) t += red[w];
+  lds_barrier();
+  return rsqrtf(t / static_cast<float>(N) + eps);
+}
+
+// Balanced split of `total` items over `parts`: part r gets [begin, end).
+__device__ __forceinline__ int split_begin(int total, int parts, int r) {
+  return static_cast<int>((static_cast<int64_t>(total) * r) / parts);
+}
+
+template <int H, int I, int NQ, int NKV>
+struct Shape {
+  static constexpr int QD = NQ * kHeadDim;
+  static constexpr int KVD = NKV * kHeadDim;
+  static constexpr int G = NQ / NKV;
+  static constexpr int QkvRows = QD + 2 * KVD;
+  static constexpr int QkvUnits = QkvRows / 2;
+  static constexpr int OUnits = H / 2;
+  static constexpr int UnitBytes = PairSlots<H>::NJ * kWave * 16;
+  static constexpr int RowBytes = RowSlots<I>::NJ * kWave * 16;
+  // QKV region: units, biases (whole float4 DMA rows), cos|sin row.
+  static constexpr int BiasF4 = (QkvRows / 4 + kWave - 1) / kWave * kWave;
+  static constexpr int LQ = (kRegionBytes - BiasF4 * 16 - kWave * 16) / UnitBytes;
+  // O region: units, partial records of every head.
+  static constexpr int PartFloats = NQ * kAttnMaxChunks * kPartStride;
+  static constexpr int LO = (kRegionBytes - PartFloats * 4) / UnitBytes;
+  static constexpr int LG = kRegionBytes / UnitBytes;
+  static constexpr int LD = (kRegionBytes - I * 4) / RowBytes;
+  static_assert(QkvRows % 2 == 0 && H % 2 == 0, "row pairs");
+  static_assert(G <= kW && NQ % NKV == 0, "one wave per query head of a group");
+  static_assert(LQ > 0 && LO > 0 && LG > 0 && LD > 0, "LDS plan");
+  static_assert(H <= 1024 && QD <= 1024, "common vectors");
+};
+
+struct AttnRegion {
+  float qs[kW * kHeadDim];
+  float kn[kHeadDim];
+  float vn[kHeadDim];
+  float4 kt[(kHeadDim / 4) * kAttnCap];
+  float vr[kAttnCap * kHeadDim];
+};
+static_assert(sizeof(AttnRegion) <= kRegionBytes, "attention region");
+
+// One role CU's view of the launch: arguments, LDS, tagged vectors, the
+// token state, and the pieces every role shares (the per-token loop, the LM
+// head and the argmax). Each role runs its own loop (run_*), so the register
+// slots of one role are never live in another role's code.
+template <int H, int I, int NQ, int NKV, bool kProfile>
+struct Roles {
+  using Sh = Shape<H, I, NQ, NKV>;
+  static constexpr int QD = Sh::QD, KVD = Sh::KVD, GROUP = Sh::G;
+  static constexpr int NJ = PairSlots<H>::NJ;
+
+  const ResidentArgs &a;
+  Common &cm;
+  unsigned char *region;
+  int rank, nrole, lane, wv, grid;
+  uint32_t per_token;
+  TagVec tqkv, tpart, th1, tact, thid, ttop;
+  Clock<kProfile> clock;
+  uint32_t token, generated = 0, stop_reason = 0;
+  float top = 0.f;
+
+  __device__ Roles(const ResidentArgs &args, unsigned char *lds, int rank_, int nrole_)
+      : a(args),
+        cm(*reinterpret_cast<Common *>(lds)),
+        region(lds + kRegionOffset),
+        rank(rank_),
+        nrole(nrole_),
+        lane(lane_id()),
+        wv(wave_u()),
+        grid(gridDim.x),
+        per_token(5u * args.layers + 1u),
+        tqkv(args.qkv, QD + 2 * KVD),
+        tpart(args.part, NQ * kAttnMaxChunks * kPartStride),
+        th1(args.h1, H),
+        tact(args.act, I),
+        thid(args.hidden, H),
+        ttop(args.top, 4 * gridDim.x),
+        token(args.first_token) {
+    clock.start(&cm.clock);
+  }
+
+  __device__ uint32_t tag(uint32_t seq) const { return a.epoch | (seq + 1u); }
+  // The host plan never gives a CU more units than it holds on chip; a plan
+  // that did is reported as an error (the other CUs' waits then give up).
+  __device__ bool fits(int n, int capacity) const {
+    if (n <= capacity) return true;
+    if (threadIdx.x == 0) atomicOr(a.error, 2u);
+    return false;
+  }
+  __device__ uint32_t seqno(uint32_t t, int l, int s) const { return t * per_token + 5u * l + s; }
+  // Layer l's weight pointers, read through the scalar cache (the table is
+  // written once before any launch): a vector load of it would be waited
+  // for with vmcnt, i.e. behind every store and DMA issued before it.
+  __device__ LayerPtrs layer(int l) const {
+    typedef const __attribute__((address_space(4))) uint64_t kword;
+    kword *src = (kword *)(reinterpret_cast<uint64_t>(a.layer_ptrs) + sizeof(LayerPtrs) * l);
+    LayerPtrs r;
+    uint64_t *dst = reinterpret_cast<uint64_t *>(&r);
+#pragma unroll
+    for (size_t i = 0; i < sizeof(LayerPtrs) / 8; ++i) dst[i] = src[i];
+    return r;
+  }
+  __device__ const float *kv_layer(const float *base, int l) const {
+    return base + static_cast<size_t>(l) * a.capacity * KVD;
+  }
+
+  // The per-token loop. layer(t, l, position) runs one layer of this role
+  // (including the prefetch of its next share) and returns false when a
+  // wait gave up; pre_lds(l, position) / pre_regs(l) issue a layer's share.
+  // defer_first: the role issues even the LDS part of the next token's
+  // layer-0 share after the LM head (its last layer ends right before the
+  // LM head's input poll, which would otherwise queue behind it).
+  template <typename Layer, typename PreLds, typename PreRegs>
+  __device__ void loop(int role, bool defer_first, Layer layer, PreLds pre_lds, PreRegs pre_regs) {
+    pre_lds(0, static_cast<int>(a.start_position));
+    pre_regs(0);
+    clock.lap(2 * role + 1);
+    for (uint32_t t = 0; t < a.max_tokens; ++t) {
+      const int position = static_cast<int>(a.start_position + t);
+      if (token >= static_cast<uint32_t>(a.vocab) || position >= a.capacity) break;
+      const bool traced = a.trace != nullptr && t == a.trace_token;
+      for (int l = 0; l < a.layers; ++l) {
+        clock.at(traced, l);
+        if (!layer(t, l, position)) return;
+      }
+      clock.at(traced, a.layers);
+      if (!lm_head(t)) return;
+      if (defer_first) pre_lds(0, position + 1);
+      pre_regs(0);  // register share of layer 0 for the next token
+      if (!argmax(t)) return;
+      if (traced) clock.flush_trace(a.trace, a.layers, role);
+      generated = t + 1;
+      if (blockIdx.x == 0 && threadIdx.x == 0) a.out_tokens[t] = token;
+      if (token == UINT32_MAX) break;  // every logit NaN
+      if (token == a.eos) {
+        stop_reason = 2u;
+        break;
+      }
+      if (generated >= a.max_tokens) {
+        stop_reason = 1u;
+        break;
+      }
+    }
+    clock.publish(a.stage_ticks, role, rank == 0);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      SeqState *st = a.st;
+      st->position = a.start_position + generated;
+      st->token = token;
+      st->generated = generated;
+      st->stop_reason = stop_reason;
+      st->stopped = 1u;
+      st->top_logit = top;
+      st->eos = a.eos;
+      st->max_tokens = a.max_tokens;
+      st->mode = kModeGenerate;
+    }
+  }
+
+  // ---- LM head + per-CU top-1 (every CU) ------------------------------------
+  __device__ bool lm_head(uint32_t t) {
+    const uint32_t par = t & 1u;
+    const uint32_t tag_last = tag(seqno(t, a.layers - 1, 4));
+    const uint32_t tag_top = tag(t * per_token + 5u * a.layers);
+    const int units = (a.vocab + 1) / 2;
+    const int gw = static_cast<int>(blockIdx.x) * kW + wv;
+    const int stride = grid * kW;
+    auto load = [&](int u, float4 (&w)[NJ]) {
+      if (u < units) {
+        const float *ra = a.head + static_cast<size_t>(2 * u) * H;
+        const float *rb = 2 * u + 1 < a.vocab ? ra + H : ra;
+        load_pair_weights<H>(ra, rb, w);
+      }
+    };
+    float4 w0[NJ], w1[NJ], w2[NJ];
+    const float4 g4 = threadIdx.x < H / 4 ? reinterpret_cast<const float4 *>(a.final_norm)[threadIdx.x]
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    load(gw, w0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!gather<(H / 2 + kT - 1) / kT>(thid, 0, H, tag_last, cm.vec, a.error, cm.flags)) return false;
+    clock.lap(2 * kRoleCount);
+    const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
+    norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
+    lds_barrier();
+    float4 xv[NJ];
+    load_pair_operand<H>(Lds{cm.xn}, xv);
+    float best = -INFINITY;
+    uint32_t best_i = UINT32_MAX;
+    float *logits = a.logits + (a.history ? static_cast<size_t>(t) * a.vocab : 0);
+    auto step = [&](int u, const float4 (&w)[NJ]) {
+      float sa, sb;
+      pair_dot<H>(w, xv, sa, sb);
+      const int r0 = 2 * u;
+      const bool has1 = r0 + 1 < a.vocab;
+      if (lane == 0) {
+        typedef __attribute__((address_space(1))) float gfloat;
+        gfloat *out = (gfloat *)(logits + r0);
+        out[0] = sa;
+        if (has1) out[1] = sb;
+      }
+      if (better(sa, r0, best, best_i)) {
+        best = sa;
+        best_i = r0;
+      }
+      if (has1 && better(sb, r0 + 1, best, best_i)) {
+        best = sb;
+        best_i = r0 + 1;
+      }
+    };
+    load(gw + stride, w1);
+    for (int u = gw; u < units; u += 3 * stride) {
+      load(u + 2 * stride, w2);
+      step(u, w0);
+      if (u + stride >= units) break;
+      load(u + 3 * stride, w0);
+      step(u + stride, w1);
+      if (u + 2 * stride >= units) break;
+      load(u + 4 * stride, w1);
+      step(u + 2 * stride, w2);
+    }
+    if (lane == 0) {
+      cm.bv[wv] = best;
+      cm.bi[wv] = best_i;
+    }
+    lds_barrier();
+    if (threadIdx.x == 0) {
+      for (int v = 1; v < kW; ++v) {
+        if (better(cm.bv[v], cm.bi[v], best, best_i)) {
+          best = cm.bv[v];
+          best_i = cm.bi[v];
+        }
+      }
+      ttop.put(par * 2 * grid + 2 * blockIdx.x, best, tag_top);
+      ttop.put(par * 2 * grid + 2 * blockIdx.x + 1, __builtin_bit_cast(float, best_i), tag_top);
+    }
+    lds_barrier();  // cm.bv/bi are reused by the argmax
+    clock.lap(2 * kRoleCount + 1);
+    return true;
+  }
+
+  // ---- argmax over the workgroup partials (every CU) ------------------------
+  __device__ bool argmax(uint32_t t) {
+    const uint32_t par = t & 1u;
+    const uint32_t tag_top = tag(t * per_token + 5u * a.layers);
+    if (!gather<(kMaxRoleGrid + kT - 1) / kT>(ttop, par * 2 * grid, 2 * grid, tag_top, cm.top,
+                                              a.error, cm.flags))
+      return false;
+    clock.lap(2 * kRoleCount + 2);
+    float best = -INFINITY;
+    uint32_t best_i = UINT32_MAX;
+    for (int p = threadIdx.x; p < grid; p += kT) {
+      const float v = cm.top[2 * p];
+      const uint32_t i = __builtin_bit_cast(uint32_t, cm.top[2 * p + 1]);
+      if (better(v, i, best, best_i)) {
+        best = v;
+        best_i = i;
+      }
+    }
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(best, o, kWave);
+      const uint32_t oi = __shfl_xor(best_i, o, kWave);
+      if (better(ov, oi, best, best_i)) {
+        best = ov;
+        best_i = oi;
+      }
+    }
+    if (lane == 0) {
+      cm.bv[wv] = best;
+      cm.bi[wv] = best_i;
+    }
+    lds_barrier();
+    best = cm.bv[0];
+    best_i = cm.bi[0];
+    for (int v = 1; v < kW; ++v) {
+      if (better(cm.bv[v], cm.bi[v], best, best_i)) {
+        best = cm.bv[v];
+        best_i = cm.bi[v];
+      }
+    }
+    lds_barrier();
+    token = best_i;
+    top = best;
+    clock.lap(2 * kRoleCount + 3);
+    return true;
+  }
+
+  // The layer input (hidden) of layer l, or this token's embedding row at l = 0.
+  __device__ bool layer_input(uint32_t t, int l, int first, int n, float *dst) {
+    if (l == 0) {
+      const float *e = a.embed + static_cast<size_t>(token) * H + first;
+      for (int c = threadIdx.x; c < n; c += kT) dst[c] = e[c];
+      vm_wait();
+      lds_barrier();
+      return true;
+    }
+    return gather<(H / 2 + kT - 1) / kT>(thid, first, n, tag(seqno(t, l - 1, 4)), dst, a.error,
+                                         cm.flags);
+  }
+
+  // ---- QKV ------------------------------------------------------------------
+  __device__ void run_qkv() {
+    const int u0 = split_begin(Sh::QkvUnits, nrole, rank);
+    PairRole<H, kSlotsQ, Sh::LQ> rq;
+    rq.n = split_begin(Sh::QkvUnits, nrole, rank + 1) - u0;
+    rq.units = reinterpret_cast<float4 *>(region);
+    if (!fits(rq.n, rq.capacity())) return;
+    float4 *q_bias = reinterpret_cast<float4 *>(region + Sh::LQ * Sh::UnitBytes);
+    float4 *q_cs = q_bias + Sh::BiasF4;
+    auto rows = [&](int l) {
+      const float *base = layer(l).wqkv;
+      return [=](int k, const float *&ra, const float *&rb) {
+        const int u = u0 + k;
+        const int row = (u / kRotary) * kHeadDim + u % kRotary;
+        ra = base + static_cast<size_t>(row) * H;
+        rb = ra + static_cast<size_t>(kRotary) * H;
+      };
+    };
+    // Biases of every packed row and the cos|sin row of the position
+    // (clamped to the table) travel with the weights.
+    auto pre_lds = [&](int l, int position) {
+      rq.prefetch_lds(rows(l));
+      if (wv != 0) return;
+      const float4 *b4 = reinterpret_cast<const float4 *>(layer(l).bqkv);
+      for (int i = 0; i < Sh::BiasF4 / kWave; ++i) {
+        const int f = i * kWave + lane;
+        dma16<0>(b4 + (f < Sh::QkvRows / 4 ? f : 0), q_bias + i * kWave);
+      }
+      const int p = min(position, a.capacity - 1);
+      const float4 *c4 = reinterpret_cast<const float4 *>(a.rope_cos + static_cast<size_t>(p) * kRotary);
+      const float4 *s4 = reinterpret_cast<const float4 *>(a.rope_sin + static_cast<size_t>(p) * kRotary);
+      constexpr int R4 = kRotary / 4;
+      dma16<0>(lane < R4 ? c4 + lane : (lane < 2 * R4 ? s4 + (lane - R4) : c4), q_cs);
+    };
+    auto pre_regs = [&](int l) { rq.prefetch_regs(rows(l)); };
+    loop(kRoleQkv, false, [&](uint32_t t, int l, int position) {
+      const LayerPtrs lw = layer(l);
+      const uint32_t tag_qkv = tag(seqno(t, l, 0));
+      const float4 g4 = threadIdx.x < H / 4 ? reinterpret_cast<const float4 *>(lw.attn_norm)[threadIdx.x]
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (!layer_input(t, l, 0, H, cm.vec)) return false;
+      clock.lap(2 * kRoleQkv);
+      const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
+      norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
+      lds_barrier();
+      clock.mark(0);
+      float4 xv[NJ];
+      load_pair_operand<H>(Lds{cm.xn}, xv);
+      const float *bias = reinterpret_cast<const float *>(q_bias);
+      const float *cs = reinterpret_cast<const float *>(q_cs);
+      const Coherent kcache(kv_layer(a.k_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
+      const Coherent vcache(kv_layer(a.v_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
+      rq.compute(xv, [&](int k) {
+        const int u = u0 + k;
+        const int ra = (u / kRotary) * kHeadDim + u % kRotary;
+        return make_float4(bias[ra], bias[ra + kRotary], cs[u % kRotary], cs[kRotary + u % kRotary]);
+      }, [&](int k, float sa, float sb, float4 c) {
+        if (lane != 0) return;
+        const int u = u0 + k;
+        const int head = u / kRotary, i = u % kRotary;
+        const float x0 = sa + c.x;
+        const float x1 = sb + c.y;
+        if (head < NQ + NKV) {
+          const float cv = c.z, sv = c.w;
+          const float first = x0 * cv - x1 * sv;
+          const float second = x1 * cv + x0 * sv;
+          if (head < NQ) {
+            tqkv.put(head * kHeadDim + i, first, tag_qkv);
+            tqkv.put(head * kHeadDim + i + kRotary, second, tag_qkv);
+          } else {
+            const int o = (head - NQ) * kHeadDim + i;
+            tqkv.put(QD + o, first, tag_qkv);
+            tqkv.put(QD + o + kRotary, second, tag_qkv);
+            kcache.st(position * KVD + o, first);
+            kcache.st(position * KVD + o + kRotary, second);
+          }
+        } else {
+          const int o = (head - NQ - NKV) * kHeadDim + i;
+          tqkv.put(QD + KVD + o, x0, tag_qkv);
+          tqkv.put(QD + KVD + o + kRotary, x1, tag_qkv);
+          vcache.st(position * KVD + o, x0);
+          vcache.st(position * KVD + o + kRotary, x1);
+        }
+      }, [&] { clock.mark(1); });
+      clock.mark(2);
+      lds_barrier();  // LDS units, biases and cos|sin are rewritten next
+      clock.lap(2 * kRoleQkv + 1);
+      if (l + 1 < a.layers) {
+        pre_lds(l + 1, position);
+        pre_regs(l + 1);
+      } else {
+        pre_lds(0, position + 1);
+      }
+      return true;
+    }, pre_lds, pre_regs);
+  }
+
+  // ---- attention ----------------------------------------------------------
+  // Units (KV head g, chunk c) -> g * chunks + c, handled by attention CU
+  // unit % nrole. A unit stages its chunk's K (by float4 columns) and V rows
+  // in LDS in windows of kAttnCap positions; the first window of a CU's
+  // first unit is loaded ahead with the other roles' weights.
+  __device__ void attn_dma(int l, int g, int wb, int we, AttnRegion &ar) {
+    const float *kc = kv_layer(a.k_cache, l);
+    const float *vc = kv_layer(a.v_cache, l);
+    const int nrow = we - wb;
+    const int nblk = (nrow + kWave - 1) / kWave;
+    for (int i = wv; i < (kHeadDim / 4) * nblk; i += kW) {
+      const int blk = i / (kHeadDim / 4), d4 = i % (kHeadDim / 4);
+      const int pos = min(wb + blk * kWave + lane, a.capacity - 1);
+      dma16<kPolicySc1>(kc + static_cast<size_t>(pos) * KVD + g * kHeadDim + 4 * d4,
+                        ar.kt + d4 * kAttnCap + blk * kWave);
+    }
+    for (int i = wv; i < (nrow + 3) / 4; i += kW) {
+      const int pos = min(wb + 4 * i + lane / 16, a.capacity - 1);
+      dma16<kPolicySc1>(vc + static_cast<size_t>(pos) * KVD + g * kHeadDim + 4 * (lane % 16),
+                        ar.vr + 4 * i * kHeadDim);
+    }
+  }
+
+  __device__ void run_attn() {
+    AttnRegion &ar = *reinterpret_cast<AttnRegion *>(region);
+    auto pre_lds = [&](int l, int position) {
+      const int length = position + 1;
+      const int chunks = attn_chunks(length), cl = attn_chunk_len(length);
+      if (rank >= NKV * chunks || position >= a.capacity) return;
+      const int g = rank / chunks, c = rank % chunks;
+      const int begin = c * cl, end = min(length, begin + cl);
+      attn_dma(l, g, begin, min(end, begin + kAttnCap), ar);
+    };
+    auto pre_regs = [](int) {};
+    loop(kRoleAttn, false, [&](uint32_t t, int l, int position) {
+      const uint32_t tag_qkv = tag(seqno(t, l, 0));
+      const uint32_t tag_part = tag(seqno(t, l, 1));
+      const int length = position + 1;
+      const int chunks = attn_chunks(length), cl = attn_chunk_len(length);
+      const int units = NKV * chunks;
+      bool first_unit = true;
+      for (int u = rank; u < units; u += nrole) {
+        const int g = u / chunks, c = u % chunks;
+        const int begin = c * cl;
+        const int end = min(length, begin + cl);
+        const bool has_new = position >= begin && position < end;
+        if (!first_unit) {
+          lds_barrier();
+          attn_dma(l, g, begin, min(end, begin + kAttnCap), ar);
+        }
+        // The group's queries, then this step's K and V rows.
+        constexpr int qpairs = GROUP * kHeadDim / 2;
+        const int pairs = qpairs + (has_new ? kHeadDim : 0);
+        if (!gather_map<1>(tqkv, pairs, tag_qkv, ar.qs, a.error, cm.flags, [&](int p, uint32_t &s, int &d) {
+              if (p < qpairs) {
+                s = (g * GROUP * kHeadDim) / 2 + p;
+                d = 2 * p;
+              } else if (p < qpairs + kHeadDim / 2) {
+                s = (QD + g * kHeadDim) / 2 + (p - qpairs);
+                d = kW * kHeadDim + 2 * (p - qpairs);
+              } else {
+                s = (QD + KVD + g * kHeadDim) / 2 + (p - qpairs - kHeadDim / 2);
+                d = kW * kHeadDim + kHeadDim + 2 * (p - qpairs - kHeadDim / 2);
+              }
+            }))
+          return false;
+        if (first_unit) clock.lap(2 * kRoleAttn);
+        float m = -INFINITY, lsum = 0.f, acc = 0.f;
+        for (int wb = begin; wb < end; wb += kAttnCap) {
+          const int we = min(end, wb + kAttnCap);
+          if (wb != begin) {
+            lds_barrier();
+            attn_dma(l, g, wb, we, ar);
+            vm_wait();
+            lds_barrier();
+          }
+          if (position >= wb && position < we) {
+            const int j = position - wb;
+            if (threadIdx.x < kHeadDim / 4)
+              ar.kt[threadIdx.x * kAttnCap + j] = reinterpret_cast<const float4 *>(ar.kn)[threadIdx.x];
+            if (threadIdx.x < kHeadDim) ar.vr[j * kHeadDim + threadIdx.x] = ar.vn[threadIdx.x];
+          }
+          lds_barrier();
+          if (wb == begin) clock.mark(0);
+          if (wv < GROUP) {
+            float4 q[kHeadDim / 4];
+#pragma unroll
+            for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
+              q[d4] = reinterpret_cast<const float4 *>(ar.qs + wv * kHeadDim)[d4];
+            attn_head_window([&](int d4, int j) { return ar.kt[d4 * kAttnCap + j]; },
+                             [&](int j, int d) { return ar.vr[j * kHeadDim + d]; }, q, we - wb, m,
+                             lsum, acc);
+          }
+        }
+        clock.mark(1);
+        if (wv < GROUP) {
+          const uint32_t rec = ((g * GROUP + wv) * kAttnMaxChunks + c) * kPartStride;
+          tpart.put(rec + 2 + lane, acc, tag_part);
+          if (lane == 0) {
+            tpart.put(rec, m, tag_part);
+            tpart.put(rec + 1, lsum, tag_part);
+          }
+        }
+        clock.mark(2);
+        first_unit = false;
+      }
+      if (first_unit) clock.lap(2 * kRoleAttn);
+      lds_barrier();  // K/V windows and queries are rewritten next
+      clock.lap(2 * kRoleAttn + 1);
+      if (l + 1 < a.layers)
+        pre_lds(l + 1, position);
+      else
+        pre_lds(0, position + 1);
+      return true;
+    }, pre_lds, pre_regs);
+  }
+
+  // ---- O projection ---------------------------------------------------------
+  __device__ void run_o() {
+    const int u0 = split_begin(Sh::OUnits, nrole, rank);
+    PairRole<QD, kSlotsO, Sh::LO> ro;
+    ro.n = split_begin(Sh::OUnits, nrole, rank + 1) - u0;
+    ro.units = reinterpret_cast<float4 *>(region);
+    if (!fits(ro.n, ro.capacity())) return;
+    float *parts = reinterpret_cast<float *>(region + Sh::LO * Sh::UnitBytes);
+    auto rows = [&](int l) {
+      const float *base = layer(l).wo;
+      return [=](int k, const float *&ra, const float *&rb) {
+        ra = base + static_cast<size_t>(2 * (u0 + k)) * QD;
+        rb = ra + QD;
+      };
+    };
+    auto pre_lds = [&](int l, int) { ro.prefetch_lds(rows(l)); };
+    auto pre_regs = [&](int l) { ro.prefetch_regs(rows(l)); };
+    loop(kRoleO, false, [&](uint32_t t, int l, int position) {
+      const uint32_t tag_part = tag(seqno(t, l, 1));
+      const uint32_t tag_h1 = tag(seqno(t, l, 2));
+      const int C = attn_chunks(position + 1);
+      // Residual rows [2 u0, 2 u0 + 2 n) of the layer input.
+      if (!layer_input(t, l, 2 * u0, 2 * ro.n, cm.vec)) return false;
+      // The partial records of every head, in passes of 4 pairs per thread
+      // (later passes find their records already published).
+      constexpr int kHalf = kPartStride / 2;
+      constexpr int kPer = 4;
+      const int pairs = NQ * C * kHalf;
+      for (int base = 0; base < pairs; base += kPer * kT) {
+        if (!gather_map<kPer>(tpart, min(kPer * kT, pairs - base), tag_part, parts, a.error, cm.flags,
+                              [&](int p, uint32_t &s, int &d) {
+                                const int rec = (base + p) / kHalf, k2 = (base + p) % kHalf;
+                                const int h = rec / C, c = rec % C;
+                                s = (h * kAttnMaxChunks + c) * kHalf + k2;
+                                d = rec * kPartStride + 2 * k2;
+                              }))
+          return false;
+      }
+      clock.lap(2 * kRoleO);
+      for (int e = threadIdx.x; e < QD; e += kT) {
+        const int h = e / kHeadDim, d = e % kHeadDim;
+        const float *rec = parts + h * C * kPartStride;
+        cm.xn[e] = attn_merge([&](int c, int k) { return rec[c * kPartStride + k]; }, C, d);
+      }
+      lds_barrier();
+      float4 xv[PairSlots<QD>::NJ];
+      load_pair_operand<QD>(Lds{cm.xn}, xv);
+      clock.mark(0);
+      ro.compute(xv, [&](int k) { return make_float4(cm.vec[2 * k], cm.vec[2 * k + 1], 0.f, 0.f); },
+                 [&](int k, float sa, float sb, float4 c) {
+                   if (lane != 0) return;
+                   const int u = u0 + k;
+                   th1.put(2 * u, c.x + sa, tag_h1);
+                   th1.put(2 * u + 1, c.y + sb, tag_h1);
+                 },
+                 [&] { clock.mark(1); });
+      clock.mark(2);
+      lds_barrier();
+      clock.lap(2 * kRoleO + 1);
+      if (l + 1 < a.layers) {
+        pre_lds(l + 1, position);
+        pre_regs(l + 1);
+      } else {
+        pre_lds(0, position + 1);
+      }
+      return true;
+    }, pre_lds, pre_regs);
+  }
+
+  // ---- gate/up + SiLU -------------------------------------------------------
+  __device__ void run_gate() {
+    const int u0 = split_begin(I, nrole, rank);
+    PairRole<H, kSlotsG, Sh::LG> rg;
+    rg.n = split_begin(I, nrole, rank + 1) - u0;
+    rg.units = reinterpret_cast<float4 *>(region);
+    if (!fits(rg.n, rg.capacity())) return;
+    auto rows = [&](int l) {
+      const LayerPtrs lp = layer(l);
+      const float *g = lp.wg, *u = lp.wu;
+      return [=](int k, const float *&ra, const float *&rb) {
+        ra = g + static_cast<size_t>(u0 + k) * H;
+        rb = u + static_cast<size_t>(u0 + k) * H;
+      };
+    };
+    auto pre_lds = [&](int l, int) { rg.prefetch_lds(rows(l)); };
+    auto pre_regs = [&](int l) { rg.prefetch_regs(rows(l)); };
+    loop(kRoleGate, false, [&](uint32_t t, int l, int position) {
+      const uint32_t tag_h1 = tag(seqno(t, l, 2));
+      const uint32_t tag_act = tag(seqno(t, l, 3));
+      const float4 g4 = threadIdx.x < H / 4
+                            ? reinterpret_cast<const float4 *>(layer(l).mlp_norm)[threadIdx.x]
+                            : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (!gather<(H / 2 + kT - 1) / kT>(th1, 0, H, tag_h1, cm.vec, a.error, cm.flags)) return false;
+      clock.lap(2 * kRoleGate);
+      const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
+      norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
+      lds_barrier();
+      float4 xv[NJ];
+      load_pair_operand<H>(Lds{cm.xn}, xv);
+      clock.mark(0);
+      rg.compute(xv, [](int) { return make_float4(0.f, 0.f, 0.f, 0.f); },
+                 [&](int k, float gt, float up, float4) {
+                   if (lane == 0) tact.put(u0 + k, gt / (1.f + expf(-gt)) * up, tag_act);
+                 },
+                 [&] { clock.mark(1); });
+      clock.mark(2);
+      lds_barrier();
+      clock.lap(2 * kRoleGate + 1);
+      if (l + 1 < a.layers) {
+        pre_lds(l + 1, position);
+        pre_regs(l + 1);
+      } else {
+        pre_lds(0, position + 1);
+      }
+      return true;
+    }, pre_lds, pre_regs);
+  }
+
+  // ---- down + residual ------------------------------------------------------
+  __device__ void run_down() {
+    const int u0 = split_begin(H, nrole, rank);
+    RowRole<I, kSlotsD, Sh::LD> rd;
+    rd.n = split_begin(H, nrole, rank + 1) - u0;
+    rd.rowsl = reinterpret_cast<float4 *>(region);
+    if (!fits(rd.n, rd.capacity())) return;
+    float *act = reinterpret_cast<float *>(region + Sh::LD * Sh::RowBytes);
+    auto row = [&](int l) {
+      const float *base = layer(l).wd;
+      return [=](int k) { return base + static_cast<size_t>(u0 + k) * I; };
+    };
+    auto pre_lds = [&](int l, int) { rd.prefetch_lds(row(l)); };
+    auto pre_regs = [&](int l) { rd.prefetch_regs(row(l)); };
+    const int hb = u0 & ~1;                       // even start of the h1 rows gathered
+    const int hn = ((u0 + rd.n + 1) & ~1) - hb;   // even count covering [u0, u0 + n)
+    loop(kRoleDown, true, [&](uint32_t t, int l, int position) {
+      const uint32_t tag_h1 = tag(seqno(t, l, 2));
+      const uint32_t tag_act = tag(seqno(t, l, 3));
+      const uint32_t tag_hid = tag(seqno(t, l, 4));
+      if (!gather<(H / 2 + kT - 1) / kT>(th1, hb, hn, tag_h1, cm.vec, a.error, cm.flags)) return false;
+      if (!gather<(I / 2 + kT - 1) / kT>(tact, 0, I, tag_act, act, a.error, cm.flags)) return false;
+      clock.lap(2 * kRoleDown);
+      clock.mark(0);
+      rd.compute(act, [&](int k) { return cm.vec[u0 + k - hb]; }, [&](int k, float s, float h1v) {
+        if (lane == 0) thid.put(u0 + k, h1v + s, tag_hid);
+      }, [&] { clock.mark(1); });
+      clock.mark(2);
+      lds_barrier();
+      clock.lap(2 * kRoleDown + 1);
+      if (l + 1 < a.layers) {  // layer 0 of the next token follows the LM head
+        pre_lds(l + 1, position);
+        pre_regs(l + 1);
+      }
+      return true;
+    }, pre_lds, pre_regs);
+  }
+};
+
+// Each role's loop is its own (non-inlined) function so the register
+// allocator sizes each role separately instead of one body holding all five.
+template <int H, int I, int NQ, int NKV, bool kProfile, int kRole>
+__device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank, int nrole) {
+  // The launch arguments, copied with scalar loads from the kernel's
+  // argument segment (whose address the kernel passes: a callee has no
+  // kernarg segment pointer of its own, and the address of the kernel's
+  // by-value parameter would name a private stack copy) into a local the
+  // compiler keeps in SGPRs.
+  ResidentArgs a;
+  {
+    typedef const __attribute__((address_space(4))) uint32_t kword;
+    // readfirstlane returns a signed int: each half is taken as uint32_t
+    // before widening, or bit 31 of the low half would sign-extend into the
+    // high half and the address would be non-canonical.
+    const uint64_t addr = reinterpret_cast<uint64_t>(kernarg);
+    const uint64_t lo =
+        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr)));
+    const uint64_t hi =
+        static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(addr >> 32)));
+    kword *src = (kword *)((hi << 32) | lo);
+    uint32_t *dst = reinterpret_cast<uint32_t *>(&a);
+#pragma unroll
+    for (size_t i = 0; i < sizeof(ResidentArgs) / 4; ++i) dst[i] = src[i];
+  }
+  Roles<H, I, NQ, NKV, kProfile> r(a, roles_lds, __builtin_amdgcn_readfirstlane(rank),
+                                   __builtin_amdgcn_readfirstlane(nrole));
+  if constexpr (kRole == kRoleQkv) r.run_qkv();
+  if constexpr (kRole == kRoleAttn) r.run_attn();
+  if constexpr (kRole == kRoleO) r.run_o();
+  if constexpr (kRole == kRoleGate) r.run_gate();
+  if constexpr (kRole == kRoleDown) r.run_down();
+}
+
+template <int H, int I, int NQ, int NKV, bool kProfile>
+__global__ __launch_bounds__(kT, 1) void roles_kernel(ResidentArgs a) {
+  const void *kernarg = (const void *)__builtin_amdgcn_kernarg_segment_ptr();
+  const int b = blockIdx.x;
+  int role = 0;
+  while (role < kRoleCount - 1 && b >= a.role_end[role]) ++role;
+  const int rbeg = role ? a.role_end[role - 1] : 0;
+  const int rank = b - rbeg, nrole = a.role_end[role] - rbeg;
+  switch (role) {
+    case kRoleQkv:
+      run_role<H, I, NQ, NKV, kProfile, kRoleQkv>(kernarg, rank, nrole);
+      break;
+    case kRoleAttn:
+      run_role<H, I, NQ, NKV, kProfile, kRoleAttn>(kernarg, rank, nrole);
+      break;
+    case kRoleO:
+      run_role<H, I, NQ, NKV, kProfile, kRoleO>(kernarg, rank, nrole);
+      break;
+    case kRoleGate:
+      run_role<H, I, NQ, NKV, kProfile, kRoleGate>(kernarg, rank, nrole);
+      break;
+    default:
+      run_role<H, I, NQ, NKV, kProfile, kRoleDown>(kernarg, rank, nrole);
+      break;
+  }
+}
+
+using Qwen = Shape<896, 4864, 14, 2>;
+const void *roles_fn(bool profile) {
+  return profile ? reinterpret_cast<const void *>(&roles_kernel<896, 4864, 14, 2, true>)
+                 : reinterpret_cast<const void *>(&roles_kernel<896, 4864, 14, 2, false>);
+}
+
+}  // namespace
+
+bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int max_length,
+                RolePlan *plan) {
+  if (hidden != 896 || inter != 4864 || heads != 14 || kv_heads != 2) return false;
+  if (grid > kMaxRoleGrid || max_length < 1) return false;
+  // Units per role, their capacity per CU (LDS + register slots) and bytes.
+  const int units[4] = {Qwen::QkvUnits, Qwen::OUnits, inter, hidden};
+  const int cap[4] = {Qwen::LQ + kW * kSlotsQ, Qwen::LO + kW * kSlotsO, Qwen::LG + kW * kSlotsG,
+                      Qwen::LD + kW * kSlotsD};
+  const double bytes[4] = {double(units[0]) * Qwen::UnitBytes, double(units[1]) * Qwen::UnitBytes,
+                           double(units[2]) * Qwen::UnitBytes, double(units[3]) * Qwen::RowBytes};
+  const double total = bytes[0] + bytes[1] + bytes[2] + bytes[3];
+  int floor_weights = 0;
+  for (int r = 0; r < 4; ++r) floor_weights += (units[r] + cap[r] - 1) / cap[r];
+  // One attention CU per (KV head, chunk) unit of the longest context, or
+  // as many as the weight roles leave (an attention CU then takes several
+  // units, the later ones staged after its query arrives).
+  const int n_attn = std::min(kv_heads * attn_chunks(max_length), grid - floor_weights);
+  if (n_attn < 1) return false;
+  const int rest = grid - n_attn;
+  int n[4], used = 0;
+  for (int r = 0; r < 4; ++r) {
+    const int need = (units[r] + cap[r] - 1) / cap[r];
+    n[r] = std::max(need, static_cast<int>(rest * bytes[r] / total));
+    n[r] = std::min(n[r], units[r]);
+    used += n[r];
+  }
+  if (rest <= 0) return false;
+  // Hand out or take back the remainder by the largest per-CU share.
+  while (used != rest) {
+    int pick = -1;
+    double best = used < rest ? -1.0 : 1e30;
+    for (int r = 0; r < 4; ++r) {
+      const double share = bytes[r] / n[r];
+      const int need = (units[r] + cap[r] - 1) / cap[r];
+      if (used < rest && n[r] < units[r] && share > best) {
+        best = share;
+        pick = r;
+      }
+      if (used > rest && n[r] > need && bytes[r] / (n[r] - 1) < best) {
+        best = bytes[r] / (n[r] - 1);
+        pick = r;
+      }
+    }
+    if (pick < 0) return false;
+    n[pick] += used < rest ? 1 : -1;
+    used += used < rest ? 1 : -1;
+  }
+  plan->end[kRoleQkv] = n[0];
+  plan->end[kRoleAttn] = n[0] + n_attn;
+  plan->end[kRoleO] = plan->end[kRoleAttn] + n[1];
+  plan->end[kRoleGate] = plan->end[kRoleO] + n[2];
+  plan->end[kRoleDown] = plan->end[kRoleGate] + n[3];
+  return plan->end[kRoleDown] == grid;
+}
+
+hipError_t launch_roles(hipStream_t s, const ResidentArgs &args, int grid) {
+  void *params[] = {const_cast<ResidentArgs *>(&args)};
+  return hipLaunchCooperativeKernel(roles_fn(args.stage_ticks || args.trace), dim3(grid), dim3(kT),
+                                    params, 0, s);
+}
+
+int roles_max_grid(int device) {
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, roles_fn(true), kT, 0) != hipSuccess)
+    return 0;
+  return cus * per_cu;
+}
+
+}  // namespace qd
