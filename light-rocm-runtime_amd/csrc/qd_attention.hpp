@@ -183,43 +183,40 @@ __device__ void attn_partial_unit(const KvSrc &kcache, const KvSrc &vcache,
 // One query head over the positions [0, n) of a chunk, computed by one wave;
 // the resident role kernel (K/V staged in LDS) and the stream-ordered kernel
 // (K/V read from the cache) both run it, so their partials are bit-identical.
-// Passes of 64 positions: lane = position for the scores (64-dim dot in
+// Blocks of 64 positions: lane = position for the scores (64-dim dot in
 // order d = 0..63, scale 1/sqrt(64)), an online softmax (running max m, sum
-// l), then P.V with lane = output dim, accumulating positions in order.
-// k4(d4, j) returns float4 d4 of position j's K row and v(j, d) element d of
-// its V row; positions j >= n are never read for V and their scores are
-// masked (k4 must still return something finite-or-not for them). q holds
-// the head's 64 query values; (m, l, acc) carry the state across calls, so a
-// chunk may be walked in windows whose lengths are multiples of 64.
+// l), then P.V with lane = output dim: position u of the block feeds
+// accumulator u % 4, the four combine as (a0 + a1) + (a2 + a3) and the block
+// sum is added to the rescaled running acc. k4(d4, j) returns float4 d4 of
+// position j's K row and v(j, d) element d of its V row; both are called
+// only with j < n (the positions of a partial last block read row n - 1,
+// with their probabilities masked to 0). q holds the head's 64 query values;
+// (m, l, acc) carry the state across calls, so a chunk may be walked in
+// windows whose lengths are multiples of 64.
 template <typename K4, typename V>
 __device__ __forceinline__ void attn_head_window(K4 k4, V v, const float4 (&q)[kHeadDim / 4], int n,
                                                  float &m, float &l, float &acc) {
   const int lane = lane_id();
   const float scale = rsqrtf(static_cast<float>(kHeadDim));
   for (int base = 0; base < n; base += kWave) {
-    const int j = base + lane;
+    const int last = n - 1 - base;  // wave-uniform: positions past it are masked
+    float4 kr[kHeadDim / 4];
+#pragma unroll
+    for (int d4 = 0; d4 < kHeadDim / 4; ++d4) kr[d4] = k4(d4, base + min(lane, last));
     float s = 0.f;
 #pragma unroll
-    for (int d4 = 0; d4 < kHeadDim / 4; ++d4) s = fma4(k4(d4, j), q[d4], s);
-    const bool in = j < n;
-    const float sv = in ? s * scale : -INFINITY;
+    for (int d4 = 0; d4 < kHeadDim / 4; ++d4) s = fma4(kr[d4], q[d4], s);
+    const float sv = lane <= last ? s * scale : -INFINITY;
     const float m_new = fmaxf(m, wave_max(sv));
     const float p = m_new == -INFINITY ? 0.f : expf(sv - m_new);
     const float corr = m_new == -INFINITY ? 1.f : expf(m - m_new);
     l = fmaf(l, corr, wave_sum(p));
     m = m_new;
-    float a = acc * corr;
-    // Positions in order; eight V reads in flight at a time.
-    const int cnt = min(kWave, n - base);
-    for (int j0 = 0; j0 < cnt; j0 += 8) {
-      float vv[8];
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int u = 0; u < 8; ++u) vv[u] = j0 + u < cnt ? v(base + j0 + u, lane) : 0.f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (j0 + u < cnt) a = fmaf(read_lane(p, j0 + u), vv[u], a);
-    }
-    acc = a;
+    for (int u = 0; u < kWave; ++u)
+      a[u & 3] = fmaf(read_lane(p, u), v(base + min(u, last), lane), a[u & 3]);
+    acc = fmaf(acc, corr, (a[0] + a[1]) + (a[2] + a[3]));
   }
 }
 

@@ -128,14 +128,15 @@ struct Plain {
   }
 };
 
-// Streaming weight load: each weight is read once per token. The pointer is
-// taken as global memory so the load is a global_load (vmcnt only); a flat
-// load would also hold lgkmcnt, making every LDS wait behind it wait for the
-// weights in flight too.
+// Streaming weight load: each weight is read once per token, so the load is
+// non-temporal (it does not displace cached lines: code, activations). The
+// pointer is taken as global memory so the load is a global_load (vmcnt
+// only); a flat load would also hold lgkmcnt, making every LDS wait behind
+// it wait for the weights in flight too.
 typedef float gf32x4 __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(1))) gf32x4 global_f32x4;
 __device__ __forceinline__ float4 ld_weight(const float4 *p) {
-  const gf32x4 v = *(global_f32x4 *)p;
+  const gf32x4 v = __builtin_nontemporal_load((global_f32x4 *)p);
   return make_float4(v.x, v.y, v.z, v.w);
 }
 

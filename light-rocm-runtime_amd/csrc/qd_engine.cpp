@@ -123,6 +123,8 @@ struct qd_engine {
   // Resident megakernel state.
   qd::LayerPtrs *layer_ptrs_dev = nullptr;  // [layers]
   uint64_t *tagged = nullptr;               // (value, tag) arena
+  float *roles_slots = nullptr;             // role kernel hand-off slots
+  size_t roles_slot_bytes = 0;
   size_t tagged_elems = 0;
   uint32_t epoch = 0;                       // last launch epoch (1..4095)
   uint32_t *resident_error = nullptr;       // [1]
@@ -563,6 +565,9 @@ struct qd_engine {
       const int reach = static_cast<int>(positions[seq] + max_tokens);
       if (qd::plan_roles(roles_grid, int(H), int(I), int(NQ), int(NKV), reach, &plan)) {
         for (int r = 0; r < qd::kRoleCount; ++r) ra.role_end[r] = plan.end[r];
+        // Every hand-off slot starts empty (all bits set).
+        check(hipMemsetAsync(roles_slots, 0xFF, roles_slot_bytes, stream), "memset");
+        ra.slots = roles_slots;
         return qd::launch_roles(stream, ra, roles_grid);
       }
     }
@@ -794,6 +799,11 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
                                                 grid_alloc);
     e->tagged = e->alloc<uint64_t>(e->tagged_elems);
     check(hipMemsetAsync(e->tagged, 0, e->tagged_elems * 8, e->stream), "memset");
+    if (e->roles_grid) {
+      e->roles_slot_bytes = 2 * e->L * 4 *
+                            qd::roles_slot_floats(int(e->H), int(e->I), int(e->NQ), int(e->NKV));
+      e->roles_slots = e->alloc<float>(e->roles_slot_bytes / 4);
+    }
     e->resident_error = e->alloc<uint32_t>(1);
     e->sync();
     *out = e.release();

@@ -128,7 +128,7 @@ __global__ __launch_bounds__(kWave) void attn_partial_kernel(
   float m = -INFINITY, l = 0.f, acc = 0.f;
   attn_head_window(
       [&](int d4, int j) {
-        return reinterpret_cast<const float4 *>(kb + static_cast<size_t>(min(j, n - 1)) * kv_dim)[d4];
+        return reinterpret_cast<const float4 *>(kb + static_cast<size_t>(j) * kv_dim)[d4];
       },
       [&](int j, int d) { return vb[static_cast<size_t>(j) * kv_dim + d]; }, qv, n, m, l, acc);
   float *rec = part + (h * kAttnMaxChunks + chunk) * kPartStride;

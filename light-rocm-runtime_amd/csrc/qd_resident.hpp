@@ -46,6 +46,8 @@ struct ResidentArgs {
   void *act;                    // tagged [intermediate]
   void *hidden;                 // tagged [hidden]
   void *top;                    // tagged [2 * grid]
+  float *slots;                 // role kernel: [layers][2][roles_slot_floats] hand-off
+                                //   slots, all bits set (kSlotEmpty) at launch
   float *logits;                // [vocab] or [max_tokens][vocab]
   uint32_t *out_tokens;         // [max_tokens]
   SeqState *st;
@@ -76,6 +78,19 @@ inline size_t resident_tagged_elems(int hidden, int heads, int kv_heads, int int
   (void)kv_heads;
   return 4 * size_t(heads) * 64 + 16 * size_t(heads) * 66 + 3 * size_t(hidden) + inter +
          4 * size_t(grid);
+}
+
+// Role kernel hand-off slots. Per (layer, token parity) one block of plain
+// floats, in order: the QKV output [q | k | v], the attention partial
+// records [heads][kAttnMaxChunks][kRoleRecStride] (m, l, 2 pad, acc[64]),
+// h1 [hidden], the MLP activation [intermediate] and the layer output
+// [hidden]. A slot holds kSlotEmpty until written; a bit pattern no
+// arithmetic produces (a NaN with every payload bit set).
+constexpr int kRoleRecStride = 68;
+constexpr uint32_t kSlotEmpty = 0xFFFFFFFFu;
+constexpr size_t roles_slot_floats(int hidden, int inter, int heads, int kv_heads) {
+  return size_t(heads + 2 * kv_heads) * 64 + size_t(heads) * kAttnMaxChunks * kRoleRecStride +
+         2 * size_t(hidden) + size_t(inter);
 }
 
 hipError_t launch_resident(hipStream_t s, const ResidentArgs &args, int grid);

@@ -209,6 +209,82 @@ __device__ bool gather(const TagVec &src, uint32_t first, int n, uint32_t tag, f
   });
 }
 
+// One (layer, token parity) block of hand-off slots: plain floats with
+// device-scope access, kSlotEmpty until written; bounds-checked by the
+// buffer descriptor.
+struct Slots {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ Slots(float *base, uint32_t floats)
+      : r(__builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(floats * 4u), kRsrcWord3)) {}
+  __device__ void put(uint32_t i, float v) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, i * 4u, 0, kPolicySc1);
+  }
+  __device__ void clear(uint32_t i) const {
+    __builtin_amdgcn_raw_buffer_store_b32(kSlotEmpty, r, i * 4u, 0, kPolicySc1);
+  }
+  __device__ u32x4 get4(uint32_t i4) const {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, i4 * 16u, 0, kPolicySc1));
+  }
+};
+struct Quad {
+  uint32_t w[4];
+};
+
+// Whole-workgroup wait for n4 float4s of hand-off slots: map(p, s4, d4)
+// names float4 p's slot index and its destination index in dst. A float4
+// is complete when none of its words is kSlotEmpty. Returns false when the
+// wait gave up (error raised).
+template <int kMaxPer, typename Map>
+__device__ bool gather4(const Slots &src, int n4, float4 *dst, uint32_t *error, uint32_t *flags,
+                        Map map) {
+  const int t = threadIdx.x;
+  uint32_t pending = 0;
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k)
+    if (t + k * kT < n4) pending |= 1u << k;
+  for (uint32_t spin = 0;; ++spin) {
+    Quad got[kMaxPer];
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k)
+      if ((pending >> k) & 1u) {
+        int s, d;
+        map(t + k * kT, s, d);
+        got[k] = __builtin_bit_cast(Quad, src.get4(s));
+      }
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+      const Quad &g = got[k];
+      if (((pending >> k) & 1u) && g.w[0] != kSlotEmpty && g.w[1] != kSlotEmpty &&
+          g.w[2] != kSlotEmpty && g.w[3] != kSlotEmpty) {
+        int s, d;
+        map(t + k * kT, s, d);
+        dst[d] = make_float4(__uint_as_float(g.w[0]), __uint_as_float(g.w[1]), __uint_as_float(g.w[2]),
+                             __uint_as_float(g.w[3]));
+        pending &= ~(1u << k);
+      }
+    }
+    // Every wave's earlier vector memory operations (its LDS DMA and its
+    // slot clears above all) are complete when the gather returns.
+    vm_wait();
+    if (block_all(pending == 0, flags)) return true;
+    if (spin > kSpinLimit) {
+      if (t == 0) atomicOr(error, 1u);
+      return false;
+    }
+  }
+}
+
+// Contiguous float4s [first4, first4 + n4) of a slot block -> dst[0, n4).
+template <int kMaxPer>
+__device__ bool gather4c(const Slots &src, int first4, int n4, float *dst, uint32_t *error,
+                         uint32_t *flags) {
+  return gather4<kMaxPer>(src, n4, reinterpret_cast<float4 *>(dst), error, flags,
+                          [&](int p, int &s, int &d) {
+                            s = first4 + p;
+                            d = p;
+                          });
+}
+
 // Profiling clock kept by thread 0 (profiled variant only). Totals and the
 // traced token's stamps live in LDS and reach global memory only when the
 // traced token ends and at exit: a global store here would make the role's
@@ -329,7 +405,7 @@ struct PairRole {
       for (int c = 0; c < NJ; ++c) {
         const int f = c * kWave + lane;
         const float4 *src = f < K4 ? a4 + f : (f < 2 * K4 ? b4 + (f - K4) : a4);
-        dma16<0>(src, dst + c * kWave);
+        dma16<kPolicyNt>(src, dst + c * kWave);
       }
     }
   }
@@ -338,8 +414,8 @@ struct PairRole {
   // counts stores too, so an LDS read issued after a store (the compiler
   // guards LDS reads behind the pending DMA with vmcnt(0)) would wait for
   // the store's round trip.
-  // prep(k) returns the per-unit constants the epilogue needs from LDS; all
-  // of them are read before the first epilogue store for the same reason.
+  // prep(k) returns the per-unit constants the epilogue needs from LDS; it
+  // is read before the unit's epilogue stores for the same reason.
   static constexpr int kLdsPerWave = (Lcap + kW - 1) / kW;
   template <typename Prep, typename Epi, typename Mid>
   __device__ void compute(const float4 (&xv)[NJ], Prep prep, Epi epi, Mid mid) const {
@@ -360,22 +436,18 @@ struct PairRole {
       }
     }
     mid();
-    float4 cst[S + kLdsPerWave];
+    // Unit j of the wave (register slot j, then LDS unit j - S) finishes in
+    // lane j: the sums move there and all the wave's epilogues run at once.
+    constexpr int kUnits = S + kLdsPerWave;
+    static_assert(kUnits <= kWave, "one lane per unit");
+    float ma = 0.f, mb = 0.f;
 #pragma unroll
-    for (int j = 0; j < S + kLdsPerWave; ++j) {
-      const int k = j < S ? w + kW * j : kW * S + w + kW * (j - S);
-      cst[j] = k < n ? prep(k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < kUnits; ++j) {
+      ma = lane == j ? sa[j] : ma;
+      mb = lane == j ? sb[j] : mb;
     }
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      const int k = w + kW * j;
-      if (k < n) epi(k, sa[j], sb[j], cst[j]);
-    }
-#pragma unroll
-    for (int i = 0; i < kLdsPerWave; ++i) {
-      const int k = kW * S + w + kW * i;
-      if (k < n && k - kW * S < Lcap) epi(k, sa[S + i], sb[S + i], cst[S + i]);
-    }
+    const int k = lane < S ? w + kW * lane : kW * S + w + kW * (lane - S);
+    if (lane < kUnits && k < n && (lane < S || k - kW * S < Lcap)) epi(k, ma, mb, prep(k));
   }
   // Units this CU can hold (the host plan never assigns more).
   static constexpr int capacity() { return kW * S + Lcap; }
@@ -411,7 +483,7 @@ struct RowRole {
       const float4 *src = reinterpret_cast<const float4 *>(row(k));
       float4 *dst = rowsl + (k - kW * S) * RowF4;
 #pragma unroll
-      for (int c = 0; c < NJ; ++c) dma16<0>(src + c * kWave + lane, dst + c * kWave);
+      for (int c = 0; c < NJ; ++c) dma16<kPolicyNt>(src + c * kWave + lane, dst + c * kWave);
     }
   }
   // Each wave's rows (its register slots and at most kLdsPerWave LDS rows)
@@ -442,23 +514,17 @@ struct RowRole {
       }
     }
     mid();
-    float res[S + kLdsPerWave];
+    // Row j of the wave finishes in lane j (see PairRole::compute).
+    constexpr int kUnits = S + kLdsPerWave;
+    static_assert(kUnits <= kWave, "one lane per row");
+    float mine = 0.f;
 #pragma unroll
-    for (int j = 0; j < S + kLdsPerWave; ++j) {
-      const int k = j < S ? w + kW * j : kW * S + w + kW * (j - S);
-      res[j] = k < n ? prep(k) : 0.f;
-      acc[j] = wave_sum(acc[j]);
+    for (int j = 0; j < kUnits; ++j) {
+      const float sum = wave_sum(acc[j]);
+      mine = lane == j ? sum : mine;
     }
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      const int k = w + kW * j;
-      if (k < n) epi(k, acc[j], res[j]);
-    }
-#pragma unroll
-    for (int i = 0; i < kLdsPerWave; ++i) {
-      const int k = kW * S + w + kW * i;
-      if (k < n && k - kW * S < Lcap) epi(k, acc[S + i], res[S + i]);
-    }
+    const int k = lane < S ? w + kW * lane : kW * S + w + kW * (lane - S);
+    if (lane < kUnits && k < n && (lane < S || k - kW * S < Lcap)) epi(k, mine, prep(k));
   }
   static constexpr int capacity() { return kW * S + Lcap; }
 };
@@ -506,7 +572,7 @@ struct Shape {
   static constexpr int BiasF4 = (QkvRows / 4 + kWave - 1) / kWave * kWave;
   static constexpr int LQ = (kRegionBytes - BiasF4 * 16 - kWave * 16) / UnitBytes;
   // O region: units, partial records of every head.
-  static constexpr int PartFloats = NQ * kAttnMaxChunks * kPartStride;
+  static constexpr int PartFloats = NQ * kAttnMaxChunks * kRoleRecStride;
   static constexpr int LO = (kRegionBytes - PartFloats * 4) / UnitBytes;
   static constexpr int LG = kRegionBytes / UnitBytes;
   static constexpr int LD = (kRegionBytes - I * 4) / RowBytes;
@@ -540,7 +606,7 @@ struct Roles {
   unsigned char *region;
   int rank, nrole, lane, wv, grid;
   uint32_t per_token;
-  TagVec tqkv, tpart, th1, tact, thid, ttop;
+  TagVec ttop;
   Clock<kProfile> clock;
   uint32_t token, generated = 0, stop_reason = 0;
   float top = 0.f;
@@ -555,17 +621,36 @@ struct Roles {
         wv(wave_u()),
         grid(gridDim.x),
         per_token(5u * args.layers + 1u),
-        tqkv(args.qkv, QD + 2 * KVD),
-        tpart(args.part, NQ * kAttnMaxChunks * kPartStride),
-        th1(args.h1, H),
-        tact(args.act, I),
-        thid(args.hidden, H),
         ttop(args.top, 4 * gridDim.x),
         token(args.first_token) {
     clock.start(&cm.clock);
   }
 
   __device__ uint32_t tag(uint32_t seq) const { return a.epoch | (seq + 1u); }
+  // Hand-off vectors inside a slot block (kRoleRecStride-float records).
+  static constexpr int kOffQkv = 0;
+  static constexpr int kOffPart = QD + 2 * KVD;
+  static constexpr int kOffH1 = kOffPart + Sh::PartFloats;
+  static constexpr int kOffAct = kOffH1 + H;
+  static constexpr int kOffHid = kOffAct + I;
+  static constexpr int kSlotFloats = kOffHid + H;
+  static_assert(kSlotFloats == roles_slot_floats(H, I, NQ, NKV) && kOffPart % 4 == 0 && H % 4 == 0 &&
+                    I % 4 == 0 && kRoleRecStride % 4 == 0,
+                "slot layout");
+  // A vector of layer l's slot block for token t (the block of t's parity).
+  // Token t's writers also clear their slots in the other parity's block
+  // (token t + 1's): every CU has finished token t - 1, whose values it
+  // held, before any CU starts token t (each waits for the argmax), and the
+  // clears are complete (vmcnt) before the writer's next gather returns.
+  __device__ Slots slots(int l, uint32_t t, int off, int n) const {
+    return Slots(a.slots + (static_cast<size_t>(l) * 2 + (t & 1u)) * kSlotFloats + off,
+                 static_cast<uint32_t>(n));
+  }
+  __device__ Slots s_qkv(int l, uint32_t t) const { return slots(l, t, kOffQkv, QD + 2 * KVD); }
+  __device__ Slots s_part(int l, uint32_t t) const { return slots(l, t, kOffPart, Sh::PartFloats); }
+  __device__ Slots s_h1(int l, uint32_t t) const { return slots(l, t, kOffH1, H); }
+  __device__ Slots s_act(int l, uint32_t t) const { return slots(l, t, kOffAct, I); }
+  __device__ Slots s_hid(int l, uint32_t t) const { return slots(l, t, kOffHid, H); }
   // The host plan never gives a CU more units than it holds on chip; a plan
   // that did is reported as an error (the other CUs' waits then give up).
   __device__ bool fits(int n, int capacity) const {
@@ -645,7 +730,6 @@ struct Roles {
   // ---- LM head + per-CU top-1 (every CU) ------------------------------------
   __device__ bool lm_head(uint32_t t) {
     const uint32_t par = t & 1u;
-    const uint32_t tag_last = tag(seqno(t, a.layers - 1, 4));
     const uint32_t tag_top = tag(t * per_token + 5u * a.layers);
     const int units = (a.vocab + 1) / 2;
     const int gw = static_cast<int>(blockIdx.x) * kW + wv;
@@ -662,7 +746,8 @@ struct Roles {
                                          : make_float4(0.f, 0.f, 0.f, 0.f);
     load(gw, w0);
     __builtin_amdgcn_sched_barrier(0);
-    if (!gather<(H / 2 + kT - 1) / kT>(thid, 0, H, tag_last, cm.vec, a.error, cm.flags)) return false;
+    if (!gather4c<(H / 4 + kT - 1) / kT>(s_hid(a.layers - 1, t), 0, H / 4, cm.vec, a.error, cm.flags))
+      return false;
     clock.lap(2 * kRoleCount);
     const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
     norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
@@ -770,17 +855,17 @@ struct Roles {
     return true;
   }
 
-  // The layer input (hidden) of layer l, or this token's embedding row at l = 0.
-  __device__ bool layer_input(uint32_t t, int l, int first, int n, float *dst) {
+  // Floats [4 first4, 4 (first4 + n4)) of layer l's input (the previous
+  // layer's output, or this token's embedding row at l = 0) -> dst.
+  __device__ bool layer_input(uint32_t t, int l, int first4, int n4, float *dst) {
     if (l == 0) {
-      const float *e = a.embed + static_cast<size_t>(token) * H + first;
-      for (int c = threadIdx.x; c < n; c += kT) dst[c] = e[c];
+      const float4 *e = reinterpret_cast<const float4 *>(a.embed + static_cast<size_t>(token) * H) + first4;
+      for (int c = threadIdx.x; c < n4; c += kT) reinterpret_cast<float4 *>(dst)[c] = e[c];
       vm_wait();
       lds_barrier();
       return true;
     }
-    return gather<(H / 2 + kT - 1) / kT>(thid, first, n, tag(seqno(t, l - 1, 4)), dst, a.error,
-                                         cm.flags);
+    return gather4c<(H / 4 + kT - 1) / kT>(s_hid(l - 1, t), first4, n4, dst, a.error, cm.flags);
   }
 
   // ---- QKV ------------------------------------------------------------------
@@ -809,21 +894,31 @@ struct Roles {
       const float4 *b4 = reinterpret_cast<const float4 *>(layer(l).bqkv);
       for (int i = 0; i < Sh::BiasF4 / kWave; ++i) {
         const int f = i * kWave + lane;
-        dma16<0>(b4 + (f < Sh::QkvRows / 4 ? f : 0), q_bias + i * kWave);
+        dma16<kPolicyNt>(b4 + (f < Sh::QkvRows / 4 ? f : 0), q_bias + i * kWave);
       }
       const int p = min(position, a.capacity - 1);
       const float4 *c4 = reinterpret_cast<const float4 *>(a.rope_cos + static_cast<size_t>(p) * kRotary);
       const float4 *s4 = reinterpret_cast<const float4 *>(a.rope_sin + static_cast<size_t>(p) * kRotary);
       constexpr int R4 = kRotary / 4;
-      dma16<0>(lane < R4 ? c4 + lane : (lane < 2 * R4 ? s4 + (lane - R4) : c4), q_cs);
+      dma16<kPolicyNt>(lane < R4 ? c4 + lane : (lane < 2 * R4 ? s4 + (lane - R4) : c4), q_cs);
     };
     auto pre_regs = [&](int l) { rq.prefetch_regs(rows(l)); };
     loop(kRoleQkv, false, [&](uint32_t t, int l, int position) {
       const LayerPtrs lw = layer(l);
-      const uint32_t tag_qkv = tag(seqno(t, l, 0));
+      const Slots out = s_qkv(l, t);
+      {
+        // Unit u's rows land at (u / 32) * 64 + u % 32 and 32 further on:
+        // packed head u / 32 is a query head, then the K and V heads.
+        const Slots next = s_qkv(l, t + 1);
+        for (int k = threadIdx.x; k < rq.n; k += kT) {
+          const int u = u0 + k;
+          next.clear((u / kRotary) * kHeadDim + u % kRotary);
+          next.clear((u / kRotary) * kHeadDim + u % kRotary + kRotary);
+        }
+      }
       const float4 g4 = threadIdx.x < H / 4 ? reinterpret_cast<const float4 *>(lw.attn_norm)[threadIdx.x]
                                            : make_float4(0.f, 0.f, 0.f, 0.f);
-      if (!layer_input(t, l, 0, H, cm.vec)) return false;
+      if (!layer_input(t, l, 0, H / 4, cm.vec)) return false;
       clock.lap(2 * kRoleQkv);
       const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
       norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
@@ -840,29 +935,26 @@ struct Roles {
         const int ra = (u / kRotary) * kHeadDim + u % kRotary;
         return make_float4(bias[ra], bias[ra + kRotary], cs[u % kRotary], cs[kRotary + u % kRotary]);
       }, [&](int k, float sa, float sb, float4 c) {
-        if (lane != 0) return;
         const int u = u0 + k;
         const int head = u / kRotary, i = u % kRotary;
+        const int slot = head * kHeadDim + i;
         const float x0 = sa + c.x;
         const float x1 = sb + c.y;
         if (head < NQ + NKV) {
           const float cv = c.z, sv = c.w;
           const float first = x0 * cv - x1 * sv;
           const float second = x1 * cv + x0 * sv;
-          if (head < NQ) {
-            tqkv.put(head * kHeadDim + i, first, tag_qkv);
-            tqkv.put(head * kHeadDim + i + kRotary, second, tag_qkv);
-          } else {
+          out.put(slot, first);
+          out.put(slot + kRotary, second);
+          if (head >= NQ) {
             const int o = (head - NQ) * kHeadDim + i;
-            tqkv.put(QD + o, first, tag_qkv);
-            tqkv.put(QD + o + kRotary, second, tag_qkv);
             kcache.st(position * KVD + o, first);
             kcache.st(position * KVD + o + kRotary, second);
           }
         } else {
           const int o = (head - NQ - NKV) * kHeadDim + i;
-          tqkv.put(QD + KVD + o, x0, tag_qkv);
-          tqkv.put(QD + KVD + o + kRotary, x1, tag_qkv);
+          out.put(slot, x0);
+          out.put(slot + kRotary, x1);
           vcache.st(position * KVD + o, x0);
           vcache.st(position * KVD + o + kRotary, x1);
         }
@@ -915,11 +1007,20 @@ struct Roles {
     };
     auto pre_regs = [](int) {};
     loop(kRoleAttn, false, [&](uint32_t t, int l, int position) {
-      const uint32_t tag_qkv = tag(seqno(t, l, 0));
-      const uint32_t tag_part = tag(seqno(t, l, 1));
       const int length = position + 1;
       const int chunks = attn_chunks(length), cl = attn_chunk_len(length);
       const int units = NKV * chunks;
+      const Slots in = s_qkv(l, t), out = s_part(l, t);
+      {
+        // This CU's records (every head of its units' KV groups).
+        const Slots next = s_part(l, t + 1);
+        for (int u = rank; u < units; u += nrole) {
+          const int g = u / chunks, c = u % chunks;
+          for (int e = threadIdx.x; e < GROUP * kRoleRecStride; e += kT)
+            next.clear(((g * GROUP + e / kRoleRecStride) * kAttnMaxChunks + c) * kRoleRecStride +
+                       e % kRoleRecStride);
+        }
+      }
       bool first_unit = true;
       for (int u = rank; u < units; u += nrole) {
         const int g = u / chunks, c = u % chunks;
@@ -930,19 +1031,20 @@ struct Roles {
           lds_barrier();
           attn_dma(l, g, begin, min(end, begin + kAttnCap), ar);
         }
-        // The group's queries, then this step's K and V rows.
-        constexpr int qpairs = GROUP * kHeadDim / 2;
-        const int pairs = qpairs + (has_new ? kHeadDim : 0);
-        if (!gather_map<1>(tqkv, pairs, tag_qkv, ar.qs, a.error, cm.flags, [&](int p, uint32_t &s, int &d) {
-              if (p < qpairs) {
-                s = (g * GROUP * kHeadDim) / 2 + p;
-                d = 2 * p;
-              } else if (p < qpairs + kHeadDim / 2) {
-                s = (QD + g * kHeadDim) / 2 + (p - qpairs);
-                d = kW * kHeadDim + 2 * (p - qpairs);
+        // The group's queries, then this step's K and V rows (float4s).
+        constexpr int q4 = GROUP * kHeadDim / 4, r4 = kHeadDim / 4;
+        const int n4 = q4 + (has_new ? 2 * r4 : 0);
+        if (!gather4<(q4 + 2 * r4 + kT - 1) / kT>(in, n4, reinterpret_cast<float4 *>(ar.qs), a.error,
+                                                  cm.flags, [&](int p, int &s, int &d) {
+              if (p < q4) {
+                s = g * q4 + p;
+                d = p;
+              } else if (p < q4 + r4) {
+                s = (QD + g * kHeadDim) / 4 + (p - q4);
+                d = kW * r4 + (p - q4);
               } else {
-                s = (QD + KVD + g * kHeadDim) / 2 + (p - qpairs - kHeadDim / 2);
-                d = kW * kHeadDim + kHeadDim + 2 * (p - qpairs - kHeadDim / 2);
+                s = (QD + KVD + g * kHeadDim) / 4 + (p - q4 - r4);
+                d = kW * r4 + r4 + (p - q4 - r4);
               }
             }))
           return false;
@@ -976,12 +1078,10 @@ struct Roles {
         }
         clock.mark(1);
         if (wv < GROUP) {
-          const uint32_t rec = ((g * GROUP + wv) * kAttnMaxChunks + c) * kPartStride;
-          tpart.put(rec + 2 + lane, acc, tag_part);
-          if (lane == 0) {
-            tpart.put(rec, m, tag_part);
-            tpart.put(rec + 1, lsum, tag_part);
-          }
+          // Record: m, l, two pad words, acc[64].
+          const uint32_t rec = ((g * GROUP + wv) * kAttnMaxChunks + c) * kRoleRecStride;
+          out.put(rec + 4 + lane, acc);
+          if (lane < 4) out.put(rec + lane, lane == 0 ? m : lane == 1 ? lsum : 0.f);
         }
         clock.mark(2);
         first_unit = false;
@@ -1015,42 +1115,73 @@ struct Roles {
     auto pre_lds = [&](int l, int) { ro.prefetch_lds(rows(l)); };
     auto pre_regs = [&](int l) { ro.prefetch_regs(rows(l)); };
     loop(kRoleO, false, [&](uint32_t t, int l, int position) {
-      const uint32_t tag_part = tag(seqno(t, l, 1));
-      const uint32_t tag_h1 = tag(seqno(t, l, 2));
       const int C = attn_chunks(position + 1);
-      // Residual rows [2 u0, 2 u0 + 2 n) of the layer input.
-      if (!layer_input(t, l, 2 * u0, 2 * ro.n, cm.vec)) return false;
-      // The partial records of every head, in passes of 4 pairs per thread
-      // (later passes find their records already published).
-      constexpr int kHalf = kPartStride / 2;
-      constexpr int kPer = 4;
-      const int pairs = NQ * C * kHalf;
-      for (int base = 0; base < pairs; base += kPer * kT) {
-        if (!gather_map<kPer>(tpart, min(kPer * kT, pairs - base), tag_part, parts, a.error, cm.flags,
-                              [&](int p, uint32_t &s, int &d) {
-                                const int rec = (base + p) / kHalf, k2 = (base + p) % kHalf;
-                                const int h = rec / C, c = rec % C;
-                                s = (h * kAttnMaxChunks + c) * kHalf + k2;
-                                d = rec * kPartStride + 2 * k2;
-                              }))
+      const Slots out = s_h1(l, t);
+      {
+        const Slots next = s_h1(l, t + 1);
+        for (int k = threadIdx.x; k < 2 * ro.n; k += kT) next.clear(2 * u0 + k);
+      }
+      // Residual rows [2 u0, 2 u0 + 2 n) of the layer input, in the float4s
+      // covering them (row r at cm.vec[r - 4 f4]).
+      const int f4 = (2 * u0) / 4, e4 = (2 * (u0 + ro.n) + 3) / 4;
+      const int roff = 2 * u0 - 4 * f4;
+      if (!layer_input(t, l, f4, e4 - f4, cm.vec)) return false;
+      // The partial records of every head (record (h, c) at (h C + c) 68 in
+      // LDS); one pass covers nine chunks per head (later passes find their
+      // records already published).
+      constexpr int kRec4 = kRoleRecStride / 4;
+      constexpr int kPer = (NQ * 9 * kRec4 + kT - 1) / kT;
+      static_assert(kPer <= 12, "partial gather pass");
+      const Slots in = s_part(l, t);
+      const int n4 = NQ * C * kRec4;
+      for (int base = 0; base < n4; base += kPer * kT) {
+        if (!gather4<kPer>(in, min(kPer * kT, n4 - base), reinterpret_cast<float4 *>(parts), a.error,
+                           cm.flags, [&](int p, int &s, int &d) {
+                             const int rec = (base + p) / kRec4, k = (base + p) % kRec4;
+                             const int h = rec / C, c = rec % C;
+                             s = (h * kAttnMaxChunks + c) * kRec4 + k;
+                             d = rec * kRec4 + k;
+                           }))
           return false;
       }
       clock.lap(2 * kRoleO);
-      for (int e = threadIdx.x; e < QD; e += kT) {
-        const int h = e / kHeadDim, d = e % kHeadDim;
-        const float *rec = parts + h * C * kPartStride;
-        cm.xn[e] = attn_merge([&](int c, int k) { return rec[c * kPartStride + k]; }, C, d);
+      // Merge, in the arithmetic of attn_merge, one wave per head: lane c
+      // holds chunk c's m and l and computes its weight w_c = e^(m_c - M)
+      // (M the head's largest m); lane d then sums w_c acc_c[d] and w_c l_c
+      // in chunk order and divides. All of a head's LDS reads are issued
+      // before the sums (chunk indices clamped to C - 1, the extra terms
+      // discarded by a select).
+      constexpr int kC = kAttnMaxChunks;
+      static_assert(kT % kHeadDim == 0 && kHeadDim == kWave && kC <= kWave, "one wave per head");
+      for (int e0 = wv * kWave; e0 < QD; e0 += kT) {
+        const float *rec = parts + (e0 / kHeadDim) * C * kRoleRecStride;
+        const int cl = min(lane, C - 1);
+        const float mc = rec[cl * kRoleRecStride];
+        const float lc = rec[cl * kRoleRecStride + 1];
+        float av[kC];
+#pragma unroll
+        for (int c = 0; c < kC; ++c) av[c] = rec[min(c, C - 1) * kRoleRecStride + 4 + lane];
+        const float mx = wave_max(lane < C ? mc : -INFINITY);
+        const float w = expf(mc - mx);
+        float num = 0.f, dsum = 0.f;
+#pragma unroll
+        for (int c = 0; c < kC; ++c) {
+          const float wc = read_lane(w, c);
+          dsum = c < C ? fmaf(wc, read_lane(lc, c), dsum) : dsum;
+          num = c < C ? fmaf(wc, av[c], num) : num;
+        }
+        cm.xn[e0 + lane] = num / dsum;
       }
       lds_barrier();
       float4 xv[PairSlots<QD>::NJ];
       load_pair_operand<QD>(Lds{cm.xn}, xv);
       clock.mark(0);
-      ro.compute(xv, [&](int k) { return make_float4(cm.vec[2 * k], cm.vec[2 * k + 1], 0.f, 0.f); },
+      ro.compute(xv,
+                 [&](int k) { return make_float4(cm.vec[roff + 2 * k], cm.vec[roff + 2 * k + 1], 0.f, 0.f); },
                  [&](int k, float sa, float sb, float4 c) {
-                   if (lane != 0) return;
                    const int u = u0 + k;
-                   th1.put(2 * u, c.x + sa, tag_h1);
-                   th1.put(2 * u + 1, c.y + sb, tag_h1);
+                   out.put(2 * u, c.x + sa);
+                   out.put(2 * u + 1, c.y + sb);
                  },
                  [&] { clock.mark(1); });
       clock.mark(2);
@@ -1084,12 +1215,15 @@ struct Roles {
     auto pre_lds = [&](int l, int) { rg.prefetch_lds(rows(l)); };
     auto pre_regs = [&](int l) { rg.prefetch_regs(rows(l)); };
     loop(kRoleGate, false, [&](uint32_t t, int l, int position) {
-      const uint32_t tag_h1 = tag(seqno(t, l, 2));
-      const uint32_t tag_act = tag(seqno(t, l, 3));
+      const Slots out = s_act(l, t);
+      {
+        const Slots next = s_act(l, t + 1);
+        for (int k = threadIdx.x; k < rg.n; k += kT) next.clear(u0 + k);
+      }
       const float4 g4 = threadIdx.x < H / 4
                             ? reinterpret_cast<const float4 *>(layer(l).mlp_norm)[threadIdx.x]
                             : make_float4(0.f, 0.f, 0.f, 0.f);
-      if (!gather<(H / 2 + kT - 1) / kT>(th1, 0, H, tag_h1, cm.vec, a.error, cm.flags)) return false;
+      if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), 0, H / 4, cm.vec, a.error, cm.flags)) return false;
       clock.lap(2 * kRoleGate);
       const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
       norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
@@ -1099,7 +1233,7 @@ struct Roles {
       clock.mark(0);
       rg.compute(xv, [](int) { return make_float4(0.f, 0.f, 0.f, 0.f); },
                  [&](int k, float gt, float up, float4) {
-                   if (lane == 0) tact.put(u0 + k, gt / (1.f + expf(-gt)) * up, tag_act);
+                   out.put(u0 + k, gt / (1.f + expf(-gt)) * up);
                  },
                  [&] { clock.mark(1); });
       clock.mark(2);
@@ -1129,18 +1263,20 @@ struct Roles {
     };
     auto pre_lds = [&](int l, int) { rd.prefetch_lds(row(l)); };
     auto pre_regs = [&](int l) { rd.prefetch_regs(row(l)); };
-    const int hb = u0 & ~1;                       // even start of the h1 rows gathered
-    const int hn = ((u0 + rd.n + 1) & ~1) - hb;   // even count covering [u0, u0 + n)
+    const int hb4 = u0 / 4;                       // float4s of h1 covering [u0, u0 + n)
+    const int hn4 = (u0 + rd.n + 3) / 4 - hb4;
     loop(kRoleDown, true, [&](uint32_t t, int l, int position) {
-      const uint32_t tag_h1 = tag(seqno(t, l, 2));
-      const uint32_t tag_act = tag(seqno(t, l, 3));
-      const uint32_t tag_hid = tag(seqno(t, l, 4));
-      if (!gather<(H / 2 + kT - 1) / kT>(th1, hb, hn, tag_h1, cm.vec, a.error, cm.flags)) return false;
-      if (!gather<(I / 2 + kT - 1) / kT>(tact, 0, I, tag_act, act, a.error, cm.flags)) return false;
+      const Slots out = s_hid(l, t);
+      {
+        const Slots next = s_hid(l, t + 1);
+        for (int k = threadIdx.x; k < rd.n; k += kT) next.clear(u0 + k);
+      }
+      if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), hb4, hn4, cm.vec, a.error, cm.flags)) return false;
+      if (!gather4c<(I / 4 + kT - 1) / kT>(s_act(l, t), 0, I / 4, act, a.error, cm.flags)) return false;
       clock.lap(2 * kRoleDown);
       clock.mark(0);
-      rd.compute(act, [&](int k) { return cm.vec[u0 + k - hb]; }, [&](int k, float s, float h1v) {
-        if (lane == 0) thid.put(u0 + k, h1v + s, tag_hid);
+      rd.compute(act, [&](int k) { return cm.vec[u0 + k - 4 * hb4]; }, [&](int k, float s, float h1v) {
+        out.put(u0 + k, h1v + s);
       }, [&] { clock.mark(1); });
       clock.mark(2);
       lds_barrier();
