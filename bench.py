@@ -46,12 +46,13 @@ PREFILL_SEED, PREFILL_DECODE = 4, 128
 WEIGHT_BYTES = 1_976_131_072
 
 
-# HBM bytes per decode token of the resident kernel, measured with rocprofv3
-# FETCH_SIZE (x2.000) + WRITE_SIZE (x1.000) on the 64-token launch of this
-# workload; the factors come from a 1 GiB device copy in the same profile
-# (profiles/resident_decode_kernel_config2.md). Re-measured when the kernel
-# changes; None where no measurement exists.
-RESIDENT_TRAFFIC_PER_TOKEN = 2_106_996_721
+# HBM bytes per decode token of the resident kernels, measured with rocprofv3
+# FETCH_SIZE + WRITE_SIZE on the 64-token launch of this workload, scaled by
+# the factors a 1 GiB device copy gives in the same profile
+# (profiles/roles_kernel_config2.md, profiles/resident_decode_kernel_config2.md).
+# Re-measured when a kernel changes; None where no measurement exists.
+RESIDENT_TRAFFIC_PER_TOKEN = 2_038_815_312
+RESIDENT_TRAFFIC_PER_TOKEN_TAGGED = 2_106_996_721
 
 
 def step_bytes(length: int) -> int:
@@ -177,8 +178,13 @@ def run_decode(K, W, no_cpu):
     if grid:
         # One resident launch runs all K tokens: its HIP-event duration on the
         # engine stream is the kernel time, its algorithmic bytes the K steps'.
-        traffic = RESIDENT_TRAFFIC_PER_TOKEN * K if RESIDENT_TRAFFIC_PER_TOKEN else None
-        roof = roofline_hbm("resident_decode_kernel", timing.total_us, float(total_bytes), traffic)
+        # The role-split kernel runs unless QD_RESIDENT_KERNEL=tagged selects
+        # the tagged-dataflow kernel.
+        tagged = os.environ.get("QD_RESIDENT_KERNEL") == "tagged"
+        per_token = RESIDENT_TRAFFIC_PER_TOKEN_TAGGED if tagged else RESIDENT_TRAFFIC_PER_TOKEN
+        traffic = per_token * K if per_token else None
+        roof = roofline_hbm("resident_decode_kernel" if tagged else "roles_kernel", timing.total_us,
+                            float(total_bytes), traffic)
     else:
         eng.kv_reset(0, PROMPT)
         prof = eng.profile_kernels(0, first, min(K, 16))

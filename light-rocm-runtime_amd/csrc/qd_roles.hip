@@ -27,15 +27,16 @@
 // streams the other roles' shares. Sizing gives every role CU about the same
 // bytes per layer, so all CUs stream at the same rate.
 //
-// Hand-offs are tagged vectors: each value is an 8-byte (value, tag) pair
-// written with one device-scope (sc1) 64-bit store; the tag names the launch
-// epoch and the producing (token, layer, stage). Consumers poll until every
-// pair they need carries the expected tag. Reuse safety: a vector is
-// rewritten only by a producer whose inputs transitively required every
-// consumer of the previous version to have read it (each consumer reads
-// before it publishes, and every role's output is needed downstream); the
-// argmax partials are double-buffered by token parity because a CU with no
-// unit in a layer contributes nothing to the next token's chain.
+// Hand-offs go through plain FP32 slots, one block per (layer, token
+// parity), which hold kSlotEmpty (all bits set) until written: a consumer
+// polls 16-byte device-scope (sc1) loads until no word of each float4 it
+// needs is empty. The writers of token t clear their slots in the other
+// parity's block (token t + 1's). That block held token t - 1's values, and
+// every CU finished token t - 1 before any CU started token t, because each
+// waits for token t - 1's argmax, which needs every CU's LM-head partial.
+// The host fills every slot with kSlotEmpty before a launch. The argmax
+// partials are (value, tag) pairs, double-buffered by token parity (the tag
+// names the launch epoch and the token).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
