@@ -112,6 +112,10 @@ struct Coherent {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r,
                                           i * 4u, 0, kPolicySc1);
   }
+  __device__ __forceinline__ void st4(uint32_t i4, float4 v) const {
+    const f32x4 x = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, i4 * 16u, 0, kPolicySc1);
+  }
   __device__ __forceinline__ void stu(uint32_t i, uint32_t v) const {
     __builtin_amdgcn_raw_buffer_store_b32(v, r, i * 4u, 0, kPolicySc1);
   }

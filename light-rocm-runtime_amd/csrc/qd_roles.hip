@@ -42,6 +42,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 
 #include "qd_attention.hpp"
 #include "qd_device.hpp"
@@ -77,7 +78,14 @@ __device__ __forceinline__ int wave_u() { return __builtin_amdgcn_readfirstlane(
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
-__device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// vm_wait is the s_waitcnt builtin (vmcnt 0; expcnt and lgkmcnt at their
+// no-wait maxima), not inline asm: the compiler's wait insertion sees it, so
+// after it no LDS access is guarded against a DMA already waited for.
+constexpr unsigned kWaitVmcnt0 = 0x0F70u;
+__device__ __forceinline__ void vm_wait() {
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  asm volatile("" ::: "memory");
+}
 // Whole-workgroup AND (flags: one LDS word per wave). The ballot is taken
 // with the whole wave active, then lane 0 records it.
 __device__ __forceinline__ bool block_all(bool v, uint32_t *flags) {
@@ -116,6 +124,15 @@ struct TagVec {
   }
 };
 
+// Float4 i of a small global vector (norm gains, an embedding row) through
+// the global address space: a flat load would count against lgkmcnt too,
+// and while one is pending the compiler waits for every vector memory
+// operation (vmcnt(0)) wherever it waits for any.
+__device__ __forceinline__ float4 ld_global4(const float *p, int i) {
+  const gf32x4 v = ((global_f32x4 *)p)[i];
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
 struct Lds {
   const float *p;
   __device__ float ld(uint32_t i) const { return p[i]; }
@@ -147,7 +164,8 @@ struct Common {
   float bv[kW];
   uint32_t bi[kW];
   uint32_t flags[kW];                   // block_all
-  float top[2 * kMaxRoleGrid];          // argmax partials (value, index bits)
+  float top[2 * kMaxRoleGrid];          // argmax partials (value, index bits); in the
+                                        //   layers, a role's outputs staged for their stores
   ClockLds clock;                       // profiling (profiled variant only)
 };
 // The kernel's one LDS block, at namespace scope so the per-role functions
@@ -223,6 +241,16 @@ struct Slots {
   __device__ void clear(uint32_t i) const {
     __builtin_amdgcn_raw_buffer_store_b32(kSlotEmpty, r, i * 4u, 0, kPolicySc1);
   }
+  __device__ void put4(uint32_t i4, float4 v) const {
+    const f32x4 x = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, i4 * 16u, 0, kPolicySc1);
+  }
+  __device__ void clear4(uint32_t i4) const {
+    const u32x4 x = {kSlotEmpty, kSlotEmpty, kSlotEmpty, kSlotEmpty};
+    __builtin_amdgcn_raw_buffer_store_b128(x, r, i4 * 16u, 0, kPolicySc1);
+  }
+  __device__ void st(uint32_t i, float v) const { put(i, v); }
+  __device__ void st4(uint32_t i4, float4 v) const { put4(i4, v); }
   __device__ u32x4 get4(uint32_t i4) const {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, i4 * 16u, 0, kPolicySc1));
   }
@@ -275,6 +303,31 @@ __device__ bool gather4(const Slots &src, int n4, float4 *dst, uint32_t *error, 
   }
 }
 
+// Light pre-poll: wave 0 waits until 8 float4s spread over [first4,
+// first4 + n4) are written (their producers are spread over the range), so
+// the full gather that follows does not re-read the whole range while
+// nothing has arrived. Returns false when the wait gave up.
+__device__ inline bool hint_wait(const Slots &src, int first4, int n4, uint32_t *error, uint32_t *flags) {
+  if (wave_u() == 0) {
+    const int lane = lane_id();
+    const int q = first4 + (lane < 8 ? (lane * n4) / 8 + n4 / 16 : 0);
+    for (uint32_t spin = 0;; ++spin) {
+      bool ok = true;
+      if (lane < 8) {
+        const Quad g = __builtin_bit_cast(Quad, src.get4(q));
+        ok = g.w[0] != kSlotEmpty && g.w[1] != kSlotEmpty && g.w[2] != kSlotEmpty && g.w[3] != kSlotEmpty;
+      }
+      vm_wait();
+      if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+      if (spin > kSpinLimit) {
+        if (lane == 0) atomicOr(error, 1u);
+        break;
+      }
+    }
+  }
+  return block_all(true, flags);
+}
+
 // Contiguous float4s [first4, first4 + n4) of a slot block -> dst[0, n4).
 template <int kMaxPer>
 __device__ bool gather4c(const Slots &src, int first4, int n4, float *dst, uint32_t *error,
@@ -284,6 +337,60 @@ __device__ bool gather4c(const Slots &src, int first4, int n4, float *dst, uint3
                             s = first4 + p;
                             d = p;
                           });
+}
+
+// Publishing a role's outputs. A role CU's outputs are fixed runs of slot
+// elements; each thread owns at most one float4 of them (OutMap, computed
+// once per launch): its float4 index q in the destination, which of its
+// four elements belong to this CU (the float4s at the ends of a run are
+// shared with neighbouring workgroups) and where the values sit in the LDS
+// stage. A whole float4 goes out with one 16-byte store, a shared one
+// element by element. Memory then sees whole-line writes rather than
+// scattered words (scattered 4-byte writes from the lanes slowed a hand-off
+// by 0.5-1.3 us). The thread reads its float4 from LDS before it stores:
+// the compiler makes an LDS read wait for every earlier store (vmcnt
+// counts stores and guards the DMA).
+struct OutMap {
+  int q = -1;         // float4 index in the destination, -1: none
+  int soff = 0;       // float4 index in the stage
+  uint32_t mask = 0;  // elements of float4 q this CU owns
+  int tag = 0;        // caller's label for the run
+  // Float4 `item` of the run [first, first + n) (stage[j] holding element
+  // sbase + j, sbase a multiple of 4); returns the run's float4 count.
+  __device__ int take(int first, int n, int sbase, int item, int run_tag) {
+    const int q0 = first >> 2, cnt = ((first + n + 3) >> 2) - q0;
+    if (item >= 0 && item < cnt) {
+      q = q0 + item;
+      soff = (4 * q - sbase) >> 2;
+      mask = 0;
+      for (int k = 0; k < 4; ++k)
+        if (4 * q + k >= first && 4 * q + k < first + n) mask |= 1u << k;
+      tag = run_tag;
+    }
+    return cnt;
+  }
+};
+// Stores v (this thread's float4 of a run) to dst at float4 q + off4.
+template <typename Dst>
+__device__ __forceinline__ void put_quad(const Dst &dst, const OutMap &m, float4 v, int off4 = 0) {
+  if (m.mask == 0xFu) {
+    dst.st4(static_cast<uint32_t>(m.q + off4), v);
+  } else {
+    const float x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if ((m.mask >> k) & 1u) dst.st(static_cast<uint32_t>(4 * (m.q + off4) + k), x[k]);
+  }
+}
+// Sets this thread's elements of a run of slots to kSlotEmpty.
+__device__ __forceinline__ void clear_quad(const Slots &dst, const OutMap &m) {
+  if (m.mask == 0xFu) {
+    dst.clear4(static_cast<uint32_t>(m.q));
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if ((m.mask >> k) & 1u) dst.clear(static_cast<uint32_t>(4 * m.q + k));
+  }
 }
 
 // Profiling clock kept by thread 0 (profiled variant only). Totals and the
@@ -702,7 +809,8 @@ struct Roles {
       if (!argmax(t)) return;
       if (traced) clock.flush_trace(a.trace, a.layers, role);
       generated = t + 1;
-      if (blockIdx.x == 0 && threadIdx.x == 0) a.out_tokens[t] = token;
+      if (blockIdx.x == 0 && threadIdx.x == 0)
+        *(__attribute__((address_space(1))) uint32_t *)(a.out_tokens + t) = token;
       if (token == UINT32_MAX) break;  // every logit NaN
       if (token == a.eos) {
         stop_reason = 2u;
@@ -743,7 +851,7 @@ struct Roles {
       }
     };
     float4 w0[NJ], w1[NJ], w2[NJ];
-    const float4 g4 = threadIdx.x < H / 4 ? reinterpret_cast<const float4 *>(a.final_norm)[threadIdx.x]
+    const float4 g4 = threadIdx.x < H / 4 ? ld_global4(a.final_norm, threadIdx.x)
                                          : make_float4(0.f, 0.f, 0.f, 0.f);
     load(gw, w0);
     __builtin_amdgcn_sched_barrier(0);
@@ -860,8 +968,8 @@ struct Roles {
   // layer's output, or this token's embedding row at l = 0) -> dst.
   __device__ bool layer_input(uint32_t t, int l, int first4, int n4, float *dst) {
     if (l == 0) {
-      const float4 *e = reinterpret_cast<const float4 *>(a.embed + static_cast<size_t>(token) * H) + first4;
-      for (int c = threadIdx.x; c < n4; c += kT) reinterpret_cast<float4 *>(dst)[c] = e[c];
+      const float *e = a.embed + static_cast<size_t>(token) * H;
+      for (int c = threadIdx.x; c < n4; c += kT) reinterpret_cast<float4 *>(dst)[c] = ld_global4(e, first4 + c);
       vm_wait();
       lds_barrier();
       return true;
@@ -904,20 +1012,26 @@ struct Roles {
       dma16<kPolicyNt>(lane < R4 ? c4 + lane : (lane < 2 * R4 ? s4 + (lane - R4) : c4), q_cs);
     };
     auto pre_regs = [&](int l) { rq.prefetch_regs(rows(l)); };
+    // Unit u's rows land at (u / 32) * 64 + u % 32 and 32 further on
+    // (packed head u / 32: the query heads, then the K and V heads), so this
+    // CU's slots are two runs per packed head it touches; thread i owns
+    // float4 i of those runs taken in order (tagged with the packed head).
+    const int sbase = (u0 / kRotary) * kHeadDim;
+    OutMap om;
+    {
+      int item = threadIdx.x;
+      for (int h = u0 / kRotary; h <= (u0 + rq.n - 1) / kRotary; ++h) {
+        const int ib = max(u0, h * kRotary) - h * kRotary;
+        const int ie = min(u0 + rq.n, (h + 1) * kRotary) - h * kRotary;
+        item -= om.take(h * kHeadDim + ib, ie - ib, sbase, item, h);
+        item -= om.take(h * kHeadDim + kRotary + ib, ie - ib, sbase, item, h);
+      }
+    }
     loop(kRoleQkv, false, [&](uint32_t t, int l, int position) {
       const LayerPtrs lw = layer(l);
       const Slots out = s_qkv(l, t);
-      {
-        // Unit u's rows land at (u / 32) * 64 + u % 32 and 32 further on:
-        // packed head u / 32 is a query head, then the K and V heads.
-        const Slots next = s_qkv(l, t + 1);
-        for (int k = threadIdx.x; k < rq.n; k += kT) {
-          const int u = u0 + k;
-          next.clear((u / kRotary) * kHeadDim + u % kRotary);
-          next.clear((u / kRotary) * kHeadDim + u % kRotary + kRotary);
-        }
-      }
-      const float4 g4 = threadIdx.x < H / 4 ? reinterpret_cast<const float4 *>(lw.attn_norm)[threadIdx.x]
+      if (om.q >= 0) clear_quad(s_qkv(l, t + 1), om);
+      const float4 g4 = threadIdx.x < H / 4 ? ld_global4(lw.attn_norm, threadIdx.x)
                                            : make_float4(0.f, 0.f, 0.f, 0.f);
       if (!layer_input(t, l, 0, H / 4, cm.vec)) return false;
       clock.lap(2 * kRoleQkv);
@@ -931,35 +1045,38 @@ struct Roles {
       const float *cs = reinterpret_cast<const float *>(q_cs);
       const Coherent kcache(kv_layer(a.k_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
       const Coherent vcache(kv_layer(a.v_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
+      float *stage = cm.top;
       rq.compute(xv, [&](int k) {
         const int u = u0 + k;
         const int ra = (u / kRotary) * kHeadDim + u % kRotary;
         return make_float4(bias[ra], bias[ra + kRotary], cs[u % kRotary], cs[kRotary + u % kRotary]);
       }, [&](int k, float sa, float sb, float4 c) {
         const int u = u0 + k;
-        const int head = u / kRotary, i = u % kRotary;
-        const int slot = head * kHeadDim + i;
+        const int head = u / kRotary;
+        const int slot = head * kHeadDim + u % kRotary - sbase;
         const float x0 = sa + c.x;
         const float x1 = sb + c.y;
         if (head < NQ + NKV) {
           const float cv = c.z, sv = c.w;
-          const float first = x0 * cv - x1 * sv;
-          const float second = x1 * cv + x0 * sv;
-          out.put(slot, first);
-          out.put(slot + kRotary, second);
-          if (head >= NQ) {
-            const int o = (head - NQ) * kHeadDim + i;
-            kcache.st(position * KVD + o, first);
-            kcache.st(position * KVD + o + kRotary, second);
-          }
+          stage[slot] = x0 * cv - x1 * sv;
+          stage[slot + kRotary] = x1 * cv + x0 * sv;
         } else {
-          const int o = (head - NQ - NKV) * kHeadDim + i;
-          out.put(slot, x0);
-          out.put(slot + kRotary, x1);
-          vcache.st(position * KVD + o, x0);
-          vcache.st(position * KVD + o + kRotary, x1);
+          stage[slot] = x0;
+          stage[slot + kRotary] = x1;
         }
       }, [&] { clock.mark(1); });
+      lds_barrier();
+      if (om.q >= 0) {
+        // The slots and, for a K or V head, the cache row (slot e of K head
+        // g is cache element position * KVD + e - QD, of V head g
+        // position * KVD + e - QD - KVD).
+        const float4 v = reinterpret_cast<const float4 *>(stage)[om.soff];
+        put_quad(out, om, v);
+        if (om.tag >= NQ + NKV)
+          put_quad(vcache, om, v, (position * KVD - QD - KVD) / 4);
+        else if (om.tag >= NQ)
+          put_quad(kcache, om, v, (position * KVD - QD) / 4);
+      }
       clock.mark(2);
       lds_barrier();  // LDS units, biases and cos|sin are rewritten next
       clock.lap(2 * kRoleQkv + 1);
@@ -1012,14 +1129,16 @@ struct Roles {
       const int chunks = attn_chunks(length), cl = attn_chunk_len(length);
       const int units = NKV * chunks;
       const Slots in = s_qkv(l, t), out = s_part(l, t);
+      // Record (h, c) is kRoleRecStride floats at (h * kAttnMaxChunks + c) *
+      // kRoleRecStride: whole float4s.
+      constexpr int kRec4 = kRoleRecStride / 4;
       {
         // This CU's records (every head of its units' KV groups).
         const Slots next = s_part(l, t + 1);
         for (int u = rank; u < units; u += nrole) {
           const int g = u / chunks, c = u % chunks;
-          for (int e = threadIdx.x; e < GROUP * kRoleRecStride; e += kT)
-            next.clear(((g * GROUP + e / kRoleRecStride) * kAttnMaxChunks + c) * kRoleRecStride +
-                       e % kRoleRecStride);
+          for (int e = threadIdx.x; e < GROUP * kRec4; e += kT)
+            next.clear4(((g * GROUP + e / kRec4) * kAttnMaxChunks + c) * kRec4 + e % kRec4);
         }
       }
       bool first_unit = true;
@@ -1078,11 +1197,18 @@ struct Roles {
           }
         }
         clock.mark(1);
+        // Record: m, l, two pad words, acc[64]; staged, then stored as
+        // whole float4s.
+        float *stage = cm.top;
         if (wv < GROUP) {
-          // Record: m, l, two pad words, acc[64].
-          const uint32_t rec = ((g * GROUP + wv) * kAttnMaxChunks + c) * kRoleRecStride;
-          out.put(rec + 4 + lane, acc);
-          if (lane < 4) out.put(rec + lane, lane == 0 ? m : lane == 1 ? lsum : 0.f);
+          stage[wv * kRoleRecStride + 4 + lane] = acc;
+          if (lane < 4) stage[wv * kRoleRecStride + lane] = lane == 0 ? m : lane == 1 ? lsum : 0.f;
+        }
+        lds_barrier();
+        if (threadIdx.x < GROUP * kRec4) {
+          const int j = threadIdx.x / kRec4, q = threadIdx.x % kRec4;
+          out.put4(((g * GROUP + j) * kAttnMaxChunks + c) * kRec4 + q,
+                   reinterpret_cast<const float4 *>(stage)[j * kRec4 + q]);
         }
         clock.mark(2);
         first_unit = false;
@@ -1105,7 +1231,13 @@ struct Roles {
     ro.n = split_begin(Sh::OUnits, nrole, rank + 1) - u0;
     ro.units = reinterpret_cast<float4 *>(region);
     if (!fits(ro.n, ro.capacity())) return;
+    // Partial records in LDS as in the slot block: record (h, c) at
+    // (h * kAttnMaxChunks + c) * kRoleRecStride. Chunk c is written only
+    // once the context has c + 1 chunks, which stays so for the rest of the
+    // launch; the zero fill here keeps the records of chunks not yet in
+    // play finite for the merge's unconditional reads.
     float *parts = reinterpret_cast<float *>(region + Sh::LO * Sh::UnitBytes);
+    for (int i = threadIdx.x; i < Sh::PartFloats; i += kT) parts[i] = 0.f;
     auto rows = [&](int l) {
       const float *base = layer(l).wo;
       return [=](int k, const float *&ra, const float *&rb) {
@@ -1115,21 +1247,19 @@ struct Roles {
     };
     auto pre_lds = [&](int l, int) { ro.prefetch_lds(rows(l)); };
     auto pre_regs = [&](int l) { ro.prefetch_regs(rows(l)); };
+    OutMap om;  // rows [2 u0, 2 u0 + 2 n), staged from element 2 u0 rounded down to 4
+    om.take(2 * u0, 2 * ro.n, (2 * u0) & ~3, threadIdx.x, 0);
     loop(kRoleO, false, [&](uint32_t t, int l, int position) {
       const int C = attn_chunks(position + 1);
       const Slots out = s_h1(l, t);
-      {
-        const Slots next = s_h1(l, t + 1);
-        for (int k = threadIdx.x; k < 2 * ro.n; k += kT) next.clear(2 * u0 + k);
-      }
+      if (om.q >= 0) clear_quad(s_h1(l, t + 1), om);
       // Residual rows [2 u0, 2 u0 + 2 n) of the layer input, in the float4s
       // covering them (row r at cm.vec[r - 4 f4]).
       const int f4 = (2 * u0) / 4, e4 = (2 * (u0 + ro.n) + 3) / 4;
       const int roff = 2 * u0 - 4 * f4;
       if (!layer_input(t, l, f4, e4 - f4, cm.vec)) return false;
-      // The partial records of every head (record (h, c) at (h C + c) 68 in
-      // LDS); one pass covers nine chunks per head (later passes find their
-      // records already published).
+      // The partial records of every head's C chunks; one pass covers nine
+      // chunks per head (later passes find their records already published).
       constexpr int kRec4 = kRoleRecStride / 4;
       constexpr int kPer = (NQ * 9 * kRec4 + kT - 1) / kT;
       static_assert(kPer <= 12, "partial gather pass");
@@ -1141,50 +1271,87 @@ struct Roles {
                              const int rec = (base + p) / kRec4, k = (base + p) % kRec4;
                              const int h = rec / C, c = rec % C;
                              s = (h * kAttnMaxChunks + c) * kRec4 + k;
-                             d = rec * kRec4 + k;
+                             d = s;
                            }))
           return false;
       }
       clock.lap(2 * kRoleO);
       // Merge, in the arithmetic of attn_merge, one wave per head: lane c
       // holds chunk c's m and l and computes its weight w_c = e^(m_c - M)
-      // (M the head's largest m); lane d then sums w_c acc_c[d] and w_c l_c
-      // in chunk order and divides. All of a head's LDS reads are issued
-      // before the sums (chunk indices clamped to C - 1, the extra terms
-      // discarded by a select).
-      constexpr int kC = kAttnMaxChunks;
-      static_assert(kT % kHeadDim == 0 && kHeadDim == kWave && kC <= kWave, "one wave per head");
-      for (int e0 = wv * kWave; e0 < QD; e0 += kT) {
-        const float *rec = parts + (e0 / kHeadDim) * C * kRoleRecStride;
-        const int cl = min(lane, C - 1);
-        const float mc = rec[cl * kRoleRecStride];
-        const float lc = rec[cl * kRoleRecStride + 1];
-        float av[kC];
+      // (M the head's largest m); the weights and l's go through a small
+      // per-wave LDS area (one wave's LDS accesses run in order) and lane d
+      // sums w_c acc_c[d] and w_c l_c in chunk order, then divides. A
+      // wave's two heads are computed side by side so their latency chains
+      // overlap. The code is specialised on C rounded up to 4 (kCm chunks,
+      // the extra terms discarded by a select); every read is an immediate
+      // offset from the head's record base.
+      static_assert(kT % kHeadDim == 0 && kHeadDim == kWave && kAttnMaxChunks <= kWave &&
+                        kAttnMaxChunks % 4 == 0,
+                    "one wave per head");
+      constexpr int kHeadsPerWave = (NQ + kW - 1) / kW;
+      constexpr int kWl = 2 * kAttnMaxChunks;  // per head: w[16], l[16]
+      float *wl = cm.top + wv * kWl * kHeadsPerWave;
+      auto merge = [&](auto cm_tag) {
+        constexpr int kCm = decltype(cm_tag)::value;
+        float mc[kHeadsPerWave], lc[kHeadsPerWave], av[kHeadsPerWave][kCm];
 #pragma unroll
-        for (int c = 0; c < kC; ++c) av[c] = rec[min(c, C - 1) * kRoleRecStride + 4 + lane];
-        const float mx = wave_max(lane < C ? mc : -INFINITY);
-        const float w = expf(mc - mx);
-        float num = 0.f, dsum = 0.f;
+        for (int j = 0; j < kHeadsPerWave; ++j) {
+          const int h = min(wv + j * kW, NQ - 1);
+          const float *rec = parts + h * kAttnMaxChunks * kRoleRecStride;
+          mc[j] = rec[min(lane, kAttnMaxChunks - 1) * kRoleRecStride];
+          lc[j] = rec[min(lane, kAttnMaxChunks - 1) * kRoleRecStride + 1];
 #pragma unroll
-        for (int c = 0; c < kC; ++c) {
-          const float wc = read_lane(w, c);
-          dsum = c < C ? fmaf(wc, read_lane(lc, c), dsum) : dsum;
-          num = c < C ? fmaf(wc, av[c], num) : num;
+          for (int c = 0; c < kCm; ++c) av[j][c] = rec[c * kRoleRecStride + 4 + lane];
         }
-        cm.xn[e0 + lane] = num / dsum;
+#pragma unroll
+        for (int j = 0; j < kHeadsPerWave; ++j) {
+          const float mx = wave_max(lane < C ? mc[j] : -INFINITY);
+          const float w = expf(mc[j] - mx);
+          if (lane < kAttnMaxChunks) {
+            wl[j * kWl + lane] = w;
+            wl[j * kWl + kAttnMaxChunks + lane] = lc[j];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < kHeadsPerWave; ++j) {
+          const int h = wv + j * kW;
+          const float4 *w4 = reinterpret_cast<const float4 *>(wl + j * kWl);
+          float wv4[kCm], lv4[kCm];
+#pragma unroll
+          for (int c4 = 0; c4 < kCm / 4; ++c4) {
+            const float4 x = w4[c4], y = w4[kAttnMaxChunks / 4 + c4];
+            wv4[4 * c4] = x.x; wv4[4 * c4 + 1] = x.y; wv4[4 * c4 + 2] = x.z; wv4[4 * c4 + 3] = x.w;
+            lv4[4 * c4] = y.x; lv4[4 * c4 + 1] = y.y; lv4[4 * c4 + 2] = y.z; lv4[4 * c4 + 3] = y.w;
+          }
+          float num = 0.f, dsum = 0.f;
+#pragma unroll
+          for (int c = 0; c < kCm; ++c) {
+            dsum = c < C ? fmaf(wv4[c], lv4[c], dsum) : dsum;
+            num = c < C ? fmaf(wv4[c], av[j][c], num) : num;
+          }
+          if (h < NQ) cm.xn[h * kHeadDim + lane] = num / dsum;
+        }
+      };
+      switch ((C + 3) / 4) {
+        case 1: merge(std::integral_constant<int, 4>{}); break;
+        case 2: merge(std::integral_constant<int, 8>{}); break;
+        case 3: merge(std::integral_constant<int, 12>{}); break;
+        default: merge(std::integral_constant<int, 16>{}); break;
       }
       lds_barrier();
       float4 xv[PairSlots<QD>::NJ];
       load_pair_operand<QD>(Lds{cm.xn}, xv);
+      float *stage = cm.top;  // row 2 u0 + j at stage[j + roff]
       clock.mark(0);
       ro.compute(xv,
                  [&](int k) { return make_float4(cm.vec[roff + 2 * k], cm.vec[roff + 2 * k + 1], 0.f, 0.f); },
                  [&](int k, float sa, float sb, float4 c) {
-                   const int u = u0 + k;
-                   out.put(2 * u, c.x + sa);
-                   out.put(2 * u + 1, c.y + sb);
+                   stage[2 * k + roff] = c.x + sa;
+                   stage[2 * k + 1 + roff] = c.y + sb;
                  },
                  [&] { clock.mark(1); });
+      lds_barrier();
+      if (om.q >= 0) put_quad(out, om, reinterpret_cast<const float4 *>(stage)[om.soff]);
       clock.mark(2);
       lds_barrier();
       clock.lap(2 * kRoleO + 1);
@@ -1215,14 +1382,14 @@ struct Roles {
     };
     auto pre_lds = [&](int l, int) { rg.prefetch_lds(rows(l)); };
     auto pre_regs = [&](int l) { rg.prefetch_regs(rows(l)); };
+    OutMap om;  // units [u0, u0 + n), staged from u0 rounded down to 4
+    om.take(u0, rg.n, u0 & ~3, threadIdx.x, 0);
     loop(kRoleGate, false, [&](uint32_t t, int l, int position) {
       const Slots out = s_act(l, t);
-      {
-        const Slots next = s_act(l, t + 1);
-        for (int k = threadIdx.x; k < rg.n; k += kT) next.clear(u0 + k);
-      }
+      if (om.q >= 0) clear_quad(s_act(l, t + 1), om);
+      float *stage = cm.top;  // unit u0 + k at stage[k + (u0 & 3)]
       const float4 g4 = threadIdx.x < H / 4
-                            ? reinterpret_cast<const float4 *>(layer(l).mlp_norm)[threadIdx.x]
+                            ? ld_global4(layer(l).mlp_norm, threadIdx.x)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
       if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), 0, H / 4, cm.vec, a.error, cm.flags)) return false;
       clock.lap(2 * kRoleGate);
@@ -1234,9 +1401,11 @@ struct Roles {
       clock.mark(0);
       rg.compute(xv, [](int) { return make_float4(0.f, 0.f, 0.f, 0.f); },
                  [&](int k, float gt, float up, float4) {
-                   out.put(u0 + k, gt / (1.f + expf(-gt)) * up);
+                   stage[k + (u0 & 3)] = gt / (1.f + expf(-gt)) * up;
                  },
                  [&] { clock.mark(1); });
+      lds_barrier();
+      if (om.q >= 0) put_quad(out, om, reinterpret_cast<const float4 *>(stage)[om.soff]);
       clock.mark(2);
       lds_barrier();
       clock.lap(2 * kRoleGate + 1);
@@ -1264,21 +1433,24 @@ struct Roles {
     };
     auto pre_lds = [&](int l, int) { rd.prefetch_lds(row(l)); };
     auto pre_regs = [&](int l) { rd.prefetch_regs(row(l)); };
+    OutMap om;  // rows [u0, u0 + n), staged from u0 rounded down to 4
+    om.take(u0, rd.n, u0 & ~3, threadIdx.x, 0);
     const int hb4 = u0 / 4;                       // float4s of h1 covering [u0, u0 + n)
     const int hn4 = (u0 + rd.n + 3) / 4 - hb4;
     loop(kRoleDown, true, [&](uint32_t t, int l, int position) {
       const Slots out = s_hid(l, t);
-      {
-        const Slots next = s_hid(l, t + 1);
-        for (int k = threadIdx.x; k < rd.n; k += kT) next.clear(u0 + k);
-      }
+      if (om.q >= 0) clear_quad(s_hid(l, t + 1), om);
+      float *stage = cm.top;  // row u0 + k at stage[k + (u0 & 3)]
       if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), hb4, hn4, cm.vec, a.error, cm.flags)) return false;
+      hint_wait(s_act(l, t), 0, I / 4, a.error, cm.flags);  // EXPERIMENT
       if (!gather4c<(I / 4 + kT - 1) / kT>(s_act(l, t), 0, I / 4, act, a.error, cm.flags)) return false;
       clock.lap(2 * kRoleDown);
       clock.mark(0);
       rd.compute(act, [&](int k) { return cm.vec[u0 + k - 4 * hb4]; }, [&](int k, float s, float h1v) {
-        out.put(u0 + k, h1v + s);
+        stage[k + (u0 & 3)] = h1v + s;
       }, [&] { clock.mark(1); });
+      lds_barrier();
+      if (om.q >= 0) put_quad(out, om, reinterpret_cast<const float4 *>(stage)[om.soff]);
       clock.mark(2);
       lds_barrier();
       clock.lap(2 * kRoleDown + 1);
