@@ -392,5 +392,36 @@ __device__ __forceinline__ float dot_row(const float *a,
   return row_dot<K>(w, xv);
 }
 
+// The down projection's row dot, in column slices. Slice s of a row's NJ
+// float4 slots is [row_slice_begin(NJ, s), row_slice_begin(NJ, s + 1)); a
+// slice's products are summed per lane in slot order from zero, each lane's
+// kRowSlices slice sums combine as a fixed tree, and the lanes' results are
+// reduced over the wave (wave_sum). The resident role kernel gives each
+// slice to its own wave (each waits only for its slice of the activation)
+// and combines the lanes' slice sums through LDS; the stream kernel walks
+// the slices in one wave, so both produce the same bits.
+constexpr int kRowSlices = 8;
+__host__ __device__ constexpr int row_slice_begin(int nj, int s) { return nj * s / kRowSlices; }
+__device__ __forceinline__ float combine_slices(const float (&p)[kRowSlices]) {
+  return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+}
+template <int K>
+__device__ __forceinline__ float dot_row_sliced(const float *a,
+                                                const float4 (&xv)[RowSlots<K>::NJ]) {
+  constexpr int NJ = RowSlots<K>::NJ;
+  static_assert(kRowSlices == 8, "combine_slices");
+  float4 w[NJ];
+  load_row_weights<K>(a, w);
+  float p[kRowSlices];
+#pragma unroll
+  for (int s = 0; s < kRowSlices; ++s) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = row_slice_begin(NJ, s); j < row_slice_begin(NJ, s + 1); ++j) acc = fma4(w[j], xv[j], acc);
+    p[s] = acc;
+  }
+  return wave_sum(combine_slices(p));
+}
+
 }  // namespace dev
 }  // namespace qd

@@ -196,7 +196,8 @@ __global__ __launch_bounds__(kBlock) void gateup_silu_kernel(
   }
 }
 
-// hidden[r] += Wd[r,:] . act; one row per wave.
+// hidden[r] += Wd[r,:] . act; one row per wave, summed in the column slices
+// of dot_row_sliced (the resident role kernel's arithmetic).
 template <int H, int I>
 __global__ __launch_bounds__(kBlock) void down_residual_kernel(
     const float *__restrict__ act, const float *__restrict__ wd,
@@ -206,7 +207,7 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(
   load_row_operand<I>(Plain(act), xv);
   for (int r = blockIdx.x * kWavesPerBlock + wave_id(); r < H;
        r += gridDim.x * kWavesPerBlock) {
-    const float s = dot_row<I>(wd + static_cast<size_t>(r) * I, xv);
+    const float s = dot_row_sliced<I>(wd + static_cast<size_t>(r) * I, xv);
     if (lane_id() == 0) hidden[r] += s;
   }
 }

@@ -62,7 +62,7 @@ constexpr int kLdsBytes = 160 * 1024 - 512;
 constexpr int kAttnCap = 256;     // positions of an attention window staged in LDS
 
 // Register slots per wave: row-pair units of the K=H roles, rows of DOWN.
-constexpr int kSlotsQ = 2, kSlotsO = 2, kSlotsG = 2, kSlotsD = 1;
+constexpr int kSlotsQ = 2, kSlotsO = 2, kSlotsG = 2;
 
 // Wave index as a wave-uniform (scalar) value: unit indices, slot branches
 // and row addresses derived from it stay in SGPRs.
@@ -561,80 +561,100 @@ struct PairRole {
   static constexpr int capacity() { return kW * S + Lcap; }
 };
 
-// ---- K=I rows (down) -------------------------------------------------------
-template <int I, int S, int Lcap>
-struct RowRole {
+// ---- K=I rows, column slices (down) -----------------------------------------
+// A CU owns rows [u0, u0 + n). Wave w owns column slice w of every row
+// (slots [c0, c0 + ns) of the row's NJ float4 slots, dot_row_sliced's
+// slices): rows [0, kRegF4 / ns) of its slice sit in register slots, the
+// rest in the wave's own LDS area. Each wave waits for its own slice of the
+// activation (straight into registers) and leaves every row's per-lane
+// slice sums in LDS; wave w then finishes rows w, w + 8, ... (per lane
+// combine_slices over the waves' sums, then wave_sum: dot_row_sliced's
+// order). Registers are indexed with the slice width as a template constant.
+template <int I>
+struct DownRole {
   static constexpr int NJ = RowSlots<I>::NJ;
-  static constexpr int RowF4 = NJ * kWave;
-  float4 wv[S][NJ];
-  float4 *rowsl = nullptr;
-  int n = 0;
+  static constexpr int kNsLo = NJ / kRowSlices, kNsHi = (NJ + kRowSlices - 1) / kRowSlices;
+  // Weight float4s per lane held in registers (a wider budget for the
+  // wide slices made the compiler keep the array in scratch).
+  __host__ __device__ static constexpr int reg_f4(int) { return kRegF4; }
+  static constexpr int kRegF4 = 18;
+  static constexpr int kMaxRows = 16;
+  static_assert(kRowSlices == kW && kNsLo >= 1, "one slice per wave");
+  // LDS 1 KiB slot-rows of the CU's n rows (what the registers do not hold).
+  __host__ __device__ static constexpr int lds_rows(int n) {
+    int total = 0;
+    for (int w = 0; w < kRowSlices; ++w) {
+      const int ns = row_slice_begin(NJ, w + 1) - row_slice_begin(NJ, w);
+      total += (n > reg_f4(ns) / ns ? n - reg_f4(ns) / ns : 0) * ns;
+    }
+    return total;
+  }
+  __host__ __device__ static constexpr int capacity() {
+    int n = kMaxRows;
+    // LDS rows, then the per-lane slice sums of every row.
+    while (n > 0 && lds_rows(n) * kWave * 16 + n * kRowSlices * kWave * 4 > kRegionBytes) --n;
+    return n;
+  }
+  float4 wr[kRegF4];
+  float4 *lw = nullptr;   // this wave's LDS rows: ((r - nr) * ns + s) * 64 + lane
+  int n = 0, c0 = 0, ns = 0, nr = 0;
 
+  __device__ void init(int rows, float4 *region_f4) {
+    n = rows;
+    const int w = wave_u();
+    c0 = row_slice_begin(NJ, w);
+    ns = row_slice_begin(NJ, w + 1) - c0;
+    nr = reg_f4(ns) / ns;
+    int off = 0;
+    for (int v = 0; v < w; ++v) {
+      const int nsv = row_slice_begin(NJ, v + 1) - row_slice_begin(NJ, v);
+      off += (n > reg_f4(nsv) / nsv ? n - reg_f4(nsv) / nsv : 0) * nsv;
+    }
+    lw = region_f4 + off * kWave;
+  }
+  template <int Ns, typename Row>
+  __device__ void prefetch_regs_ns(Row row) {
+    constexpr int Nr = reg_f4(Ns) / Ns;
+    const int lane = lane_id();
+#pragma unroll
+    for (int r = 0; r < Nr; ++r)
+#pragma unroll
+      for (int s = 0; s < Ns; ++s)
+        wr[r * Ns + s] = r < n ? ld_weight(reinterpret_cast<const float4 *>(row(r)) + (c0 + s) * kWave + lane)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   template <typename Row>
   __device__ void prefetch_regs(Row row) {
-    const int w = wave_u();
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      const int k = w + kW * j;
-      if (k < n) {
-        load_row_weights<I>(row(k), wv[j]);
-      } else {
-#pragma unroll
-        for (int c = 0; c < NJ; ++c) wv[j][c] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
+    if (ns == kNsHi) prefetch_regs_ns<kNsHi>(row); else prefetch_regs_ns<kNsLo>(row);
   }
   template <typename Row>
   __device__ void prefetch_lds(Row row) {
     const int lane = lane_id();
-    for (int k = kW * S + wave_u(); k < n && k - kW * S < Lcap; k += kW) {
-      const float4 *src = reinterpret_cast<const float4 *>(row(k));
-      float4 *dst = rowsl + (k - kW * S) * RowF4;
-#pragma unroll
-      for (int c = 0; c < NJ; ++c) dma16<kPolicyNt>(src + c * kWave + lane, dst + c * kWave);
-    }
+    for (int r = nr; r < n; ++r)
+      for (int s = 0; s < ns; ++s)
+        dma16<kPolicyNt>(reinterpret_cast<const float4 *>(row(r)) + (c0 + s) * kWave + lane,
+                         lw + ((r - nr) * ns + s) * kWave);
   }
-  // Each wave's rows (its register slots and at most kLdsPerWave LDS rows)
-  // share every operand float4 read from LDS; the operand is read in
-  // chunks of 4 float4 so the compiler cannot hoist all of it at once.
-  static constexpr int kLdsPerWave = (Lcap + kW - 1) / kW;
-  template <typename Prep, typename Epi, typename Mid>
-  __device__ void compute(const float *x, Prep prep, Epi epi, Mid mid) const {
-    const int w = wave_u(), lane = lane_id();
-    const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    float acc[S + kLdsPerWave];
+  // Per-lane slice sums of every row with this wave's activation slice xa:
+  // row r's lands in part[(r * kW + wave) * 64 + lane].
+  template <int Ns>
+  __device__ void sums_ns(const float4 (&xa)[kNsHi], float *part) const {
+    constexpr int Nr = reg_f4(Ns) / Ns;
+    const int lane = lane_id(), w = wave_u();
 #pragma unroll
-    for (int r = 0; r < S + kLdsPerWave; ++r) acc[r] = 0.f;
+    for (int r = 0; r < kMaxRows; ++r) {
+      if (r < n) {
+        float acc = 0.f;
 #pragma unroll
-    for (int c0 = 0; c0 < NJ; c0 += 4) {
-      asm volatile("" ::: "memory");
-#pragma unroll
-      for (int c = c0; c < c0 + 4 && c < NJ; ++c) {
-        const float4 xc = x4[c * kWave + lane];
-#pragma unroll
-        for (int j = 0; j < S; ++j) acc[j] = fma4(wv[j][c], xc, acc[j]);
-#pragma unroll
-        for (int i = 0; i < kLdsPerWave; ++i) {
-          const int k = kW * S + w + kW * i;
-          if (k < n && k - kW * S < Lcap)
-            acc[S + i] = fma4(rowsl[(k - kW * S) * RowF4 + c * kWave + lane], xc, acc[S + i]);
-        }
+        for (int s = 0; s < Ns; ++s)
+          acc = fma4(r < Nr ? wr[(r < Nr ? r : 0) * Ns + s] : lw[((r - Nr) * Ns + s) * kWave + lane], xa[s], acc);
+        part[(r * kW + w) * kWave + lane] = acc;
       }
     }
-    mid();
-    // Row j of the wave finishes in lane j (see PairRole::compute).
-    constexpr int kUnits = S + kLdsPerWave;
-    static_assert(kUnits <= kWave, "one lane per row");
-    float mine = 0.f;
-#pragma unroll
-    for (int j = 0; j < kUnits; ++j) {
-      const float sum = wave_sum(acc[j]);
-      mine = lane == j ? sum : mine;
-    }
-    const int k = lane < S ? w + kW * lane : kW * S + w + kW * (lane - S);
-    if (lane < kUnits && k < n && (lane < S || k - kW * S < Lcap)) epi(k, mine, prep(k));
   }
-  static constexpr int capacity() { return kW * S + Lcap; }
+  __device__ void sums(const float4 (&xa)[kNsHi], float *part) const {
+    if (ns == kNsHi) sums_ns<kNsHi>(xa, part); else sums_ns<kNsLo>(xa, part);
+  }
 };
 
 // 1/rms of x[0..N) over the workgroup: the arithmetic of block_inv_rms
@@ -683,10 +703,9 @@ struct Shape {
   static constexpr int PartFloats = NQ * kAttnMaxChunks * kRoleRecStride;
   static constexpr int LO = (kRegionBytes - PartFloats * 4) / UnitBytes;
   static constexpr int LG = kRegionBytes / UnitBytes;
-  static constexpr int LD = (kRegionBytes - I * 4) / RowBytes;
   static_assert(QkvRows % 2 == 0 && H % 2 == 0, "row pairs");
   static_assert(G <= kW && NQ % NKV == 0, "one wave per query head of a group");
-  static_assert(LQ > 0 && LO > 0 && LG > 0 && LD > 0, "LDS plan");
+  static_assert(LQ > 0 && LO > 0 && LG > 0, "LDS plan");
   static_assert(H <= 1024 && QD <= 1024, "common vectors");
 };
 
@@ -1422,11 +1441,10 @@ struct Roles {
   // ---- down + residual ------------------------------------------------------
   __device__ void run_down() {
     const int u0 = split_begin(H, nrole, rank);
-    RowRole<I, kSlotsD, Sh::LD> rd;
-    rd.n = split_begin(H, nrole, rank + 1) - u0;
-    rd.rowsl = reinterpret_cast<float4 *>(region);
-    if (!fits(rd.n, rd.capacity())) return;
-    float *act = reinterpret_cast<float *>(region + Sh::LD * Sh::RowBytes);
+    DownRole<I> rd;
+    const int n = split_begin(H, nrole, rank + 1) - u0;
+    if (!fits(n, DownRole<I>::capacity())) return;
+    rd.init(n, reinterpret_cast<float4 *>(region));
     auto row = [&](int l) {
       const float *base = layer(l).wd;
       return [=](int k) { return base + static_cast<size_t>(u0 + k) * I; };
@@ -1434,21 +1452,57 @@ struct Roles {
     auto pre_lds = [&](int l, int) { rd.prefetch_lds(row(l)); };
     auto pre_regs = [&](int l) { rd.prefetch_regs(row(l)); };
     OutMap om;  // rows [u0, u0 + n), staged from u0 rounded down to 4
-    om.take(u0, rd.n, u0 & ~3, threadIdx.x, 0);
+    om.take(u0, n, u0 & ~3, threadIdx.x, 0);
     const int hb4 = u0 / 4;                       // float4s of h1 covering [u0, u0 + n)
-    const int hn4 = (u0 + rd.n + 3) / 4 - hb4;
+    const int hn4 = (u0 + n + 3) / 4 - hb4;
+    // Per-lane slice sums [row][wave][lane], after this CU's LDS rows.
+    float *part = reinterpret_cast<float *>(region) + DownRole<I>::lds_rows(n) * kWave * 4;
+    float *stage = cm.top;  // row u0 + k at stage[k + (u0 & 3)]
     loop(kRoleDown, true, [&](uint32_t t, int l, int position) {
       const Slots out = s_hid(l, t);
       if (om.q >= 0) clear_quad(s_hid(l, t + 1), om);
-      float *stage = cm.top;  // row u0 + k at stage[k + (u0 & 3)]
       if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), hb4, hn4, cm.vec, a.error, cm.flags)) return false;
-      hint_wait(s_act(l, t), 0, I / 4, a.error, cm.flags);  // EXPERIMENT
-      if (!gather4c<(I / 4 + kT - 1) / kT>(s_act(l, t), 0, I / 4, act, a.error, cm.flags)) return false;
+      // This wave's slice of the activation, straight into registers.
+      float4 xa[DownRole<I>::kNsHi];
+      bool ok = true;
+      {
+        const Slots src = s_act(l, t);
+        uint32_t pending = (1u << rd.ns) - 1u;
+        for (uint32_t spin = 0; ok; ++spin) {
+          Quad got[DownRole<I>::kNsHi];
+#pragma unroll
+          for (int s = 0; s < DownRole<I>::kNsHi; ++s)
+            if ((pending >> s) & 1u) got[s] = __builtin_bit_cast(Quad, src.get4((rd.c0 + s) * kWave + lane));
+#pragma unroll
+          for (int s = 0; s < DownRole<I>::kNsHi; ++s) {
+            const Quad &g = got[s];
+            if (((pending >> s) & 1u) && g.w[0] != kSlotEmpty && g.w[1] != kSlotEmpty &&
+                g.w[2] != kSlotEmpty && g.w[3] != kSlotEmpty) {
+              xa[s] = make_float4(__uint_as_float(g.w[0]), __uint_as_float(g.w[1]), __uint_as_float(g.w[2]),
+                                  __uint_as_float(g.w[3]));
+              pending &= ~(1u << s);
+            }
+          }
+          vm_wait();
+          if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
+          if (spin > kSpinLimit) {
+            if (lane == 0) atomicOr(a.error, 1u);
+            ok = false;
+          }
+        }
+      }
       clock.lap(2 * kRoleDown);
       clock.mark(0);
-      rd.compute(act, [&](int k) { return cm.vec[u0 + k - 4 * hb4]; }, [&](int k, float s, float h1v) {
-        stage[k + (u0 & 3)] = h1v + s;
-      }, [&] { clock.mark(1); });
+      if (ok) rd.sums(xa, part);
+      clock.mark(1);
+      if (!block_all(ok, cm.flags)) return false;
+      for (int k = wv; k < n; k += kW) {
+        float p[kRowSlices];
+#pragma unroll
+        for (int w = 0; w < kRowSlices; ++w) p[w] = part[(k * kW + w) * kWave + lane];
+        const float sum = wave_sum(combine_slices(p));
+        if (lane == 0) stage[k + (u0 & 3)] = cm.vec[u0 + k - 4 * hb4] + sum;
+      }
       lds_barrier();
       if (om.q >= 0) put_quad(out, om, reinterpret_cast<const float4 *>(stage)[om.soff]);
       clock.mark(2);
@@ -1539,7 +1593,7 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
   // Units per role, their capacity per CU (LDS + register slots) and bytes.
   const int units[4] = {Qwen::QkvUnits, Qwen::OUnits, inter, hidden};
   const int cap[4] = {Qwen::LQ + kW * kSlotsQ, Qwen::LO + kW * kSlotsO, Qwen::LG + kW * kSlotsG,
-                      Qwen::LD + kW * kSlotsD};
+                      DownRole<4864>::capacity()};
   const double bytes[4] = {double(units[0]) * Qwen::UnitBytes, double(units[1]) * Qwen::UnitBytes,
                            double(units[2]) * Qwen::UnitBytes, double(units[3]) * Qwen::RowBytes};
   const double total = bytes[0] + bytes[1] + bytes[2] + bytes[3];
