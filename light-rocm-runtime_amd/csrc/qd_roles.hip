@@ -86,6 +86,21 @@ __device__ __forceinline__ void vm_wait() {
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   asm volatile("" ::: "memory");
 }
+// Prefetch pacing: after each prefetch load a wave waits until at most
+// kPaceDepth of its vector memory operations are outstanding (0: no limit).
+// A role issues its next-layer weights right after it publishes; unpaced,
+// the gate/up CUs alone put ~35 MB of loads in flight at once, queued ahead
+// of the hand-off polls of other roles. Depth 2 still completes every role's
+// share well before its next input arrives.
+#ifndef QD_PACE
+#define QD_PACE 2
+#endif
+constexpr unsigned kPaceDepth = QD_PACE;
+static_assert(kPaceDepth < 64, "vmcnt is six bits");
+__device__ __forceinline__ void pace() {
+  if constexpr (kPaceDepth > 0)
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | (kPaceDepth & 15u) | ((kPaceDepth >> 4) << 14));
+}
 // Whole-workgroup AND (flags: one LDS word per wave). The ballot is taken
 // with the whole wave active, then lane 0 records it.
 __device__ __forceinline__ bool block_all(bool v, uint32_t *flags) {
@@ -492,6 +507,7 @@ struct PairRole {
         const float *ra, *rb;
         rows(k, ra, rb);
         load_pair_weights<H>(ra, rb, wv[j]);
+        pace();
       } else {
         // An empty slot is still redefined, so its previous contents are
         // not kept live across the code between two prefetches.
@@ -514,6 +530,7 @@ struct PairRole {
         const int f = c * kWave + lane;
         const float4 *src = f < K4 ? a4 + f : (f < 2 * K4 ? b4 + (f - K4) : a4);
         dma16<kPolicyNt>(src, dst + c * kWave);
+        pace();
       }
     }
   }
@@ -617,11 +634,13 @@ struct DownRole {
     constexpr int Nr = reg_f4(Ns) / Ns;
     const int lane = lane_id();
 #pragma unroll
-    for (int r = 0; r < Nr; ++r)
+    for (int r = 0; r < Nr; ++r) {
 #pragma unroll
       for (int s = 0; s < Ns; ++s)
         wr[r * Ns + s] = r < n ? ld_weight(reinterpret_cast<const float4 *>(row(r)) + (c0 + s) * kWave + lane)
                                : make_float4(0.f, 0.f, 0.f, 0.f);
+      pace();
+    }
   }
   template <typename Row>
   __device__ void prefetch_regs(Row row) {
@@ -631,9 +650,11 @@ struct DownRole {
   __device__ void prefetch_lds(Row row) {
     const int lane = lane_id();
     for (int r = nr; r < n; ++r)
-      for (int s = 0; s < ns; ++s)
+      for (int s = 0; s < ns; ++s) {
         dma16<kPolicyNt>(reinterpret_cast<const float4 *>(row(r)) + (c0 + s) * kWave + lane,
                          lw + ((r - nr) * ns + s) * kWave);
+        pace();
+      }
   }
   // Per-lane slice sums of every row with this wave's activation slice xa:
   // row r's lands in part[(r * kW + wave) * 64 + lane].
@@ -1152,10 +1173,14 @@ struct Roles {
       // kRoleRecStride: whole float4s.
       constexpr int kRec4 = kRoleRecStride / 4;
       {
-        // This CU's records (every head of its units' KV groups).
+        // The records token t + 1 reads (its own chunk count), spread over
+        // the role's CUs like its units. This holds however the count moves:
+        // it drops when the chunk length grows (context 1024 -> 1025) and
+        // regrows later, which leaves older records in slots beyond it.
         const Slots next = s_part(l, t + 1);
-        for (int u = rank; u < units; u += nrole) {
-          const int g = u / chunks, c = u % chunks;
+        const int chunks_next = attn_chunks(length + 1);
+        for (int u = rank; u < NKV * chunks_next; u += nrole) {
+          const int g = u / chunks_next, c = u % chunks_next;
           for (int e = threadIdx.x; e < GROUP * kRec4; e += kT)
             next.clear4(((g * GROUP + e / kRec4) * kAttnMaxChunks + c) * kRec4 + e % kRec4);
         }
@@ -1251,10 +1276,9 @@ struct Roles {
     ro.units = reinterpret_cast<float4 *>(region);
     if (!fits(ro.n, ro.capacity())) return;
     // Partial records in LDS as in the slot block: record (h, c) at
-    // (h * kAttnMaxChunks + c) * kRoleRecStride. Chunk c is written only
-    // once the context has c + 1 chunks, which stays so for the rest of the
-    // launch; the zero fill here keeps the records of chunks not yet in
-    // play finite for the merge's unconditional reads.
+    // (h * kAttnMaxChunks + c) * kRoleRecStride. The merge reads chunks
+    // beyond the token's count too (discarded by a select); the zero fill
+    // keeps what they read finite until some token has gathered them.
     float *parts = reinterpret_cast<float *>(region + Sh::LO * Sh::UnitBytes);
     for (int i = threadIdx.x; i < Sh::PartFloats; i += kT) parts[i] = 0.f;
     auto rows = [&](int l) {

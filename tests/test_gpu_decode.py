@@ -194,6 +194,29 @@ def test_resident_and_stream_generation_agree(full, monkeypatch):
     # KV written by the resident launch equals the stream path's rows too.
 
 
+def test_resident_across_chunk_length_changes_matches_stream(full, monkeypatch):
+    """Attention chunks are 64 positions up to context 1024 and 128 after:
+    the chunk count drops from 16 to 9 at 1025 and regrows to 10 at 1153.
+    A resident generation across both points equals the stream path bit for
+    bit (hand-off slots beyond the chunk count hold older records)."""
+    eng, _ = full
+    prompt = qo.fill_tokens(1000, 1, PROMPT_STREAM + 4, FULL.vocab)
+    say("resident vs stream generation, context 1001..1170")
+    eng.kv_reset(1, 0)
+    first, _, _ = eng.prefill(1, prompt, want_logits=False)
+    toks, _, logits = eng.generate(1, first, 170, want_logits=True)
+    monkeypatch.setenv("QD_RESIDENT", "0")
+    stream = qd.Engine(layers=FULL.layers, vocab=FULL.vocab, capacity=1200, max_batch=1)
+    monkeypatch.delenv("QD_RESIDENT")
+    assert stream.resident_grid() == 0
+    stream.load_synthetic(1)
+    first2, _, _ = stream.prefill(0, prompt, want_logits=False)
+    toks2, _, logits2 = stream.generate(0, first2, 170, want_logits=True)
+    stream.close()
+    assert first2 == first and toks2.tolist() == toks.tolist()
+    assert np.array_equal(logits, logits2)
+
+
 def test_generate_stops_at_eos(full):
     eng, _ = full
     prompt = qo.fill_tokens(5, 1, PROMPT_STREAM + 2, FULL.vocab)
