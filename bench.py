@@ -51,7 +51,7 @@ WEIGHT_BYTES = 1_976_131_072
 # the factors a 1 GiB device copy gives in the same profile
 # (profiles/roles_kernel_config2.md, profiles/resident_decode_kernel_config2.md).
 # Re-measured when a kernel changes; None where no measurement exists.
-RESIDENT_TRAFFIC_PER_TOKEN = 2_029_499_638
+RESIDENT_TRAFFIC_PER_TOKEN = 2_029_372_267
 RESIDENT_TRAFFIC_PER_TOKEN_TAGGED = 2_106_996_721
 
 
