@@ -53,6 +53,9 @@ WEIGHT_BYTES = 1_976_131_072
 # Re-measured when a kernel changes; None where no measurement exists.
 RESIDENT_TRAFFIC_PER_TOKEN = 2_029_372_267
 RESIDENT_TRAFFIC_PER_TOKEN_TAGGED = 2_106_996_721
+# The role-split kernel on the 32-token launch of the config-3 workload
+# (profiles/roles_kernel_config3.md).
+RESIDENT_TRAFFIC_PER_TOKEN_LONG = 2_125_781_706
 
 
 def step_bytes(length: int) -> int:
@@ -147,19 +150,36 @@ def cpu_prefill_baseline(seed, n):
 
 # ---- workloads ------------------------------------------------------------------
 
+CONFIG2_TEXT = ("BASELINE config 2: 24-layer Qwen2.5-0.5B-shape FP32 decoder + tied 151936x896 LM "
+                "head, batch 1, prompt 512 then greedy decode with device argmax feedback")
+# the same model decoding at KV context up to 4096.
+LONG_PROMPT = 4064
+CONFIG3_TEXT = ("BASELINE config 3: 24-layer Qwen2.5-0.5B-shape FP32 decoder + tied 151936x896 LM "
+                "head, batch 1, prompt 4064 then greedy decode to KV context 4096 with device "
+                "argmax feedback")
+
+
 def run_decode(K, W, no_cpu):
-    capacity = PROMPT + max(K, W) + 8
+    return decode_line(K, W, no_cpu, PROMPT, CONFIG2_TEXT, RESIDENT_TRAFFIC_PER_TOKEN)
+
+
+def run_long(K, W, no_cpu):
+    return decode_line(K, W, no_cpu, LONG_PROMPT, CONFIG3_TEXT, RESIDENT_TRAFFIC_PER_TOKEN_LONG)
+
+
+def decode_line(K, W, no_cpu, prompt_len, workload, traffic_per_token):
+    capacity = prompt_len + max(K, W) + 8
     log("engine create + synthetic weights")
     eng = qd.Engine(capacity=capacity, max_batch=1)
     eng.load_synthetic(SEED)
-    prompt = stream_tokens(PROMPT, SEED, PROMPT_STREAM, VOCAB)
-    log("prefill 512")
+    prompt = stream_tokens(prompt_len, SEED, PROMPT_STREAM, VOCAB)
+    log(f"prefill {prompt_len}")
     first, _, _ = eng.prefill(0, prompt, want_logits=False)
 
     if W:
         log(f"warmup {W}")
         eng.generate(0, first, W)
-        eng.kv_reset(0, PROMPT)
+        eng.kv_reset(0, prompt_len)
 
     log(f"timed {K} decode steps")
     eng.sync()
@@ -171,7 +191,7 @@ def run_decode(K, W, no_cpu):
     assert len(toks) == K, (len(toks), reason)
     dev_s = timing.total_us * 1e-6
     tok_s = K / wall
-    total_bytes = sum(step_bytes(PROMPT + 1 + i) for i in range(K))
+    total_bytes = sum(step_bytes(prompt_len + 1 + i) for i in range(K))
     step_gbs = total_bytes / dev_s / 1e9
 
     grid = eng.resident_grid()
@@ -181,12 +201,14 @@ def run_decode(K, W, no_cpu):
         # The role-split kernel runs unless QD_RESIDENT_KERNEL=tagged selects
         # the tagged-dataflow kernel.
         tagged = os.environ.get("QD_RESIDENT_KERNEL") == "tagged"
-        per_token = RESIDENT_TRAFFIC_PER_TOKEN_TAGGED if tagged else RESIDENT_TRAFFIC_PER_TOKEN
+        per_token = RESIDENT_TRAFFIC_PER_TOKEN_TAGGED if tagged else traffic_per_token
+        if tagged and prompt_len != PROMPT:
+            per_token = None
         traffic = per_token * K if per_token else None
         roof = roofline_hbm("resident_decode_kernel" if tagged else "roles_kernel", timing.total_us,
                             float(total_bytes), traffic)
     else:
-        eng.kv_reset(0, PROMPT)
+        eng.kv_reset(0, prompt_len)
         prof = eng.profile_kernels(0, first, min(K, 16))
         name, (_, avg_us, avg_bytes, _) = dominant(prof)
         roof = roofline_hbm(name, avg_us, avg_bytes)
@@ -195,9 +217,9 @@ def run_decode(K, W, no_cpu):
 
     cpu = None
     if not no_cpu:
-        steps, el, cores = cpu_decode_baseline(SEED, [PROMPT])
+        steps, el, cores = cpu_decode_baseline(SEED, [prompt_len])
         cpu = {"value": round(steps / el, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
-               "sample": f"{steps} decode steps at context {PROMPT + 1}..{PROMPT + steps}, "
+               "sample": f"{steps} decode steps at context {prompt_len + 1}..{prompt_len + steps}, "
                          f"24 layers + 151936-row LM head, oracle/libqwen_oracle.so FP32 OpenMP"}
     return {
         "metric": METRIC,
@@ -207,12 +229,10 @@ def run_decode(K, W, no_cpu):
         "higher_is_better": True,
         "dtype": "f32",
         "data": "synthetic: random-init N(0,0.02) weights / N(0,0.01) biases, seed 1; "
-                "512 uniform random prompt tokens",
+                f"{prompt_len} uniform random prompt tokens",
         "config": {
-            "workload": "BASELINE config 2: 24-layer Qwen2.5-0.5B-shape FP32 decoder + tied "
-                        "151936x896 LM head, batch 1, prompt 512 then greedy decode with "
-                        "device argmax feedback",
-            "batch": 1, "context": f"{PROMPT + 1}..{PROMPT + K}", "layers": 24,
+            "workload": workload,
+            "batch": 1, "context": f"{prompt_len + 1}..{prompt_len + K}", "layers": 24,
             "hidden": 896, "vocab": VOCAB,
         },
         "step_hbm": {"achieved_gbs": round(step_gbs, 1), "peak_gbs": HBM_PEAK_GBS,
@@ -394,7 +414,7 @@ def copy_probe(mib: int):
     log(f"copy probe: 3 x {mib} MiB device-to-device")
 
 
-DEFAULTS = {"decode": (64, 8), "batch16": (32, 4), "prefill": (20, 3)}
+DEFAULTS = {"decode": (64, 8), "long": (32, 4), "batch16": (32, 4), "prefill": (20, 3)}
 
 
 def main():
@@ -415,7 +435,8 @@ def main():
     W = args.warmup if args.warmup is not None else DEFAULTS[args.workload][1]
     if K <= 0:
         sys.exit("--steps must be positive")
-    run = {"decode": run_decode, "batch16": run_batch16, "prefill": run_prefill}[args.workload]
+    run = {"decode": run_decode, "long": run_long, "batch16": run_batch16,
+           "prefill": run_prefill}[args.workload]
     out = run(K, W, args.no_cpu)
     if args.copy_probe:
         copy_probe(args.copy_probe)
