@@ -318,31 +318,6 @@ __device__ bool gather4(const Slots &src, int n4, float4 *dst, uint32_t *error, 
   }
 }
 
-// Light pre-poll: wave 0 waits until 8 float4s spread over [first4,
-// first4 + n4) are written (their producers are spread over the range), so
-// the full gather that follows does not re-read the whole range while
-// nothing has arrived. Returns false when the wait gave up.
-__device__ inline bool hint_wait(const Slots &src, int first4, int n4, uint32_t *error, uint32_t *flags) {
-  if (wave_u() == 0) {
-    const int lane = lane_id();
-    const int q = first4 + (lane < 8 ? (lane * n4) / 8 + n4 / 16 : 0);
-    for (uint32_t spin = 0;; ++spin) {
-      bool ok = true;
-      if (lane < 8) {
-        const Quad g = __builtin_bit_cast(Quad, src.get4(q));
-        ok = g.w[0] != kSlotEmpty && g.w[1] != kSlotEmpty && g.w[2] != kSlotEmpty && g.w[3] != kSlotEmpty;
-      }
-      vm_wait();
-      if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
-      if (spin > kSpinLimit) {
-        if (lane == 0) atomicOr(error, 1u);
-        break;
-      }
-    }
-  }
-  return block_all(true, flags);
-}
-
 // Contiguous float4s [first4, first4 + n4) of a slot block -> dst[0, n4).
 template <int kMaxPer>
 __device__ bool gather4c(const Slots &src, int first4, int n4, float *dst, uint32_t *error,
