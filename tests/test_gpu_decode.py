@@ -67,6 +67,31 @@ def full():
     model.close()
 
 
+@pytest.fixture(scope="module")
+def stream_full():
+    """The same model on an engine that generates with the stream-ordered
+    kernels only (QD_RESIDENT=0 at create time): the resident kernel's
+    bit-exact twin."""
+    say("full model: stream-ordered engine (QD_RESIDENT=0)")
+    os.environ["QD_RESIDENT"] = "0"
+    try:
+        eng = qd.Engine(layers=FULL.layers, vocab=FULL.vocab, capacity=CAPACITY, max_batch=2)
+    finally:
+        del os.environ["QD_RESIDENT"]
+    assert eng.resident_grid() == 0
+    eng.load_synthetic(1)
+    yield eng
+    eng.close()
+
+
+def assert_kv_equal(a, b, slot_a, slot_b, start, count, what):
+    """KV rows [start, start + count) of every layer bit-identical."""
+    for layer in range(FULL.layers):
+        ka, va = a.read_kv(slot_a, layer, start, count)
+        kb, vb = b.read_kv(slot_b, layer, start, count)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"{what}: layer {layer}"
+
+
 def test_synthetic_weights_bit_identical_to_oracle(full):
     eng, model = full
     say("weights readback")
@@ -171,9 +196,9 @@ def test_generate_matches_step_loop_and_oracle(full):
         feed = rtok
 
 
-def test_resident_and_stream_generation_agree(full, monkeypatch):
+def test_resident_and_stream_generation_agree(full, stream_full):
     """The resident megakernel and the stream-ordered kernels run the same
-    arithmetic in the same order: identical tokens and logits."""
+    arithmetic in the same order: identical tokens, logits and KV rows."""
     eng, _ = full
     assert eng.resident_grid() > 0
     prompt = qo.fill_tokens(9, 1, PROMPT_STREAM + 3, FULL.vocab)
@@ -181,20 +206,17 @@ def test_resident_and_stream_generation_agree(full, monkeypatch):
     eng.kv_reset(0, 0)
     first, _, _ = eng.prefill(0, prompt, want_logits=False)
     toks, _, logits = eng.generate(0, first, 12, want_logits=True)
-    monkeypatch.setenv("QD_RESIDENT", "0")
-    stream = qd.Engine(layers=FULL.layers, vocab=FULL.vocab, capacity=64, max_batch=1)
-    monkeypatch.delenv("QD_RESIDENT")
-    assert stream.resident_grid() == 0
-    stream.load_synthetic(1)
+    stream = stream_full
+    stream.kv_reset(0, 0)
     first2, _, _ = stream.prefill(0, prompt, want_logits=False)
     toks2, _, logits2 = stream.generate(0, first2, 12, want_logits=True)
-    stream.close()
     assert first2 == first and toks2.tolist() == toks.tolist()
     assert np.array_equal(logits, logits2)
-    # KV written by the resident launch equals the stream path's rows too.
+    # KV rows written by the resident launch (the last token's included).
+    assert_kv_equal(eng, stream, 0, 0, len(prompt), 12, "resident KV")
 
 
-def test_resident_across_chunk_length_changes_matches_stream(full, monkeypatch):
+def test_resident_across_chunk_length_changes_matches_stream(full, stream_full):
     """Attention chunks are 64 positions up to context 1024 and 128 after:
     the chunk count drops from 16 to 9 at 1025 and regrows to 10 at 1153.
     A resident generation across both points equals the stream path bit for
@@ -205,16 +227,71 @@ def test_resident_across_chunk_length_changes_matches_stream(full, monkeypatch):
     eng.kv_reset(1, 0)
     first, _, _ = eng.prefill(1, prompt, want_logits=False)
     toks, _, logits = eng.generate(1, first, 170, want_logits=True)
-    monkeypatch.setenv("QD_RESIDENT", "0")
-    stream = qd.Engine(layers=FULL.layers, vocab=FULL.vocab, capacity=1200, max_batch=1)
-    monkeypatch.delenv("QD_RESIDENT")
-    assert stream.resident_grid() == 0
-    stream.load_synthetic(1)
+    stream = stream_full
+    stream.kv_reset(0, 0)
     first2, _, _ = stream.prefill(0, prompt, want_logits=False)
     toks2, _, logits2 = stream.generate(0, first2, 170, want_logits=True)
-    stream.close()
     assert first2 == first and toks2.tolist() == toks.tolist()
     assert np.array_equal(logits, logits2)
+    assert_kv_equal(eng, stream, 1, 0, len(prompt), 170, "resident KV")
+
+
+def synthetic_context(engines, cache, length, seed=7):
+    """N(0,1) K/V rows at positions [0, length) of every layer, written into
+    slot 0 of each engine and into the oracle cache."""
+    for layer in range(FULL.layers):
+        k = qo.fill_normal(length * 128, seed, KV_STREAM + 2 * layer, 0.0, 1.0).reshape(length, 128)
+        v = qo.fill_normal(length * 128, seed, KV_STREAM + 2 * layer + 1, 0.0, 1.0).reshape(length, 128)
+        for e in engines:
+            e.write_kv(0, layer, 0, k, v)
+        cache.layer(layer, False)[:length] = k
+        cache.layer(layer, True)[:length] = v
+    for e in engines:
+        e.kv_reset(0, length)
+
+
+def long_context_generation(full, stream_full, context, steps, token, what):
+    """Resident generation of `steps` tokens after a synthetic context,
+    against the stream path (bit-exact tokens, logits, KV rows) and the
+    oracle teacher-forced on the engine's tokens (logits within the bar)."""
+    eng, model = full
+    cache = qo.Cache(model, context + steps + 8)
+    synthetic_context([eng, stream_full], cache, context)
+    say(f"{what}: resident generation")
+    toks, reason, logits = eng.generate(0, token, steps, want_logits=True)
+    assert reason == qd.STOP_MAXIMUM_TOKENS and len(toks) == steps
+    say(f"{what}: stream generation")
+    toks2, _, logits2 = stream_full.generate(0, token, steps, want_logits=True)
+    assert toks.tolist() == toks2.tolist()
+    assert np.array_equal(logits, logits2)
+    assert_kv_equal(eng, stream_full, 0, 0, context, steps, what)
+    say(f"{what}: oracle, {steps} teacher-forced steps")
+    feed, errs = token, []
+    for i in range(steps):
+        last = i == steps - 1
+        want = last or i % 8 == 0
+        rtok, _, rlog = cache.decode_step(feed, context + i, want_logits=want)
+        if want:
+            errs.append(check_logits(int(toks[i]), logits[i], rtok, rlog, f"{what} step {i}"))
+        feed = int(toks[i])
+    gk, gv = eng.read_kv(0, 23, context + steps - 1, 1)
+    assert rel_err(gk[0], cache.layer(23, False)[context + steps - 1]) <= HIDDEN_RTOL
+    assert rel_err(gv[0], cache.layer(23, True)[context + steps - 1]) <= HIDDEN_RTOL
+    cache.close()
+    say(f"{what}: max logits rel err {max(errs):.3e}")
+
+
+def test_resident_config3_context_4096_matches_stream_and_oracle(full, stream_full):
+    """BASELINE config 3 as the bench runs it: the resident kernel at context
+    4065..4096 (32 (KV head, 256-position chunk) attention units, more than
+    the attention CUs of the role plan, so CUs take two units)."""
+    long_context_generation(full, stream_full, 4064, 32, 4242, "config 3 resident 4065..4096")
+
+
+def test_resident_multi_window_beyond_4096_matches_stream_and_oracle(full, stream_full):
+    """Past context 4096 a chunk is 320+ positions and the resident kernel's
+    attention walks it in two LDS windows of at most 256 positions."""
+    long_context_generation(full, stream_full, 4090, 40, 777, "resident 4091..4130 (two windows)")
 
 
 def test_generate_stops_at_eos(full):
@@ -262,7 +339,7 @@ def test_prefill_512_config5_matches_oracle(full):
     prompt = qo.fill_tokens(512, 4, PROMPT_STREAM, FULL.vocab)
     say("prefill 512 (config 5) vs oracle")
     eng.kv_reset(0, 0)
-    cache = qo.Cache(model, 520)
+    cache = qo.Cache(model, 530)
     tok, _, logits = eng.prefill(0, prompt)
     rtok, _, rlogits = cache.prefill(prompt)
     check_logits(tok, logits, rtok, rlogits, "prefill 512")
@@ -277,6 +354,14 @@ def test_prefill_512_config5_matches_oracle(full):
         rtok, _, rlogits = cache.decode_step(feed, 512 + i)
         check_logits(tok, logits, rtok, rlogits, f"decode after prefill {i}")
         feed = rtok
+    # Config 2's decode range (context 516..523) on the resident kernel,
+    # directly against the oracle teacher-forced on the engine's tokens.
+    say("resident generation at context 516..523 vs oracle")
+    toks, _, gen_logits = eng.generate(0, feed, 8, want_logits=True)
+    for i, t in enumerate(toks.tolist()):
+        rtok, _, rlogits = cache.decode_step(feed, 515 + i)
+        check_logits(t, gen_logits[i], rtok, rlogits, f"resident after prefill {i}")
+        feed = t
 
 
 def test_profile_prefill_matches_prefill(full):
