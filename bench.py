@@ -49,10 +49,9 @@ WEIGHT_BYTES = 1_976_131_072
 # HBM bytes per decode token of the resident kernels, measured with rocprofv3
 # FETCH_SIZE + WRITE_SIZE on the 64-token launch of this workload, scaled by
 # the factors a 1 GiB device copy gives in the same profile
-# (profiles/roles_kernel_config2.md, profiles/resident_decode_kernel_config2.md).
+# (profiles/roles_kernel_config2.md).
 # Re-measured when a kernel changes; None where no measurement exists.
 RESIDENT_TRAFFIC_PER_TOKEN = 2_029_372_267
-RESIDENT_TRAFFIC_PER_TOKEN_TAGGED = 2_106_996_721
 # The role-split kernel on the 32-token launch of the config-3 workload
 # (profiles/roles_kernel_config3.md).
 RESIDENT_TRAFFIC_PER_TOKEN_LONG = 2_125_781_706
@@ -198,15 +197,8 @@ def decode_line(K, W, no_cpu, prompt_len, workload, traffic_per_token):
     if grid:
         # One resident launch runs all K tokens: its HIP-event duration on the
         # engine stream is the kernel time, its algorithmic bytes the K steps'.
-        # The role-split kernel runs unless QD_RESIDENT_KERNEL=tagged selects
-        # the tagged-dataflow kernel.
-        tagged = os.environ.get("QD_RESIDENT_KERNEL") == "tagged"
-        per_token = RESIDENT_TRAFFIC_PER_TOKEN_TAGGED if tagged else traffic_per_token
-        if tagged and prompt_len != PROMPT:
-            per_token = None
-        traffic = per_token * K if per_token else None
-        roof = roofline_hbm("resident_decode_kernel" if tagged else "roles_kernel", timing.total_us,
-                            float(total_bytes), traffic)
+        traffic = traffic_per_token * K if traffic_per_token else None
+        roof = roofline_hbm("roles_kernel", timing.total_us, float(total_bytes), traffic)
     else:
         eng.kv_reset(0, prompt_len)
         prof = eng.profile_kernels(0, first, min(K, 16))

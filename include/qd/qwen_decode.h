@@ -136,8 +136,11 @@ QD_API qd_status qd_engine_device_bytes(const qd_engine *engine, uint64_t *bytes
 
 /* Workgroups of the resident decode megakernel qd_generate_resident uses
  * (one per CU), or 0 when the engine generates with stream-ordered kernels
- * (QD_RESIDENT=0 in the environment at create time, or a capacity beyond
- * the resident kernel's split-KV table). */
+ * (QD_RESIDENT=0 in the environment at create time, a device that cannot
+ * co-schedule one workgroup per CU, or a refused cooperative launch). A
+ * resident hand-off wait that gives up (a producer never published within
+ * its spin limit) fails the call with QD_ERROR_DEVICE_FAULT; every
+ * workgroup still exits. */
 QD_API qd_status qd_engine_resident_grid(const qd_engine *engine,
                                          uint32_t *grid);
 
@@ -165,7 +168,9 @@ QD_API qd_status qd_kv_reset(qd_engine *engine, uint32_t seq,
                              uint32_t position);
 /* Writes / reads `count` positions of one layer's K and V starting at
  * `start`, token-major [count][kv_heads*head_dim]. Writing mirrors the KV
- * half of DecoderLayer::copy_inputs (examples/triton/mini_decoder_layer.hpp:256-276). */
+ * half of DecoderLayer::copy_inputs (examples/triton/mini_decoder_layer.hpp:256-276);
+ * every written NaN is stored as the canonical quiet NaN 0x7FC00000, as are
+ * NaNs in weights loaded by qd_load_bundle. */
 QD_API qd_status qd_write_kv(qd_engine *engine, uint32_t seq, uint32_t layer,
                              uint32_t start, uint32_t count, const float *k,
                              const float *v);

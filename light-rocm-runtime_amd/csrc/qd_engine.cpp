@@ -106,6 +106,7 @@ struct qd_engine {
   uint64_t device_bytes = 0;
 
   float *weights = nullptr;  // arena of all layer weights
+  size_t weights_floats = 0;
   std::vector<qd::LayerPtrs> layers;
   float *embed = nullptr, *lm_head = nullptr, *final_norm = nullptr;
   float *k_cache = nullptr, *v_cache = nullptr;
@@ -120,18 +121,15 @@ struct qd_engine {
   float *history = nullptr;        // generate-mode logits [capacity][vocab]
   size_t history_rows = 0;
 
-  // Resident megakernel state.
+  // Resident megakernel state (qd_roles.hip): one workgroup per CU.
   qd::LayerPtrs *layer_ptrs_dev = nullptr;  // [layers]
-  uint64_t *tagged = nullptr;               // (value, tag) arena
-  float *roles_slots = nullptr;             // role kernel hand-off slots
+  uint64_t *top_pairs = nullptr;            // argmax (value, tag) partials [4 * roles_grid]
+  float *roles_slots = nullptr;             // hand-off slots
   size_t roles_slot_bytes = 0;
-  size_t tagged_elems = 0;
   uint32_t epoch = 0;                       // last launch epoch (1..4095)
   uint32_t *resident_error = nullptr;       // [1]
-  int resident_grid = 0;                    // 0: resident path unavailable
-  // Role-split resident kernel (one 512-thread workgroup per CU); when
-  // roles_grid is 0 the tagged-dataflow kernel runs with resident_grid.
-  int roles_grid = 0;
+  uint32_t spin_limit = qd::kResidentSpinLimit;
+  int roles_grid = 0;                       // 0: resident path unavailable
   std::string resident_off_reason;
   // Prompt workspace (allocated on the first prefill): rows of the hidden
   // states, RMSNorm output, packed QKV, attention output, gate|up and SwiGLU
@@ -507,23 +505,25 @@ struct qd_engine {
     }
   }
 
-  // Launches the resident megakernel (stream ordered; no synchronisation).
-  // Each launch gets a fresh epoch so no tag of an earlier launch matches;
-  // when the epoch counter wraps the tagged arena is cleared first.
-  // Returns the launch status; the caller decides how to handle a refused
-  // cooperative launch.
-  hipError_t launch_resident(uint32_t seq, uint32_t first_token, uint32_t max_tokens,
-                             uint32_t eos, float *hist, int use_hist, uint64_t *stage_ticks,
-                             uint64_t *trace = nullptr, uint32_t trace_token = 0) {
+  // Role plan of a resident launch whose longest context is `reach`; false
+  // when the resident path is off or the plan does not fit the grid.
+  bool resident_plan(uint32_t reach, qd::RolePlan *plan) const {
+    return roles_grid > 0 &&
+           qd::plan_roles(roles_grid, int(H), int(I), int(NQ), int(NKV), int(reach), plan);
+  }
+
+  // Launches the resident megakernel (stream ordered; no synchronisation)
+  // with a plan from resident_plan. Each launch gets a fresh epoch so no
+  // argmax tag of an earlier launch matches; when the epoch counter wraps
+  // the tag arena is cleared first. Returns the launch status; the caller
+  // decides how to handle a refused cooperative launch.
+  hipError_t launch_resident(const qd::RolePlan &plan, uint32_t seq, uint32_t first_token,
+                             uint32_t max_tokens, uint32_t eos, float *hist, int use_hist,
+                             uint64_t *stage_ticks, uint64_t *trace = nullptr,
+                             uint32_t trace_token = 0) {
     epoch = epoch % 4095u + 1u;
     if (epoch == 1u)
-      check(hipMemsetAsync(tagged, 0, tagged_elems * 8, stream), "memset");
-    uint64_t *p = tagged;
-    auto take = [&](size_t n) {
-      uint64_t *r = p;
-      p += n;
-      return static_cast<void *>(r);
-    };
+      check(hipMemsetAsync(top_pairs, 0, 4 * size_t(roles_grid) * 8, stream), "memset");
     qd::ResidentArgs ra{};
     ra.layer_ptrs = layer_ptrs_dev;
     ra.embed = embed;
@@ -533,13 +533,8 @@ struct qd_engine {
     ra.rope_sin = rope_sin;
     ra.k_cache = kv_slice(k_cache, seq, 0);
     ra.v_cache = kv_slice(v_cache, seq, 0);
-    ra.qkv = take(3 * QD);
-    ra.part = take(size_t(qd::kAttnMaxChunks) * NQ * qd::kPartStride);
-    ra.attn = take(QD);
-    ra.h1 = take(H);
-    ra.act = take(I);
-    ra.hidden = take(H);
-    ra.top = take(4 * size_t(std::max(resident_grid, roles_grid)));
+    ra.top = top_pairs;
+    ra.slots = roles_slots;
     ra.logits = hist;
     ra.out_tokens = tokens_dev;
     ra.st = states + seq;
@@ -559,28 +554,30 @@ struct qd_engine {
     ra.max_tokens = max_tokens;
     ra.eos = eos;
     ra.epoch = epoch << qd::kTagSeqBits;
+    ra.spin_limit = spin_limit;
+    for (int r = 0; r < qd::kRoleCount; ++r) ra.role_end[r] = plan.end[r];
     check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
-    if (roles_grid) {
-      qd::RolePlan plan{};
-      const int reach = static_cast<int>(positions[seq] + max_tokens);
-      if (qd::plan_roles(roles_grid, int(H), int(I), int(NQ), int(NKV), reach, &plan)) {
-        for (int r = 0; r < qd::kRoleCount; ++r) ra.role_end[r] = plan.end[r];
-        // Every hand-off slot starts empty (all bits set).
-        check(hipMemsetAsync(roles_slots, 0xFF, roles_slot_bytes, stream), "memset");
-        ra.slots = roles_slots;
-        return qd::launch_roles(stream, ra, roles_grid);
-      }
-    }
-    return qd::launch_resident(stream, ra, resident_grid);
+    // Every hand-off slot starts empty (all bits set).
+    check(hipMemsetAsync(roles_slots, 0xFF, roles_slot_bytes, stream), "memset");
+    return qd::launch_roles(stream, ra, roles_grid);
   }
 
-  // Grid of the resident kernel a launch reaching `reach` positions uses.
-  int active_resident_grid(uint32_t reach) const {
-    qd::RolePlan plan{};
-    if (roles_grid &&
-        qd::plan_roles(roles_grid, int(H), int(I), int(NQ), int(NKV), int(reach), &plan))
-      return roles_grid;
-    return resident_grid;
+  // After a resident launch has completed (stream synchronised): turns the
+  // kernel's error word into a status.
+  void check_resident_error() {
+    uint32_t err = 0;
+    check(hipMemcpyAsync(&err, resident_error, 4, hipMemcpyDeviceToHost, stream), "D2H");
+    sync();
+    if (err & qd::kResidentPlanOverfill)
+      fail(QD_ERROR_RUNTIME,
+           "resident role plan gives a CU more weight units than it holds on chip (error word 0x%x)",
+           err);
+    if (err & qd::kResidentWaitGaveUp)
+      fail(QD_ERROR_DEVICE_FAULT,
+           "resident kernel: a hand-off wait gave up after %u polls without its producer "
+           "(error word 0x%x)",
+           spin_limit, err);
+    if (err) fail(QD_ERROR_DEVICE_FAULT, "resident kernel error word 0x%x", err);
   }
 
   // A cooperative launch can be refused while another process holds the
@@ -589,7 +586,6 @@ struct qd_engine {
   bool resident_refused(hipError_t err) {
     if (err != hipErrorIllegalState && err != hipErrorCooperativeLaunchTooLarge) return false;
     (void)hipGetLastError();
-    resident_grid = 0;
     roles_grid = 0;
     resident_off_reason = std::string("cooperative launch refused: ") + hipGetErrorString(err);
     return true;
@@ -597,7 +593,7 @@ struct qd_engine {
 
   // Resident launches name (token, stage) pairs in kTagSeqBits bits.
   bool resident_fits(uint32_t max_tokens) const {
-    return uint64_t(max_tokens) * (6 * L + 1) + 1 < (uint64_t(1) << qd::kTagSeqBits);
+    return uint64_t(max_tokens) * (5 * L + 1) + 1 < (uint64_t(1) << qd::kTagSeqBits);
   }
 
   void sync() { check(hipStreamSynchronize(stream), "hipStreamSynchronize"); }
@@ -717,7 +713,8 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     auto round = [](size_t n) { return (n + 63) / 64 * 64; };  // floats
     const size_t per_layer = round(e->QKV * e->H) + round(e->QKV) + round(e->H * e->QD) +
                              2 * round(e->I * e->H) + round(e->H * e->I) + 2 * round(e->H);
-    e->weights = e->alloc<float>(per_layer * e->L);
+    e->weights_floats = per_layer * e->L;
+    e->weights = e->alloc<float>(e->weights_floats);
     e->layers.resize(e->L);
     for (size_t l = 0; l < e->L; ++l) {
       float *p = e->weights + l * per_layer;
@@ -760,46 +757,34 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     e->positions.assign(e->B, 0);
     e->build_rope_tables(c.rope_theta);
 
-    // Resident path: one workgroup per CU, all co-resident (cooperative
-    // launch); disabled by QD_RESIDENT=0 or when the split-KV merge of the
-    // capacity does not fit the kernel's LDS table.
+    // Resident path: the role-split kernel, one 512-thread workgroup on
+    // every CU, all co-resident (cooperative launch), for the model shapes
+    // it is built for. QD_RESIDENT=0 turns it off (the engine then
+    // generates with the stream-ordered kernels); QD_RESIDENT_SPIN_LIMIT
+    // lowers the polls a hand-off wait makes before it gives up (tests
+    // force the give-up path with it).
     const int cus = qd::device_cu_count(c.device);
-    const int max_grid = qd::resident_max_grid(c.device);
     const char *env = std::getenv("QD_RESIDENT");
+    qd::RolePlan plan{};
     if (env && std::strcmp(env, "0") == 0) {
       e->resident_off_reason = "QD_RESIDENT=0";
-    } else if (cus < 64 || max_grid < cus) {
-      e->resident_off_reason = "device cannot co-schedule one workgroup per CU";
+    } else if (cus < 64 || cus > qd::kMaxRoleGrid || qd::roles_max_grid(c.device) < cus) {
+      e->resident_off_reason = "device cannot co-schedule one role workgroup per CU";
+    } else if (!qd::plan_roles(cus, int(e->H), int(e->I), int(e->NQ), int(e->NKV), 1, &plan)) {
+      e->resident_off_reason = "no role plan for this model shape";
     } else {
-      // Two workgroups per CU when they fit: twice the waves in flight.
-      e->resident_grid = std::min({max_grid, 2 * cus, qd::kMaxResidentGrid});
-      // Diagnostic override of the resident grid (1..max co-resident).
-      if (const char *g = std::getenv("QD_RESIDENT_GRID")) {
-        const int want = std::atoi(g);
-        if (want >= 64 && want <= std::min(max_grid, qd::kMaxResidentGrid)) e->resident_grid = want;
-      }
+      e->roles_grid = cus;
     }
-    // The role-split kernel: one 512-thread workgroup on every CU, for the
-    // model shapes it is built for; QD_RESIDENT_KERNEL=tagged keeps the
-    // tagged-dataflow kernel.
-    if (e->resident_grid > 0) {
-      const char *kind = std::getenv("QD_RESIDENT_KERNEL");
-      const int role_max = qd::roles_max_grid(c.device);
-      qd::RolePlan plan{};
-      if (!(kind && std::strcmp(kind, "tagged") == 0) && role_max >= cus &&
-          cus <= qd::kMaxRoleGrid &&
-          qd::plan_roles(cus, int(e->H), int(e->I), int(e->NQ), int(e->NKV), 1, &plan))
-        e->roles_grid = cus;
+    if (const char *lim = std::getenv("QD_RESIDENT_SPIN_LIMIT")) {
+      const long v = std::atol(lim);
+      if (v >= 1 && v <= long(qd::kResidentSpinLimit)) e->spin_limit = uint32_t(v);
     }
-    const int grid_alloc = std::max({cus, max_grid, 1});
     e->layer_ptrs_dev = e->alloc<qd::LayerPtrs>(e->L);
     check(hipMemcpyAsync(e->layer_ptrs_dev, e->layers.data(), e->L * sizeof(qd::LayerPtrs),
                          hipMemcpyHostToDevice, e->stream), "layer table upload");
-    e->tagged_elems = qd::resident_tagged_elems(int(e->H), int(e->NQ), int(e->NKV), int(e->I),
-                                                grid_alloc);
-    e->tagged = e->alloc<uint64_t>(e->tagged_elems);
-    check(hipMemsetAsync(e->tagged, 0, e->tagged_elems * 8, e->stream), "memset");
     if (e->roles_grid) {
+      e->top_pairs = e->alloc<uint64_t>(4 * size_t(e->roles_grid));
+      check(hipMemsetAsync(e->top_pairs, 0, 4 * size_t(e->roles_grid) * 8, e->stream), "memset");
       e->roles_slot_bytes = 2 * e->L * 4 *
                             qd::roles_slot_floats(int(e->H), int(e->I), int(e->NQ), int(e->NKV));
       e->roles_slots = e->alloc<float>(e->roles_slot_bytes / 4);
@@ -835,7 +820,7 @@ qd_status qd_engine_device_bytes(const qd_engine *e, uint64_t *bytes) {
 qd_status qd_engine_resident_grid(const qd_engine *e, uint32_t *grid) {
   return guard([&] {
     if (!e || !grid) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
-    *grid = static_cast<uint32_t>(e->roles_grid ? e->roles_grid : e->resident_grid);
+    *grid = static_cast<uint32_t>(e->roles_grid);
   });
 }
 
@@ -966,6 +951,12 @@ qd_status qd_load_bundle(qd_engine *e, const char *directory) {
     e->upload(e->embed, t.token_embeddings.data(), e->V * e->H);
     e->upload(e->final_norm, t.final_norm_weight.data(), e->H);
     if (e->lm_head != e->embed) e->upload(e->lm_head, t.lm_head_weight.data(), e->V * e->H);
+    // No loaded NaN keeps its payload (see launch_canonical_nan).
+    check(qd::launch_canonical_nan(e->stream, e->weights, e->weights_floats), "canonical NaN");
+    check(qd::launch_canonical_nan(e->stream, e->embed, e->V * e->H), "canonical NaN");
+    check(qd::launch_canonical_nan(e->stream, e->final_norm, e->H), "canonical NaN");
+    if (e->lm_head != e->embed)
+      check(qd::launch_canonical_nan(e->stream, e->lm_head, e->V * e->H), "canonical NaN");
     e->sync();
     if (theta != e->cfg.rope_theta) e->build_rope_tables(theta);
     e->loaded = true;
@@ -1037,6 +1028,11 @@ static void kv_copy(qd_engine *e, uint32_t seq, uint32_t layer, uint32_t start, 
   const hipMemcpyKind kind = write ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
   if (k) check(hipMemcpyAsync(write ? static_cast<void *>(dk) : k, write ? static_cast<const void *>(k) : dk, bytes, kind, e->stream), "kv copy");
   if (v) check(hipMemcpyAsync(write ? static_cast<void *>(dv) : v, write ? static_cast<const void *>(v) : dv, bytes, kind, e->stream), "kv copy");
+  if (write) {
+    // Written rows hold no NaN payload but the canonical one.
+    if (k) check(qd::launch_canonical_nan(e->stream, dk, size_t(count) * e->KVD), "canonical NaN");
+    if (v) check(qd::launch_canonical_nan(e->stream, dv, size_t(count) * e->KVD), "canonical NaN");
+  }
   e->sync();
 }
 
@@ -1340,10 +1336,12 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
       use_hist = 1;
     }
     e->push_state(seq, first_token, qd::kModeGenerate, eos, max_tokens);
-    bool resident = e->resident_grid > 0 && e->resident_fits(max_tokens);
+    qd::RolePlan plan{};
+    bool resident = e->resident_fits(max_tokens) && e->resident_plan(e->positions[seq] + max_tokens, &plan);
     check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
     if (resident) {
-      const hipError_t err = e->launch_resident(seq, first_token, max_tokens, eos, hist, use_hist, nullptr);
+      const hipError_t err =
+          e->launch_resident(plan, seq, first_token, max_tokens, eos, hist, use_hist, nullptr);
       if (err != hipSuccess) {
         if (!e->resident_refused(err)) check(err, "resident launch");
         resident = false;
@@ -1355,11 +1353,7 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
                          e->stream), "D2H");
     e->sync();
-    if (resident) {
-      uint32_t err = 0;
-      check(hipMemcpy(&err, e->resident_error, 4, hipMemcpyDeviceToHost), "D2H");
-      if (err) fail(QD_ERROR_RUNTIME, "resident kernel barrier wait timed out");
-    }
+    if (resident) e->check_resident_error();
     const qd::SeqState &s = e->h_states[seq];
     const uint32_t n = s.generated;
     check(hipMemcpyAsync(out_tokens, e->tokens_dev, size_t(n) * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
@@ -1449,18 +1443,19 @@ void profiled_resident_launch(qd_engine *e, uint32_t seq, uint32_t first_token, 
                               uint64_t *ticks_out, uint64_t *trace_out, uint32_t trace_token) {
   e->check_seq(seq);
   e->check_loaded();
-  if (e->resident_grid == 0)
+  if (e->roles_grid == 0)
     fail(QD_ERROR_NOT_SUPPORTED, "resident path disabled: %s", e->resident_off_reason.c_str());
   if (tokens == 0) fail(QD_ERROR_INVALID_ARGUMENT, "tokens must be positive");
   if (first_token >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", first_token);
   if (size_t(e->positions[seq]) + tokens > e->CAP)
     fail(QD_ERROR_INVALID_ARGUMENT, "profiling %u tokens overflows capacity", tokens);
   if (!e->resident_fits(tokens)) fail(QD_ERROR_INVALID_ARGUMENT, "too many tokens for one resident launch");
+  qd::RolePlan plan{};
+  if (!e->resident_plan(e->positions[seq] + tokens, &plan))
+    fail(QD_ERROR_NOT_SUPPORTED, "no resident role plan reaches context %zu", size_t(e->positions[seq]) + tokens);
   e->set_device();
   const size_t trace_elems =
-      trace_out ? size_t(e->active_resident_grid(e->positions[seq] + tokens)) * (e->L + 1) *
-                      qd::kResidentStages
-                : 0;
+      trace_out ? size_t(e->roles_grid) * (e->L + 1) * qd::kResidentStages : 0;
   // Temporary buffers of a diagnostic call, released before returning.
   uint64_t *ticks = nullptr, *trace = nullptr;
   check(hipMalloc(&ticks, qd::kResidentStages * sizeof(uint64_t)), "hipMalloc");
@@ -1475,7 +1470,7 @@ void profiled_resident_launch(qd_engine *e, uint32_t seq, uint32_t first_token, 
   try {
     check(hipMemsetAsync(ticks, 0, qd::kResidentStages * sizeof(uint64_t), e->stream), "memset");
     if (trace) check(hipMemsetAsync(trace, 0, trace_elems * sizeof(uint64_t), e->stream), "memset");
-    const hipError_t launched = e->launch_resident(seq, first_token, tokens, UINT32_MAX,
+    const hipError_t launched = e->launch_resident(plan, seq, first_token, tokens, UINT32_MAX,
                                                    e->logits + size_t(seq) * e->V, 0, ticks, trace,
                                                    trace_token);
     if (launched != hipSuccess) {
@@ -1491,9 +1486,7 @@ void profiled_resident_launch(qd_engine *e, uint32_t seq, uint32_t first_token, 
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState),
                          hipMemcpyDeviceToHost, e->stream), "D2H");
     e->sync();
-    uint32_t err = 0;
-    check(hipMemcpy(&err, e->resident_error, 4, hipMemcpyDeviceToHost), "D2H");
-    if (err) fail(QD_ERROR_RUNTIME, "resident kernel barrier wait timed out");
+    e->check_resident_error();
     e->positions[seq] = e->h_states[seq].position;
   } catch (...) {
     release();
@@ -1524,12 +1517,12 @@ qd_status qd_trace_resident(qd_engine *e, uint32_t seq, uint32_t first_token, ui
       fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
     if (trace_token >= tokens) fail(QD_ERROR_INVALID_ARGUMENT, "trace_token must be below tokens");
     e->check_seq(seq);
-    const int grid = e->active_resident_grid(e->positions[seq] + tokens);
+    const int grid = e->roles_grid;
     const size_t need = size_t(grid) * (e->L + 1) * qd::kResidentStages;
     *workgroups = uint32_t(grid);
     *rows = uint32_t(e->L + 1);
     *stages = qd::kResidentStages;
-    if (e->resident_grid == 0)
+    if (e->roles_grid == 0)
       fail(QD_ERROR_NOT_SUPPORTED, "resident path disabled: %s", e->resident_off_reason.c_str());
     if (capacity < need) fail(QD_ERROR_INVALID_ARGUMENT, "timeline needs %zu entries", need);
     uint64_t h[qd::kResidentStages] = {};

@@ -17,6 +17,7 @@
 //   embedding feedback      benchmarks/qwen_stateful_graph_kernel.cpp:358-390
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <type_traits>
@@ -327,9 +328,42 @@ __global__ __launch_bounds__(kBlock) void argmax_finalize_kernel(
   }
 }
 
+// Every NaN of x[0, n) becomes the canonical quiet NaN 0x7FC00000, so no
+// loaded value (nor any result derived from it: arithmetic propagates a NaN
+// operand's payload) can equal the resident kernel's empty-slot pattern.
+// A grid-stride loop over float4s plus the tail.
+__global__ void canonical_nan_kernel(float *__restrict__ x, size_t n) {
+  const size_t n4 = n / 4;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  float4 *x4 = reinterpret_cast<float4 *>(x);
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    float4 v = x4[i];
+    const bool any = __builtin_isnan(v.x) || __builtin_isnan(v.y) || __builtin_isnan(v.z) ||
+                     __builtin_isnan(v.w);
+    if (any) {
+      const float q = __builtin_bit_cast(float, 0x7FC00000u);
+      v.x = __builtin_isnan(v.x) ? q : v.x;
+      v.y = __builtin_isnan(v.y) ? q : v.y;
+      v.z = __builtin_isnan(v.z) ? q : v.z;
+      v.w = __builtin_isnan(v.w) ? q : v.w;
+      x4[i] = v;
+    }
+  }
+  const size_t tail = n4 * 4 + static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tail < n && __builtin_isnan(x[tail])) x[tail] = __builtin_bit_cast(float, 0x7FC00000u);
+}
+
 }  // namespace
 
 // ---- host launchers -----------------------------------------------------------
+
+hipError_t launch_canonical_nan(hipStream_t s, float *x, size_t n) {
+  if (n == 0) return hipSuccess;
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return hipErrorInvalidValue;
+  const size_t blocks = std::min<size_t>((n / 4 + kBlock - 1) / kBlock + 1, 4096);
+  canonical_nan_kernel<<<static_cast<unsigned>(blocks), kBlock, 0, s>>>(x, n);
+  return hipGetLastError();
+}
 
 const char *kernel_name(int id) {
   static const char *const names[kKernelCount] = {

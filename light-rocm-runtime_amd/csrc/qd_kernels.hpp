@@ -72,5 +72,7 @@ hipError_t launch_embed(hipStream_t s, const float *emb, const SeqState *st,
                         Marker *m = nullptr);
 hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m = nullptr);
 hipError_t launch_tail(hipStream_t s, const TailLaunch &p, Marker *m = nullptr);
+// Rewrites every NaN of x[0, n) (x 16-byte aligned) as 0x7FC00000.
+hipError_t launch_canonical_nan(hipStream_t s, float *x, size_t n);
 
 }  // namespace qd

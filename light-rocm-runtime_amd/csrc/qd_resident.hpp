@@ -1,4 +1,4 @@
-// Host-side launcher of the resident decode megakernel (qd_resident.hip).
+// Host-side interface of the resident decode megakernel (qd_roles.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -14,12 +14,10 @@ namespace qd {
 // LM head, argmax -> 14 entries (wait, work), then the attention work's
 // sub-phases (K/V staging, math, emit) -> 17 entries.
 constexpr int kResidentStages = 17;
-// Largest resident grid (the argmax partials are staged in LDS).
-constexpr int kMaxResidentGrid = 1024;
 
-// Role-split resident kernel (qd_roles.hip): one 512-thread workgroup per
-// CU; workgroups [0, end[kRoleQkv]) compute QKV, [end[kRoleQkv],
-// end[kRoleAttn]) attention, then O, gate/up and down.
+// Role-split resident kernel: one 512-thread workgroup per CU; workgroups
+// [0, end[kRoleQkv]) compute QKV, [end[kRoleQkv], end[kRoleAttn]) attention,
+// then O, gate/up and down.
 constexpr int kRoleThreads = 512;
 constexpr int kMaxRoleGrid = 512;
 enum ResidentRole : int { kRoleQkv = 0, kRoleAttn, kRoleO, kRoleGate, kRoleDown, kRoleCount };
@@ -27,8 +25,16 @@ struct RolePlan {
   int end[kRoleCount];  // cumulative workgroup ends per role
 };
 
-// Arguments of one resident generation on one sequence slot. The tagged
-// vectors hold 8-byte (value, tag) elements; see qd_resident.hip.
+// Bits of the kernel's error word (zero at launch). A CU that raises one
+// stops; the CUs waiting on it give up after their own bounded polls, so
+// every workgroup exits.
+constexpr uint32_t kResidentWaitGaveUp = 1u;    // a hand-off poll exhausted its spin limit
+constexpr uint32_t kResidentPlanOverfill = 2u;  // the host plan gave a CU more units than it holds
+// Polls before a hand-off wait gives up (several milliseconds; a healthy
+// hand-off takes a few microseconds).
+constexpr uint32_t kResidentSpinLimit = 1u << 21;
+
+// Arguments of one resident generation on one sequence slot.
 struct ResidentArgs {
   const LayerPtrs *layer_ptrs;  // device array [layers]
   const float *embed;           // [vocab, hidden]
@@ -38,20 +44,13 @@ struct ResidentArgs {
   const float *rope_sin;
   float *k_cache;               // slot base [layers][capacity][kv_heads*64]
   float *v_cache;
-  void *qkv;                    // tagged [heads][3 * 64]: per query head, its query,
-                                //   then this step's K and V rows of its KV head
-  void *part;                   // tagged [heads][kAttnMaxChunks][66]
-  void *attn;                   // tagged [heads*64] merged attention
-  void *h1;                     // tagged [hidden]
-  void *act;                    // tagged [intermediate]
-  void *hidden;                 // tagged [hidden]
-  void *top;                    // tagged [2 * grid]
-  float *slots;                 // role kernel: [layers][2][roles_slot_floats] hand-off
-                                //   slots, all bits set (kSlotEmpty) at launch
+  void *top;                    // (value, tag) argmax partials [2 token parities][2 * grid]
+  float *slots;                 // [layers][2][roles_slot_floats] hand-off slots, all bits set
+                                //   (kSlotEmpty) at launch
   float *logits;                // [vocab] or [max_tokens][vocab]
   uint32_t *out_tokens;         // [max_tokens]
   SeqState *st;
-  uint32_t *error;              // zero at launch; nonzero: a wait gave up
+  uint32_t *error;              // zero at launch; kResident* bits
   uint64_t *stage_ticks;        // nullptr, or [kResidentStages] 100 MHz ticks
   uint64_t *trace;              // nullptr, or [grid][layers + 1][kResidentStages]
                                 //   100 MHz timestamps of token trace_token
@@ -68,24 +67,21 @@ struct ResidentArgs {
   uint32_t max_tokens;
   uint32_t eos;
   uint32_t epoch;               // launch epoch << kTagSeqBits, never 0
-  int role_end[kRoleCount];     // role-split kernel only (RolePlan::end)
+  uint32_t spin_limit;          // polls before a wait gives up
+  int role_end[kRoleCount];     // RolePlan::end
 };
 
-// Tags: epoch << kTagSeqBits | (token * (6 * layers + 1) + stage + 1).
+// Argmax partial tags: epoch << kTagSeqBits | (token * (5 * layers + 1) + stage + 1).
 constexpr int kTagSeqBits = 20;
-// Elements of the tagged arena for a given grid.
-inline size_t resident_tagged_elems(int hidden, int heads, int kv_heads, int inter, int grid) {
-  (void)kv_heads;
-  return 4 * size_t(heads) * 64 + 16 * size_t(heads) * 66 + 3 * size_t(hidden) + inter +
-         4 * size_t(grid);
-}
 
 // Role kernel hand-off slots. Per (layer, token parity) one block of plain
 // floats, in order: the QKV output [q | k | v], the attention partial
 // records [heads][kAttnMaxChunks][kRoleRecStride] (m, l, 2 pad, acc[64]),
 // h1 [hidden], the MLP activation [intermediate] and the layer output
-// [hidden]. A slot holds kSlotEmpty until written; a bit pattern no
-// arithmetic produces (a NaN with every payload bit set).
+// [hidden]. A slot holds kSlotEmpty until written: a NaN bit pattern (every
+// payload bit set) that the kernels' arithmetic never produces, since the
+// engine canonicalises every NaN it loads (weights, embeddings, K/V rows)
+// to 0x7FC00000.
 constexpr int kRoleRecStride = 68;
 constexpr uint32_t kSlotEmpty = 0xFFFFFFFFu;
 constexpr size_t roles_slot_floats(int hidden, int inter, int heads, int kv_heads) {
@@ -93,9 +89,6 @@ constexpr size_t roles_slot_floats(int hidden, int inter, int heads, int kv_head
          2 * size_t(hidden) + size_t(inter);
 }
 
-hipError_t launch_resident(hipStream_t s, const ResidentArgs &args, int grid);
-// Largest co-resident grid on `device` (0 if the query fails).
-int resident_max_grid(int device);
 int device_cu_count(int device);
 
 // Role split of `grid` CUs for generations reaching context `max_length`;

@@ -56,7 +56,6 @@ using namespace dev;
 
 constexpr int kT = kRoleThreads;  // threads per workgroup
 constexpr int kW = kT / kWave;    // waves per workgroup
-constexpr uint32_t kSpinLimit = 1u << 21;
 // 160 KiB of LDS per CU, less what the runtime's own block reductions use.
 constexpr int kLdsBytes = 160 * 1024 - 512;
 constexpr int kAttnCap = 256;     // positions of an attention window staged in LDS
@@ -113,6 +112,12 @@ __device__ __forceinline__ bool block_all(bool v, uint32_t *flags) {
   lds_barrier();
   return all != 0u;
 }
+
+// Where a bounded wait reports that it gave up, and after how many polls.
+struct Wait {
+  uint32_t *error;
+  uint32_t limit;
+};
 
 struct Pair2 {
   float v0;
@@ -194,7 +199,7 @@ constexpr int kRegionBytes = kLdsBytes - kRegionOffset;
 // names pair p's source pair index and its destination float index (two
 // consecutive floats). Returns false when the wait gave up (error raised).
 template <int kMaxPer, typename Map>
-__device__ bool gather_map(const TagVec &src, int pairs, uint32_t tag, float *dst, uint32_t *error,
+__device__ bool gather_map(const TagVec &src, int pairs, uint32_t tag, float *dst, Wait wait,
                            uint32_t *flags, Map map) {
   const int t = threadIdx.x;
   uint32_t pending = 0;
@@ -226,8 +231,8 @@ __device__ bool gather_map(const TagVec &src, int pairs, uint32_t tag, float *ds
     // are complete when the gather returns.
     vm_wait();
     if (block_all(pending == 0, flags)) return true;
-    if (spin > kSpinLimit) {
-      if (t == 0) atomicOr(error, 1u);
+    if (spin > wait.limit) {
+      if (t == 0) atomicOr(wait.error, kResidentWaitGaveUp);
       return false;
     }
   }
@@ -236,8 +241,8 @@ __device__ bool gather_map(const TagVec &src, int pairs, uint32_t tag, float *ds
 // Contiguous gather: elements [first, first + n) (first and n even) -> dst.
 template <int kMaxPer>
 __device__ bool gather(const TagVec &src, uint32_t first, int n, uint32_t tag, float *dst,
-                       uint32_t *error, uint32_t *flags) {
-  return gather_map<kMaxPer>(src, n / 2, tag, dst, error, flags, [&](int p, uint32_t &s, int &d) {
+                       Wait wait, uint32_t *flags) {
+  return gather_map<kMaxPer>(src, n / 2, tag, dst, wait, flags, [&](int p, uint32_t &s, int &d) {
     s = first / 2 + p;
     d = 2 * p;
   });
@@ -279,7 +284,7 @@ struct Quad {
 // is complete when none of its words is kSlotEmpty. Returns false when the
 // wait gave up (error raised).
 template <int kMaxPer, typename Map>
-__device__ bool gather4(const Slots &src, int n4, float4 *dst, uint32_t *error, uint32_t *flags,
+__device__ bool gather4(const Slots &src, int n4, float4 *dst, Wait wait, uint32_t *flags,
                         Map map) {
   const int t = threadIdx.x;
   uint32_t pending = 0;
@@ -311,8 +316,8 @@ __device__ bool gather4(const Slots &src, int n4, float4 *dst, uint32_t *error, 
     // slot clears above all) are complete when the gather returns.
     vm_wait();
     if (block_all(pending == 0, flags)) return true;
-    if (spin > kSpinLimit) {
-      if (t == 0) atomicOr(error, 1u);
+    if (spin > wait.limit) {
+      if (t == 0) atomicOr(wait.error, kResidentWaitGaveUp);
       return false;
     }
   }
@@ -320,9 +325,9 @@ __device__ bool gather4(const Slots &src, int n4, float4 *dst, uint32_t *error, 
 
 // Contiguous float4s [first4, first4 + n4) of a slot block -> dst[0, n4).
 template <int kMaxPer>
-__device__ bool gather4c(const Slots &src, int first4, int n4, float *dst, uint32_t *error,
+__device__ bool gather4c(const Slots &src, int first4, int n4, float *dst, Wait wait,
                          uint32_t *flags) {
-  return gather4<kMaxPer>(src, n4, reinterpret_cast<float4 *>(dst), error, flags,
+  return gather4<kMaxPer>(src, n4, reinterpret_cast<float4 *>(dst), wait, flags,
                           [&](int p, int &s, int &d) {
                             s = first4 + p;
                             d = p;
@@ -750,6 +755,7 @@ struct Roles {
   }
 
   __device__ uint32_t tag(uint32_t seq) const { return a.epoch | (seq + 1u); }
+  __device__ Wait wt() const { return Wait{a.error, a.spin_limit}; }
   // Hand-off vectors inside a slot block (kRoleRecStride-float records).
   static constexpr int kOffQkv = 0;
   static constexpr int kOffPart = QD + 2 * KVD;
@@ -778,7 +784,7 @@ struct Roles {
   // that did is reported as an error (the other CUs' waits then give up).
   __device__ bool fits(int n, int capacity) const {
     if (n <= capacity) return true;
-    if (threadIdx.x == 0) atomicOr(a.error, 2u);
+    if (threadIdx.x == 0) atomicOr(a.error, kResidentPlanOverfill);
     return false;
   }
   __device__ uint32_t seqno(uint32_t t, int l, int s) const { return t * per_token + 5u * l + s; }
@@ -870,7 +876,7 @@ struct Roles {
                                          : make_float4(0.f, 0.f, 0.f, 0.f);
     load(gw, w0);
     __builtin_amdgcn_sched_barrier(0);
-    if (!gather4c<(H / 4 + kT - 1) / kT>(s_hid(a.layers - 1, t), 0, H / 4, cm.vec, a.error, cm.flags))
+    if (!gather4c<(H / 4 + kT - 1) / kT>(s_hid(a.layers - 1, t), 0, H / 4, cm.vec, wt(), cm.flags))
       return false;
     clock.lap(2 * kRoleCount);
     const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
@@ -937,7 +943,7 @@ struct Roles {
     const uint32_t par = t & 1u;
     const uint32_t tag_top = tag(t * per_token + 5u * a.layers);
     if (!gather<(kMaxRoleGrid + kT - 1) / kT>(ttop, par * 2 * grid, 2 * grid, tag_top, cm.top,
-                                              a.error, cm.flags))
+                                              wt(), cm.flags))
       return false;
     clock.lap(2 * kRoleCount + 2);
     float best = -INFINITY;
@@ -989,7 +995,7 @@ struct Roles {
       lds_barrier();
       return true;
     }
-    return gather4c<(H / 4 + kT - 1) / kT>(s_hid(l - 1, t), first4, n4, dst, a.error, cm.flags);
+    return gather4c<(H / 4 + kT - 1) / kT>(s_hid(l - 1, t), first4, n4, dst, wt(), cm.flags);
   }
 
   // ---- QKV ------------------------------------------------------------------
@@ -1173,7 +1179,7 @@ struct Roles {
         // The group's queries, then this step's K and V rows (float4s).
         constexpr int q4 = GROUP * kHeadDim / 4, r4 = kHeadDim / 4;
         const int n4 = q4 + (has_new ? 2 * r4 : 0);
-        if (!gather4<(q4 + 2 * r4 + kT - 1) / kT>(in, n4, reinterpret_cast<float4 *>(ar.qs), a.error,
+        if (!gather4<(q4 + 2 * r4 + kT - 1) / kT>(in, n4, reinterpret_cast<float4 *>(ar.qs), wt(),
                                                   cm.flags, [&](int p, int &s, int &d) {
               if (p < q4) {
                 s = g * q4 + p;
@@ -1284,7 +1290,7 @@ struct Roles {
       const Slots in = s_part(l, t);
       const int n4 = NQ * C * kRec4;
       for (int base = 0; base < n4; base += kPer * kT) {
-        if (!gather4<kPer>(in, min(kPer * kT, n4 - base), reinterpret_cast<float4 *>(parts), a.error,
+        if (!gather4<kPer>(in, min(kPer * kT, n4 - base), reinterpret_cast<float4 *>(parts), wt(),
                            cm.flags, [&](int p, int &s, int &d) {
                              const int rec = (base + p) / kRec4, k = (base + p) % kRec4;
                              const int h = rec / C, c = rec % C;
@@ -1409,7 +1415,7 @@ struct Roles {
       const float4 g4 = threadIdx.x < H / 4
                             ? ld_global4(layer(l).mlp_norm, threadIdx.x)
                             : make_float4(0.f, 0.f, 0.f, 0.f);
-      if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), 0, H / 4, cm.vec, a.error, cm.flags)) return false;
+      if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), 0, H / 4, cm.vec, wt(), cm.flags)) return false;
       clock.lap(2 * kRoleGate);
       const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
       norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
@@ -1460,7 +1466,7 @@ struct Roles {
     loop(kRoleDown, true, [&](uint32_t t, int l, int position) {
       const Slots out = s_hid(l, t);
       if (om.q >= 0) clear_quad(s_hid(l, t + 1), om);
-      if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), hb4, hn4, cm.vec, a.error, cm.flags)) return false;
+      if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), hb4, hn4, cm.vec, wt(), cm.flags)) return false;
       // This wave's slice of the activation, straight into registers.
       float4 xa[DownRole<I>::kNsHi];
       bool ok = true;
@@ -1484,8 +1490,8 @@ struct Roles {
           }
           vm_wait();
           if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
-          if (spin > kSpinLimit) {
-            if (lane == 0) atomicOr(a.error, 1u);
+          if (spin > a.spin_limit) {
+            if (lane == 0) atomicOr(a.error, kResidentWaitGaveUp);
             ok = false;
           }
         }
@@ -1644,6 +1650,13 @@ hipError_t launch_roles(hipStream_t s, const ResidentArgs &args, int grid) {
   void *params[] = {const_cast<ResidentArgs *>(&args)};
   return hipLaunchCooperativeKernel(roles_fn(args.stage_ticks || args.trace), dim3(grid), dim3(kT),
                                     params, 0, s);
+}
+
+int device_cu_count(int device) {
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    return 0;
+  return cus;
 }
 
 int roles_max_grid(int device) {
