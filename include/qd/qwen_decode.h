@@ -186,11 +186,56 @@ QD_API qd_status qd_read_decode_state(qd_engine *engine, uint32_t seq,
                                       qd_decode_state *state);
 
 /* One decoder layer on a host hidden vector at the slot's current position
- * (writes K/V at that position, attends over 0..position). Does not advance
- * the position. Replaces DecoderLayer::decode_to_hidden_state
- * (examples/triton/mini_decoder_layer.hpp:345-372). */
+ * (writes K/V at that position, attends over 0..position), in place. Does
+ * not advance the position. The host round trip of copy_inputs + run +
+ * copy_output of one reference DecoderLayer (single-layer checks such as
+ * BASELINE config 1); the device-resident hand-off is qd_layer_decode. */
 QD_API qd_status qd_layer_step(qd_engine *engine, uint32_t seq,
                                uint32_t layer, float *hidden);
+
+/* ---- layer-by-layer decode (the reference executor surface) ----------------
+ * The slot's device hidden vector is the hand-off between these calls: it
+ * never travels through the host. A driver of the reference stack
+ * (benchmarks/triton_mini_decoder_layer.cpp:1051-1068) maps to
+ *   qd_embed_hidden (or qd_load_hidden), qd_layer_decode per layer (or one
+ *   call for the whole stack), qd_tail, qd_read_logits,
+ * and produces exactly qd_step's logits, token and K/V rows. */
+
+/* Host row -> the slot's device hidden vector (the next layer's input).
+ * Replaces DecoderLayer::copy_hidden_state
+ * (examples/triton/mini_decoder_layer.hpp:286-303). Synchronous. */
+QD_API qd_status qd_load_hidden(qd_engine *engine, uint32_t seq,
+                                const float *hidden);
+/* hidden = embeddings[token] on the device: the lookup the reference
+ * driver does on the host before copy_hidden_state
+ * (benchmarks/triton_mini_decoder_layer.cpp:1052-1054). Asynchronous. */
+QD_API qd_status qd_embed_hidden(qd_engine *engine, uint32_t seq,
+                                 uint32_t token);
+/* Decoder layers [first_layer, first_layer + layer_count) on the slot's
+ * device hidden vector for the query at position valid_keys - 1: each layer
+ * writes its K/V row there, attends over positions 0..valid_keys - 1 and
+ * leaves its output on the device as the next layer's input. Sets the
+ * slot's position to valid_keys - 1 (the token in flight; qd_tail
+ * completes it). Asynchronous: errors surface at the next synchronising
+ * call. Replaces DecoderLayer::decode_to_hidden_state / decode_to_buffer
+ * (examples/triton/mini_decoder_layer.hpp:345-372), whose valid_keys it
+ * takes. */
+QD_API qd_status qd_layer_decode(qd_engine *engine, uint32_t seq,
+                                 uint32_t first_layer, uint32_t layer_count,
+                                 uint32_t valid_keys);
+/* Final RMSNorm + LM head + argmax (lowest index on ties) on the slot's
+ * device hidden vector; advances the slot's position by one. logits_out
+ * (vocab floats), greedy_out and top_logit may be NULL; the logits also
+ * stay on the device for qd_read_logits. Replaces ModelTail::run
+ * (examples/triton/mini_decoder_layer.hpp:819-859) plus the host top_logits
+ * of benchmarks/triton_mini_decoder_layer.cpp:394-422. Synchronous. */
+QD_API qd_status qd_tail(qd_engine *engine, uint32_t seq, float *logits_out,
+                         uint32_t *greedy_out, float *top_logit);
+/* The slot's logits of its last qd_step / qd_tail / qd_prefill (`count`
+ * must equal vocab). Replaces ModelTail::copy_logits
+ * (examples/triton/mini_decoder_layer.hpp:866-871). */
+QD_API qd_status qd_read_logits(qd_engine *engine, uint32_t seq, float *out,
+                                size_t count);
 
 /* One full decode step of `token_in` at the slot's position: embedding, all
  * layers, final norm, LM head, argmax (lowest index on ties); advances the

@@ -1,14 +1,18 @@
 // qwen_decode.hpp -- header-only C++ wrappers over the C ABI in qwen_decode.h.
 //
-// They keep the method shapes of the reference's host classes so a driver
-// written against them ports call for call:
+// They keep the method shapes and semantics of the reference's host classes
+// so the reference's decode driver (benchmarks/triton_mini_decoder_layer.cpp:
+// 1051-1068) ports call for call:
 //   qd::DecoderLayer  ~ examples/triton/mini_decoder_layer.hpp:179-768
-//                       (decode_to_hidden_state, copy_inputs' KV half)
+//                       (copy_hidden_state, decode_to_hidden_state,
+//                       decode_to_buffer, copy_inputs' KV half)
 //   qd::ModelTail     ~ examples/triton/mini_decoder_layer.hpp:770-894
-//                       (run, copy_logits) + host top-1 of
-//                       benchmarks/triton_mini_decoder_layer.cpp:394-422
+//                       (hidden_buffer, run, copy_logits, copy_hidden) + the
+//                       host top-1 of benchmarks/triton_mini_decoder_layer.cpp:394-422
 //   qd::ResidentExecutor ~ include/lrrt/persistent_graph/resident_executor.hpp:268-475
 //                       (initialize, launch, read_state)
+// One difference: the layers of a sequence slot share one device hidden
+// vector, so a hand-off's destination position is the query's own.
 // Errors surface as qd::Error (a std::runtime_error carrying the status), the
 // way the reference's C++ layer throws lrrt::Error (include/lrrt/error.hpp:10-27).
 #pragma once
@@ -136,21 +140,72 @@ class Engine {
   std::unique_ptr<qd_engine, Destroy> engine_;
 };
 
-// One decoder layer of an engine, driven on a host hidden vector
-// (the reference's DecoderLayer::decode_to_hidden_state).
+class ModelTail;
+
+// The hidden vector a ModelTail reads (the reference's
+// ModelTail::hidden_buffer()): the slot's device hidden vector, which the
+// last layer's decode_to_buffer writes.
+struct HiddenBuffer {
+  Engine *engine;
+  uint32_t seq;
+};
+
+// One decoder layer of one sequence slot, with the reference DecoderLayer's
+// decode methods (examples/triton/mini_decoder_layer.hpp:286-372). The
+// engine keeps one hidden vector per slot on the device: each layer reads
+// it and leaves its output there for the next, so a hand-off never
+// touches the host, and `dst_position` must be the query position
+// valid_keys - 1 (the one row the slot holds).
 class DecoderLayer {
  public:
   DecoderLayer(Engine &engine, uint32_t layer, uint32_t seq = 0)
       : engine_(&engine), layer_(layer), seq_(seq) {}
+
+  uint32_t layer() const noexcept { return layer_; }
+  uint32_t seq() const noexcept { return seq_; }
 
   // KV half of DecoderLayer::copy_inputs: token-major [count][kv_heads*64].
   void copy_kv(uint32_t start, uint32_t count, const std::vector<float> &k,
                const std::vector<float> &v) {
     check(qd_write_kv(engine_->get(), seq_, layer_, start, count, k.data(), v.data()));
   }
-  // Runs the layer at the slot's position; hidden is updated in place.
-  void decode_to_hidden_state(std::vector<float> &hidden) {
-    check(qd_layer_step(engine_->get(), seq_, layer_, hidden.data()));
+  // DecoderLayer::copy_hidden_state: the input row of the token at
+  // `position` (the slot's one hidden row).
+  void copy_hidden_state(uint32_t position, const std::vector<float> &hidden_state) {
+    if (position >= engine_->config().capacity)
+      throw Error(QD_ERROR_INVALID_ARGUMENT, "hidden state position is out of range");
+    if (hidden_state.size() != engine_->config().hidden)
+      throw Error(QD_ERROR_INVALID_ARGUMENT, "hidden state row shape mismatch");
+    check(qd_load_hidden(engine_->get(), seq_, hidden_state.data()));
+  }
+  // The same row from the engine's embedding table, looked up on the device.
+  void embed_token(uint32_t position, uint32_t token) {
+    if (position >= engine_->config().capacity)
+      throw Error(QD_ERROR_INVALID_ARGUMENT, "hidden state position is out of range");
+    check(qd_embed_hidden(engine_->get(), seq_, token));
+  }
+  // Decodes the query at valid_keys - 1 (K/V row written there, attention
+  // over 0..valid_keys - 1) into dst's input on the device.
+  void decode_to_hidden_state(uint32_t valid_keys, DecoderLayer &dst, uint32_t dst_position) {
+    if (dst.engine_ != engine_ || dst.seq_ != seq_)
+      throw Error(QD_ERROR_INVALID_ARGUMENT,
+                  "direct handoff requires a layer of the same engine and sequence slot");
+    if (valid_keys == 0 || dst_position != valid_keys - 1)
+      throw Error(QD_ERROR_INVALID_ARGUMENT,
+                  "direct handoff position must be the query position valid_keys - 1");
+    check(qd_layer_decode(engine_->get(), seq_, layer_, 1, valid_keys));
+  }
+  // The same into the model tail's input (the last layer of a stack).
+  void decode_to_buffer(uint32_t valid_keys, const HiddenBuffer &dst) {
+    if (dst.engine != engine_ || dst.seq != seq_)
+      throw Error(QD_ERROR_INVALID_ARGUMENT,
+                  "direct output buffer must be the same engine and sequence slot's tail");
+    check(qd_layer_decode(engine_->get(), seq_, layer_, 1, valid_keys));
+  }
+  // The layer's output row (the slot's hidden vector) on the host.
+  void copy_output(std::vector<float> &hidden) const {
+    hidden.resize(engine_->config().hidden);
+    check(qd_read_activation(engine_->get(), seq_, 0, hidden.data(), hidden.size()));
   }
   void synchronize() { engine_->sync(); }
 
@@ -160,24 +215,36 @@ class DecoderLayer {
   uint32_t seq_;
 };
 
-// Final norm + LM head + top-1 for one sequence slot (ModelTail::run,
-// copy_logits and the host top-1 in one call per token).
+// Final RMSNorm + LM head + greedy top-1 of one sequence slot, with the
+// reference ModelTail's methods (examples/triton/mini_decoder_layer.hpp:
+// 770-894); run() takes no token: it reads the hidden vector the last
+// decoder layer left, and completes that token (the slot's position
+// advances by one).
 class ModelTail {
  public:
   explicit ModelTail(Engine &engine, uint32_t seq = 0) : engine_(&engine), seq_(seq) {}
 
-  // Consumes `token` through the whole model; keeps the logits.
-  uint32_t run(uint32_t token) {
-    return top_token_ = engine_->step(seq_, token, &logits_, &top_logit_);
+  HiddenBuffer hidden_buffer() const { return HiddenBuffer{engine_, seq_}; }
+  void run() { check(qd_tail(engine_->get(), seq_, nullptr, &top_token_, &top_logit_)); }
+  void synchronize() { engine_->sync(); }
+  void copy_logits(std::vector<float> &out) const {
+    if (out.size() != engine_->config().vocab)
+      throw Error(QD_ERROR_INVALID_ARGUMENT, "model tail logits shape mismatch");
+    check(qd_read_logits(engine_->get(), seq_, out.data(), out.size()));
   }
-  const std::vector<float> &copy_logits() const { return logits_; }
+  void copy_hidden(std::vector<float> &out) const {
+    if (out.size() != engine_->config().hidden)
+      throw Error(QD_ERROR_INVALID_ARGUMENT, "model tail hidden shape mismatch");
+    check(qd_read_activation(engine_->get(), seq_, 0, out.data(), out.size()));
+  }
+  // Greedy token and its logit of the last run() (the device argmax: the
+  // largest logit, the lowest index on ties).
   uint32_t top_token() const noexcept { return top_token_; }
   float top_logit() const noexcept { return top_logit_; }
 
  private:
   Engine *engine_;
   uint32_t seq_;
-  std::vector<float> logits_;
   uint32_t top_token_ = 0;
   float top_logit_ = 0.f;
 };

@@ -33,7 +33,7 @@
 
 namespace {
 
-constexpr uint32_t kAbiVersion = 2;
+constexpr uint32_t kAbiVersion = 3;
 constexpr int kLmHeadParts = 1024;  // LM-head workgroups = top-1 partials
 
 thread_local std::string g_error;
@@ -1098,6 +1098,88 @@ qd_status qd_layer_step(qd_engine *e, uint32_t seq, uint32_t layer, float *hidde
     e->upload(e->hidden + seq * e->H, hidden, e->H);
     check(qd::launch_layer(e->stream, e->layer_args(seq, layer)), "layer launch");
     check(hipMemcpyAsync(hidden, e->hidden + seq * e->H, e->H * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    e->sync();
+  });
+}
+
+qd_status qd_load_hidden(qd_engine *e, uint32_t seq, const float *hidden) {
+  return guard([&] {
+    if (!e || !hidden) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_seq(seq);
+    e->set_device();
+    e->upload(e->hidden + size_t(seq) * e->H, hidden, e->H);
+    e->sync();
+  });
+}
+
+qd_status qd_embed_hidden(qd_engine *e, uint32_t seq, uint32_t token) {
+  return guard([&] {
+    if (!e) fail(QD_ERROR_INVALID_ARGUMENT, "null engine");
+    e->check_seq(seq);
+    e->check_loaded();
+    if (token >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab %zu", token, e->V);
+    e->set_device();
+    // The embedding kernel reads the token from the slot state.
+    check(qd::launch_set_state(e->stream, e->states + seq, e->positions[seq], token), "state launch");
+    check(qd::launch_embed(e->stream, e->embed, e->states + seq, e->hidden + size_t(seq) * e->H,
+                           static_cast<int>(e->H), static_cast<int>(e->V)),
+          "embed launch");
+  });
+}
+
+qd_status qd_layer_decode(qd_engine *e, uint32_t seq, uint32_t first_layer, uint32_t layer_count,
+                          uint32_t valid_keys) {
+  return guard([&] {
+    if (!e) fail(QD_ERROR_INVALID_ARGUMENT, "null engine");
+    e->check_seq(seq);
+    e->check_loaded();
+    if (layer_count == 0 || first_layer >= e->L || layer_count > e->L - first_layer)
+      fail(QD_ERROR_INVALID_ARGUMENT, "layers [%u, %u) outside [0, %zu)", first_layer,
+           first_layer + layer_count, e->L);
+    if (valid_keys == 0 || valid_keys > e->CAP)
+      fail(QD_ERROR_INVALID_ARGUMENT, "valid_keys %u outside [1, capacity %zu]", valid_keys, e->CAP);
+    e->set_device();
+    // The query sits at position valid_keys - 1: the slot's position while
+    // this token is in flight (qd_tail completes it).
+    e->positions[seq] = valid_keys - 1;
+    check(qd::launch_set_state(e->stream, e->states + seq, valid_keys - 1, 0), "state launch");
+    for (uint32_t l = first_layer; l < first_layer + layer_count; ++l)
+      check(qd::launch_layer(e->stream, e->layer_args(seq, l)), "layer launch");
+  });
+}
+
+qd_status qd_tail(qd_engine *e, uint32_t seq, float *logits_out, uint32_t *greedy, float *top_logit) {
+  return guard([&] {
+    if (!e) fail(QD_ERROR_INVALID_ARGUMENT, "null engine");
+    e->check_seq(seq);
+    e->check_loaded();
+    if (e->positions[seq] >= e->CAP)
+      fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full (capacity %zu)", seq, e->CAP);
+    e->set_device();
+    // A fresh step-mode state at the slot's position (a layer_decode call
+    // left this; a qd_step or prefill left the position after its token).
+    check(qd::launch_set_state(e->stream, e->states + seq, e->positions[seq], 0), "state launch");
+    float *dev_logits = e->logits + size_t(seq) * e->V;
+    check(qd::launch_tail(e->stream, e->tail_args(seq, dev_logits, 0, nullptr)), "tail launch");
+    check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState),
+                         hipMemcpyDeviceToHost, e->stream), "D2H");
+    if (logits_out)
+      check(hipMemcpyAsync(logits_out, dev_logits, e->V * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    e->sync();
+    e->positions[seq] += 1;
+    if (greedy) *greedy = e->h_states[seq].token;
+    if (top_logit) *top_logit = e->h_states[seq].top_logit;
+  });
+}
+
+qd_status qd_read_logits(qd_engine *e, uint32_t seq, float *out, size_t count) {
+  return guard([&] {
+    if (!e || !out) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_seq(seq);
+    if (count != e->V) fail(QD_ERROR_INVALID_ARGUMENT, "logits have %zu elements, caller asked %zu", e->V, count);
+    e->set_device();
+    check(hipMemcpyAsync(out, e->logits + size_t(seq) * e->V, e->V * 4, hipMemcpyDeviceToHost, e->stream),
+          "D2H");
     e->sync();
   });
 }

@@ -328,6 +328,18 @@ __global__ __launch_bounds__(kBlock) void argmax_finalize_kernel(
   }
 }
 
+// Writes a slot's decode state for a step-mode token at `position` from
+// kernel arguments (no host buffer stays referenced after the launch).
+__global__ void set_state_kernel(SeqState *__restrict__ st, uint32_t position, uint32_t token) {
+  if (threadIdx.x != 0) return;
+  SeqState s{};
+  s.position = position;
+  s.token = token;
+  s.eos = UINT32_MAX;
+  s.mode = kModeStep;
+  *st = s;
+}
+
 // Every NaN of x[0, n) becomes the canonical quiet NaN 0x7FC00000, so no
 // loaded value (nor any result derived from it: arithmetic propagates a NaN
 // operand's payload) can equal the resident kernel's empty-slot pattern.
@@ -356,6 +368,11 @@ __global__ void canonical_nan_kernel(float *__restrict__ x, size_t n) {
 }  // namespace
 
 // ---- host launchers -----------------------------------------------------------
+
+hipError_t launch_set_state(hipStream_t s, SeqState *st, uint32_t position, uint32_t token) {
+  set_state_kernel<<<1, kWave, 0, s>>>(st, position, token);
+  return hipGetLastError();
+}
 
 hipError_t launch_canonical_nan(hipStream_t s, float *x, size_t n) {
   if (n == 0) return hipSuccess;

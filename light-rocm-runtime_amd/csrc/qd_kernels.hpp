@@ -72,6 +72,8 @@ hipError_t launch_embed(hipStream_t s, const float *emb, const SeqState *st,
                         Marker *m = nullptr);
 hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m = nullptr);
 hipError_t launch_tail(hipStream_t s, const TailLaunch &p, Marker *m = nullptr);
+// Sets a slot's state to a step-mode token at `position` (device side).
+hipError_t launch_set_state(hipStream_t s, SeqState *st, uint32_t position, uint32_t token);
 // Rewrites every NaN of x[0, n) (x 16-byte aligned) as 0x7FC00000.
 hipError_t launch_canonical_nan(hipStream_t s, float *x, size_t n);
 

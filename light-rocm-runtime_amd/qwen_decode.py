@@ -84,6 +84,11 @@ _SIGNATURES = {
     "qd_read_decode_state": (C.c_int, [_E, C.c_uint32, C.POINTER(DecodeState)]),
     "qd_read_activation": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F, C.c_size_t]),
     "qd_layer_step": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F]),
+    "qd_load_hidden": (C.c_int, [_E, C.c_uint32, _F]),
+    "qd_embed_hidden": (C.c_int, [_E, C.c_uint32, C.c_uint32]),
+    "qd_layer_decode": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
+    "qd_tail": (C.c_int, [_E, C.c_uint32, _F, _U, _F]),
+    "qd_read_logits": (C.c_int, [_E, C.c_uint32, _F, C.c_size_t]),
     "qd_step": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F, _U, _F]),
     "qd_prefill": (C.c_int, [_E, C.c_uint32, _U, C.c_uint32, _F, _U, _F]),
     "qd_step_batch": (C.c_int, [_E, C.c_uint32, _U, _U, _F, _U]),
@@ -259,6 +264,29 @@ class Engine:
         h = np.array(hidden, np.float32, copy=True)
         _check(lib().qd_layer_step(self.handle, seq, layer, _f(h)))
         return h
+
+    def load_hidden(self, seq: int, hidden: np.ndarray):
+        h = np.ascontiguousarray(hidden, np.float32)
+        assert h.size == self.config.hidden
+        _check(lib().qd_load_hidden(self.handle, seq, _f(h)))
+
+    def embed_hidden(self, seq: int, token: int):
+        _check(lib().qd_embed_hidden(self.handle, seq, token))
+
+    def layer_decode(self, seq: int, first_layer: int, layer_count: int, valid_keys: int):
+        _check(lib().qd_layer_decode(self.handle, seq, first_layer, layer_count, valid_keys))
+
+    def tail(self, seq: int, want_logits: bool = True):
+        logits = np.empty(self.config.vocab, np.float32) if want_logits else None
+        tok = C.c_uint32()
+        top = C.c_float()
+        _check(lib().qd_tail(self.handle, seq, _f(logits), C.byref(tok), C.byref(top)))
+        return int(tok.value), float(top.value), logits
+
+    def read_logits(self, seq: int) -> np.ndarray:
+        out = np.empty(self.config.vocab, np.float32)
+        _check(lib().qd_read_logits(self.handle, seq, _f(out), out.size))
+        return out
 
     def step(self, seq: int, token: int, want_logits: bool = True):
         logits = np.empty(self.config.vocab, np.float32) if want_logits else None

@@ -294,6 +294,44 @@ def test_resident_multi_window_beyond_4096_matches_stream_and_oracle(full, strea
     long_context_generation(full, stream_full, 4090, 40, 777, "resident 4091..4130 (two windows)")
 
 
+def test_layer_by_layer_decode_equals_step(full):
+    """The reference driver's per-token loop through the C ABI
+    (benchmarks/triton_mini_decoder_layer.cpp:1051-1068): the embedding row
+    into the slot's hidden, 24 device hand-offs (qd_layer_decode, one layer
+    per call: decode_to_hidden_state / decode_to_buffer), then qd_tail
+    (ModelTail::run) gives qd_step's token, logits and K/V rows bit for bit;
+    so does one call for the whole stack after a host-side embedding row."""
+    eng, _ = full
+    prompt = qo.fill_tokens(7, 1, PROMPT_STREAM + 6, FULL.vocab)
+    say("layer-by-layer decode vs qd_step, 4 tokens")
+    for slot in (0, 1):
+        eng.kv_reset(slot, 0)
+        first, _, _ = eng.prefill(slot, prompt, want_logits=False)
+    emb = eng.read_weight(0, qd.EMBED, FULL.vocab * FULL.hidden).reshape(FULL.vocab, FULL.hidden)
+    feed = first
+    for i in range(4):
+        pos = len(prompt) + i
+        tok, top, logits = eng.step(0, feed)
+        if i % 2 == 0:
+            eng.embed_hidden(1, feed)
+            for layer in range(FULL.layers):
+                eng.layer_decode(1, layer, 1, pos + 1)
+        else:
+            eng.load_hidden(1, emb[feed])
+            eng.layer_decode(1, 0, FULL.layers, pos + 1)
+        tok2, top2, logits2 = eng.tail(1)
+        assert tok2 == tok and top2 == top, i
+        assert np.array_equal(logits2, logits), i
+        assert np.array_equal(eng.read_logits(1), logits), i
+        assert eng.decode_state(1).token_position == pos + 1
+        feed = tok
+    assert_kv_equal(eng, eng, 0, 1, len(prompt), 4, "layer-by-layer KV")
+    # The slot continues with the fused path from where the layers left it.
+    a, _, la = eng.step(0, feed)
+    b, _, lb = eng.step(1, feed)
+    assert a == b and np.array_equal(la, lb)
+
+
 def test_generate_stops_at_eos(full):
     eng, _ = full
     prompt = qo.fill_tokens(5, 1, PROMPT_STREAM + 2, FULL.vocab)

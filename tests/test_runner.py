@@ -39,7 +39,17 @@ def test_help_exits_zero():
     (("--weights-dir", "/nonexistent", "--prompt-token-ids", "1"), "--weights-dir requires --layers"),
     (("--synthetic-seed", "1", "--prompt-token-ids", "1,,2"), "empty entry"),
     (("--synthetic-seed", "x", "--prompt-token-ids", "1"), "non-negative integer"),
-    (("--synthetic-seed", "1", "--prompt-token-ids", "1", "--max-new-tokens", "0"), "must be positive"),
+    (("--synthetic-seed", "1", "--prompt-token-ids", "1", "--no-model-tail"),
+     "--prompt-token-ids requires model tail"),
+    (("--synthetic-seed", "1", "--no-model-tail", "--e2e-check"), "--e2e-check requires model tail"),
+    (("--synthetic-seed", "1", "--prompt-token-ids", "1,2", "--valid-keys", "3"),
+     "valid key count must match prompt token count"),
+    (("--synthetic-seed", "1", "--prompt-token-ids", "1", "--max-new-tokens", "2", "--layer-sweep"),
+     "mutually exclusive"),
+    (("--synthetic-seed", "1", "--prompt-token-ids", "1", "--no-warmup", "--warmup-iterations", "2"),
+     "mutually exclusive"),
+    (("--weights", "layer_0/weights.json"), "--weights (one layer manifest"),
+    (("--synthetic-seed", "1", "--prompt-token-ids", "1", "3", "4"), "unknown option 4"),
     (("--synthetic-seed", "1", "--prompt-token-ids", "1,2,3", "--max-new-tokens", "4", "--keys", "2"),
      "--keys must cover"),
     (("--bogus",), "unknown option --bogus"),
@@ -48,6 +58,61 @@ def test_argument_errors(args, needle):
     r = run(*args)
     assert r.returncode == 2, r.stderr
     assert needle in r.stderr
+
+
+def reference_benchmark_argv(benchmark, bundle_dir, iterations, layers, valid_keys=None,
+                             no_warmup=False, no_model_tail=False, e2e_check=False,
+                             token_ids="", max_new_tokens=0, sync_stack=False, layer_sweep=False,
+                             trace_setup=False, trace_run=False):
+    """The argv tools/run_qwen_benchmark.py:115-149 (benchmark_command) builds,
+    restated flag for flag in its order."""
+    command = [str(benchmark), str(iterations), "--weights-dir", str(bundle_dir), "--layers", str(layers)]
+    if valid_keys is not None:
+        command.extend(["--valid-keys", str(valid_keys)])
+    if no_warmup:
+        command.append("--no-warmup")
+    if no_model_tail:
+        command.append("--no-model-tail")
+    if e2e_check:
+        command.append("--e2e-check")
+    if max_new_tokens > 0:
+        command.extend(["--prompt-token-ids", token_ids, "--max-new-tokens", str(max_new_tokens)])
+    if sync_stack:
+        command.append("--sync-stack")
+    if layer_sweep:
+        command.append("--layer-sweep")
+    if trace_setup:
+        command.append("--trace-setup")
+    if trace_run:
+        command.append("--trace-run")
+    return command
+
+
+# The combinations the reference's wrappers produce: the e2e runner's
+# (tools/run_qwen_e2e.py:667-693: valid keys = prompt length, --no-warmup,
+# --e2e-check, --sync-stack) and the benchmark wrapper's other switches.
+WRAPPER_ARGVS = [
+    dict(iterations=1, layers=2, valid_keys=4, no_warmup=True, e2e_check=True, token_ids="5,17,400,9",
+         max_new_tokens=6, sync_stack=True),
+    dict(iterations=3, layers=2, valid_keys=4, no_warmup=True, e2e_check=True, token_ids="5,17,400,9",
+         max_new_tokens=6, sync_stack=True, trace_setup=True, trace_run=True),
+    dict(iterations=2, layers=2, no_model_tail=True, layer_sweep=True),
+    dict(iterations=2, layers=2, token_ids="5,17", max_new_tokens=3),
+]
+
+
+@needs_runner
+@pytest.mark.parametrize("kw", WRAPPER_ARGVS)
+def test_reference_wrapper_argv_parses(kw, tmp_path):
+    """Every argv the reference wrapper builds gets past argument parsing: on
+    a host without a GPU the runner then stops at engine creation (exit 3),
+    never at an unknown or rejected option (exit 2)."""
+    if qd.device_count() > 0:
+        pytest.skip("a GPU is visible: covered by the GPU runner tests")
+    argv = reference_benchmark_argv(RUNNER, tmp_path, **kw)
+    r = subprocess.run(argv, capture_output=True, text=True, timeout=60)
+    assert r.returncode == 3, r.stderr
+    assert "no HIP device" in r.stderr
 
 
 @needs_runner
@@ -65,7 +130,7 @@ def test_stdout_contract_matches_engine(resident):
     print(f"[gpu-case] qd_run 2 layers vocab 4096 resident={resident}", flush=True)
     prompt = [5, 17, 400, 9]
     n = 6
-    args = ["--synthetic-seed", 3, "--layers", 2, "--vocab", 4096,
+    args = ["2", "--synthetic-seed", 3, "--layers", 2, "--vocab", 4096,
             "--prompt-token-ids", ",".join(map(str, prompt)), "--max-new-tokens", n, "--e2e-check"]
     if resident:
         args.append("--resident")
@@ -105,3 +170,51 @@ def test_eos_stops_runner():
         got = [int(x) for x in GENERATED_TOKEN_IDS_RE.search(r.stdout).group(1).split(",")]
         assert got == ids[:stop + 1], flags
         assert STOP_REASON_RE.search(r.stdout).group(1) == "eos_token"
+
+
+@needs_runner
+@pytest.mark.gpu
+def test_reference_wrapper_argv_runs_layer_by_layer(tmp_path):
+    """The e2e wrapper's argv (--sync-stack: the reference's layer-by-layer
+    decode with a synchronisation per layer) on a converted bundle gives the
+    same tokens as the fused step path, and the other wrapper switches run."""
+    print("[gpu-case] qd_run reference wrapper argv on a bundle", flush=True)
+    with qd.Engine(layers=2, vocab=4096, capacity=64, max_batch=1) as eng:
+        eng.load_synthetic(3)
+        write_bundle(eng, tmp_path, layers=2, vocab=4096)
+    prompt = "5,17,400,9"
+    sync = subprocess.run(reference_benchmark_argv(RUNNER, tmp_path, **WRAPPER_ARGVS[1]),
+                          capture_output=True, text=True, timeout=300)
+    assert sync.returncode == 0, sync.stderr
+    assert "layer-by-layer" in sync.stdout and "trace setup" in sync.stderr
+    fused = run("--weights-dir", tmp_path, "--layers", 2, "--prompt-token-ids", prompt,
+                "--max-new-tokens", 6, "--no-warmup", "1")
+    assert fused.returncode == 0, fused.stderr
+    ids = GENERATED_TOKEN_IDS_RE.search(sync.stdout).group(1)
+    assert ids == GENERATED_TOKEN_IDS_RE.search(fused.stdout).group(1)
+    assert TOP_LOGIT_RE.findall(sync.stdout) == TOP_LOGIT_RE.findall(fused.stdout)
+    sweep = subprocess.run(reference_benchmark_argv(RUNNER, tmp_path, **WRAPPER_ARGVS[2]),
+                           capture_output=True, text=True, timeout=300)
+    assert sweep.returncode == 0, sweep.stderr
+    assert re.findall(r"layer_sweep layers=(\d+)", sweep.stdout) == ["1", "2"]
+    prof = run("--weights-dir", tmp_path, "--layers", 2, "--prompt-token-ids", "5,17", "--max-new-tokens", 2,
+               "--gpu-stage-profile", "--cpu-submit-profile", "1")
+    assert prof.returncode == 0, prof.stderr
+    assert "kernel=gateup_silu_kernel" in prof.stdout and "cpu_submit" in prof.stdout
+
+
+def write_bundle(eng, directory, layers, vocab):
+    """The engine's resident weights as a reference bundle directory."""
+    kinds = [(896,), (896,), (896 * 896,), (128 * 896,), (128 * 896,), (896,), (128,), (128,),
+             (896 * 896,), (4864 * 896,), (4864 * 896,), (896 * 4864,)]
+    for layer in range(layers):
+        d = os.path.join(directory, f"layer_{layer}")
+        os.makedirs(d)
+        tensors = np.concatenate([eng.read_weight(layer, k, n[0]) for k, n in enumerate(kinds)])
+        qd.bundle_write_layer(os.path.join(d, "weights.json"), "weights.bin", [64, 896, 14, 2, 64, 4864],
+                              1e6, tensors)
+    d = os.path.join(directory, "model_tail")
+    os.makedirs(d)
+    emb = eng.read_weight(0, qd.EMBED, vocab * 896)
+    qd.bundle_write_tail(os.path.join(d, "weights.json"), "weights.bin", 896, vocab, np.arange(vocab), emb,
+                         eng.read_weight(0, qd.FINAL_NORM, 896), emb)
