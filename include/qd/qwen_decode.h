@@ -262,6 +262,21 @@ QD_API qd_status qd_step_batch(qd_engine *engine, uint32_t n_seq,
                                const uint32_t *seq_ids, const uint32_t *tokens,
                                float *logits, uint32_t *greedy);
 
+/* qd_step_batch for one group of 1..16 sequences that allocates nothing:
+ * no hipMalloc, hipFree or other allocating call, on its first call or
+ * later. Its scratch (activation rows, attention records, split-K partials,
+ * arrival counters, LM-head partials: 2.25 MiB) is a static device array of
+ * the library, one per GPU, whose address the engine looks up when it is
+ * created. Results equal qd_step_batch's bit for bit. Calls that overlap on
+ * one GPU (two engines, or two host threads) share that array and race.
+ * More than 16 sequences: QD_ERROR_INVALID_ARGUMENT. No counterpart in the
+ * reference; it is for callers that cannot allocate (code under graph
+ * capture, allocation-free serving loops). */
+QD_API qd_status qd_step_batch_noalloc(qd_engine *engine, uint32_t n_seq,
+                                       const uint32_t *seq_ids,
+                                       const uint32_t *tokens, float *logits,
+                                       uint32_t *greedy);
+
 /* Device-resident greedy generation: consumes first_token, then feeds each
  * argmax back on the device until max_tokens tokens were produced or eos
  * was produced; one host synchronisation at the end. Mirrors the resident

@@ -23,6 +23,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 
 #include "qd_attention.hpp"
 #include "qd_batch.hpp"
@@ -719,7 +720,83 @@ struct Scope {
   }
 };
 
+__global__ void clear_counters_kernel(uint32_t *__restrict__ counters, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) counters[i] = 0u;
+}
+
+// The static batch workspace: one copy per GPU the library runs on. Host
+// code never passes this name to a kernel (on the host it is a stand-in,
+// not a device address); it uses the per-device address batch_scratch()
+// obtains from hipGetSymbolAddress.
+__device__ __align__(256) static unsigned char scratch[kBatchScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxScratchDevices] = {};
+
+size_t round256(size_t bytes) { return (bytes + 255) / 256 * 256; }
+
 }  // namespace
+
+size_t batch_workspace_bytes(int nq) {
+  const size_t r = kBatchRows, qd = size_t(nq) * kHeadDim;
+  return round256(r * kH * 4) + 2 * round256(r * qd * 4) + round256(r * kI * 4) +
+         round256(r * nq * kAttnMaxChunks * kPartStride * 4) + round256(size_t(kBatchSplitFloats) * 4) +
+         round256(size_t(kBatchCounters) * 4) + 2 * round256(r * kBatchLmParts * 4) + 2 * round256(r * 4);
+}
+
+BatchWorkspace carve_batch_workspace(void *base, int nq) {
+  unsigned char *p = static_cast<unsigned char *>(base);
+  auto take = [&](size_t bytes) {
+    void *r = p;
+    p += round256(bytes);
+    return r;
+  };
+  const size_t r = kBatchRows, qd = size_t(nq) * kHeadDim;
+  BatchWorkspace w{};
+  w.hidden = static_cast<float *>(take(r * kH * 4));
+  w.q = static_cast<float *>(take(r * qd * 4));
+  w.attn = static_cast<float *>(take(r * qd * 4));
+  w.act = static_cast<float *>(take(r * kI * 4));
+  w.part = static_cast<float *>(take(r * nq * kAttnMaxChunks * kPartStride * 4));
+  w.split = static_cast<float *>(take(size_t(kBatchSplitFloats) * 4));
+  w.counters = static_cast<uint32_t *>(take(size_t(kBatchCounters) * 4));
+  w.part_val = static_cast<float *>(take(r * kBatchLmParts * 4));
+  w.part_idx = static_cast<uint32_t *>(take(r * kBatchLmParts * 4));
+  w.out_token = static_cast<uint32_t *>(take(r * 4));
+  w.out_top = static_cast<float *>(take(r * 4));
+  return w;
+}
+
+static_assert(kH / kHeadDim == 14, "the batched kernels take 14 query heads");
+
+void *batch_scratch(int device, hipError_t *err) {
+  *err = hipSuccess;
+  if (device < 0 || device >= kMaxScratchDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  if (batch_workspace_bytes(kH / kHeadDim) > kBatchScratchBytes) {
+    *err = hipErrorInvalidValue;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+      return nullptr;
+    }
+    g_scratch_ptr[device] = p;
+  }
+  return g_scratch_ptr[device];
+}
+
+hipError_t launch_batch_clear_counters(hipStream_t s, uint32_t *counters) {
+  clear_counters_kernel<<<(kBatchCounters + kBlock - 1) / kBlock, kBlock, 0, s>>>(counters, kBatchCounters);
+  return hipGetLastError();
+}
 
 const char *batch_kernel_name(int id) {
   static const char *const names[kBatchKernelCount] = {

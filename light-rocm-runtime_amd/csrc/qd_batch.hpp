@@ -60,6 +60,37 @@ struct BatchTail {
   int vocab;
 };
 
+// The scratch of one batched group: every buffer of BatchLaunch and
+// BatchTail that is neither an input nor an output of the step. Carved in
+// this order from one block, each region 256-byte aligned.
+struct BatchWorkspace {
+  float *hidden;        // [kBatchRows][896]
+  float *q;             // [kBatchRows][nq * 64]
+  float *attn;          // [kBatchRows][nq * 64]
+  float *act;           // [kBatchRows][4864]
+  float *part;          // [kBatchRows][nq][kAttnMaxChunks][kPartStride]
+  float *split;         // [kBatchSplitFloats]
+  uint32_t *counters;   // [kBatchCounters], zero before a step
+  float *part_val;      // [kBatchRows][kBatchLmParts]
+  uint32_t *part_idx;   // [kBatchRows][kBatchLmParts]
+  uint32_t *out_token;  // [kBatchRows]
+  float *out_top;       // [kBatchRows]
+};
+// Bytes a BatchWorkspace for nq query heads takes; carves one from `base`
+// (256-byte aligned, at least that many bytes).
+size_t batch_workspace_bytes(int nq);
+BatchWorkspace carve_batch_workspace(void *base, int nq);
+
+// The library's static batch workspace (a file-scope device array of
+// kBatchScratchBytes, one copy per GPU, held until the process ends): its
+// address on `device`, looked up once per device with hipGetSymbolAddress
+// while that device is current. nullptr (and *err set) on failure.
+constexpr size_t kBatchScratchBytes = size_t(9) << 18;  // 2.25 MiB
+void *batch_scratch(int device, hipError_t *err);
+// Zeroes a workspace's arrival counters with a fill kernel (a step expects
+// them zero; a step that stopped early can leave them set).
+hipError_t launch_batch_clear_counters(hipStream_t s, uint32_t *counters);
+
 // Kernels of the batched step, for per-kernel event timing.
 enum BatchKernelId : int {
   kBEmbed = 0,

@@ -147,6 +147,10 @@ struct qd_engine {
         *bt_part = nullptr, *bt_split = nullptr, *bt_val = nullptr, *bt_top = nullptr;
   uint32_t *bt_idx = nullptr, *bt_counters = nullptr, *bt_token = nullptr;
   uint32_t *h_bt_out = nullptr;  // pinned [max_batch] tokens then [max_batch] top logits
+  // The library's static batch workspace on this engine's device
+  // (qd_step_batch_noalloc), looked up at creation; null if the lookup failed.
+  void *batch_scratch = nullptr;
+  std::string batch_scratch_error;
 
   qd::SeqState *h_states = nullptr;  // pinned [max_batch]
   uint32_t *h_tokens = nullptr;      // pinned [capacity]
@@ -790,6 +794,11 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
       e->roles_slots = e->alloc<float>(e->roles_slot_bytes / 4);
     }
     e->resident_error = e->alloc<uint32_t>(1);
+    {
+      hipError_t err = hipSuccess;
+      e->batch_scratch = qd::batch_scratch(c.device, &err);
+      if (!e->batch_scratch) e->batch_scratch_error = hipGetErrorString(err);
+    }
     e->sync();
     *out = e.release();
   });
@@ -1386,6 +1395,80 @@ qd_status qd_step_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, c
       e->positions[seq_ids[i]] += 1;
       if (greedy) greedy[i] = e->h_bt_out[i];
     }
+  });
+}
+
+qd_status qd_step_batch_noalloc(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids,
+                                const uint32_t *tokens, float *logits, uint32_t *greedy) {
+  return guard([&] {
+    if (!e || !seq_ids || !tokens) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    e->check_loaded();
+    if (n_seq == 0 || n_seq > uint32_t(qd::kBatchRows))
+      fail(QD_ERROR_INVALID_ARGUMENT,
+           "qd_step_batch_noalloc takes 1..%d sequences (its static workspace holds one group), got %u",
+           qd::kBatchRows, n_seq);
+    if (n_seq > e->B) fail(QD_ERROR_INVALID_ARGUMENT, "n_seq %u exceeds max_batch %zu", n_seq, e->B);
+    for (uint32_t i = 0; i < n_seq; ++i) {
+      e->check_seq(seq_ids[i]);
+      for (uint32_t j = 0; j < i; ++j)
+        if (seq_ids[j] == seq_ids[i]) fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u listed twice", seq_ids[i]);
+      if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u >= vocab", tokens[i]);
+      if (size_t(e->positions[seq_ids[i]]) + 1 > e->CAP)
+        fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full", seq_ids[i]);
+    }
+    if (!e->batch_scratch)
+      fail(QD_ERROR_NOT_SUPPORTED, "static batch workspace unavailable: %s", e->batch_scratch_error.c_str());
+    e->set_device();
+    // Every buffer but the step's inputs and outputs (weights, KV cache,
+    // slot states, the logits rows) lives in the static workspace.
+    const qd::BatchWorkspace w = qd::carve_batch_workspace(e->batch_scratch, int(e->NQ));
+    qd::BatchLaunch b{};
+    b.rows = static_cast<int>(n_seq);
+    for (uint32_t i = 0; i < n_seq; ++i) {
+      b.slot[i] = seq_ids[i];
+      b.pos[i] = e->positions[seq_ids[i]];
+      b.token[i] = tokens[i];
+    }
+    b.states = e->states;
+    b.hidden = w.hidden;
+    b.q = w.q;
+    b.attn = w.attn;
+    b.act = w.act;
+    b.part = w.part;
+    b.split = w.split;
+    b.counters = w.counters;
+    b.k_cache = e->k_cache;
+    b.v_cache = e->v_cache;
+    b.rope_cos = e->rope_cos;
+    b.rope_sin = e->rope_sin;
+    b.layers = static_cast<int>(e->L);
+    b.capacity = static_cast<int>(e->CAP);
+    b.nq = static_cast<int>(e->NQ);
+    b.nkv = static_cast<int>(e->NKV);
+    b.eps = e->cfg.rms_eps;
+    qd::BatchTail t{};
+    t.final_norm = e->final_norm;
+    t.head = e->lm_head;
+    t.logits = e->logits;
+    t.part_val = w.part_val;
+    t.part_idx = w.part_idx;
+    t.out_token = w.out_token;
+    t.out_top = w.out_top;
+    t.vocab = static_cast<int>(e->V);
+    // The workspace keeps the last call's contents: the arrival counters
+    // start at zero (a fill kernel, no memset node).
+    check(qd::launch_batch_clear_counters(e->stream, w.counters), "counter clear");
+    check(qd::launch_batch_embed(e->stream, b, e->embed, static_cast<int>(e->V)), "batch embed launch");
+    for (size_t l = 0; l < e->L; ++l)
+      check(qd::launch_batch_layer(e->stream, b, e->layers[l], static_cast<int>(l)), "batch layer launch");
+    check(qd::launch_batch_tail(e->stream, b, t), "batch tail launch");
+    if (greedy)
+      check(hipMemcpyAsync(greedy, w.out_token, n_seq * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
+    if (logits)
+      check(hipMemcpyAsync(logits, e->logits, size_t(n_seq) * e->V * 4, hipMemcpyDeviceToHost, e->stream),
+            "D2H");
+    e->sync();
+    for (uint32_t i = 0; i < n_seq; ++i) e->positions[seq_ids[i]] += 1;
   });
 }
 

@@ -92,6 +92,7 @@ _SIGNATURES = {
     "qd_step": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F, _U, _F]),
     "qd_prefill": (C.c_int, [_E, C.c_uint32, _U, C.c_uint32, _F, _U, _F]),
     "qd_step_batch": (C.c_int, [_E, C.c_uint32, _U, _U, _F, _U]),
+    "qd_step_batch_noalloc": (C.c_int, [_E, C.c_uint32, _U, _U, _F, _U]),
     "qd_generate_resident": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                        _U, _U, _U, _F]),
     "qd_last_timing": (C.c_int, [_E, C.POINTER(Timing)]),
@@ -309,6 +310,16 @@ class Engine:
         logits = np.empty((s.size, self.config.vocab), np.float32) if want_logits else None
         greedy = np.empty(s.size, np.uint32)
         _check(lib().qd_step_batch(self.handle, s.size, _u(s), _u(t), _f(logits), _u(greedy)))
+        return greedy, logits
+
+    def step_batch_noalloc(self, seq_ids, tokens, want_logits: bool = True):
+        """qd_step_batch_noalloc: one group of up to 16 sequences, scratch in
+        the library's static device workspace."""
+        s = np.ascontiguousarray(seq_ids, np.uint32)
+        t = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.empty((s.size, self.config.vocab), np.float32) if want_logits else None
+        greedy = np.empty(s.size, np.uint32)
+        _check(lib().qd_step_batch_noalloc(self.handle, s.size, _u(s), _u(t), _f(logits), _u(greedy)))
         return greedy, logits
 
     def generate(self, seq: int, first_token: int, max_tokens: int, eos: int = NO_EOS,
