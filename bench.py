@@ -158,66 +158,142 @@ CONFIG3_TEXT = ("BASELINE config 3: 24-layer Qwen2.5-0.5B-shape FP32 decoder + t
                 "argmax feedback")
 
 
-def run_decode(K, W, no_cpu):
-    return decode_line(K, W, no_cpu, PROMPT, CONFIG2_TEXT, RESIDENT_TRAFFIC_PER_TOKEN)
+def run_decode(K, W, no_cpu, trials):
+    return decode_line(K, W, no_cpu, trials, PROMPT, CONFIG2_TEXT, RESIDENT_TRAFFIC_PER_TOKEN)
 
 
-def run_long(K, W, no_cpu):
-    return decode_line(K, W, no_cpu, LONG_PROMPT, CONFIG3_TEXT, RESIDENT_TRAFFIC_PER_TOKEN_LONG)
+def run_long(K, W, no_cpu, trials):
+    return decode_line(K, W, no_cpu, trials, LONG_PROMPT, CONFIG3_TEXT, RESIDENT_TRAFFIC_PER_TOKEN_LONG)
 
 
-def decode_line(K, W, no_cpu, prompt_len, workload, traffic_per_token):
-    capacity = prompt_len + max(K, W) + 8
+def host_info():
+    """The host the CPU baseline ran on: CPU model, logical CPUs, the CPUs this
+    process may use, and the OpenMP thread setting."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"cpu_model": model, "nproc": os.cpu_count(), "usable_cpus": usable,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def trial_orders(paths):
+    """Rotations of the path list, forwards then backwards: trial t runs the
+    paths in order t mod 2n (benchmarks/qwen_stateful_graph.cpp:247-261)."""
+    n = len(paths)
+    orders = [[(off + i) % n for i in range(n)] for off in range(n)]
+    orders += [[(off + n - i) % n for i in range(n)] for off in range(n)]
+    return [[paths[i] for i in o] for o in orders]
+
+
+def spread(samples):
+    v = sorted(samples)
+    mid = len(v) // 2
+    med = v[mid] if len(v) % 2 else 0.5 * (v[mid - 1] + v[mid])
+    return {"median": med, "min": v[0], "max": v[-1]}
+
+
+def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token):
+    capacity = prompt_len + max(K, W) + 24
     log("engine create + synthetic weights")
     eng = qd.Engine(capacity=capacity, max_batch=1)
     eng.load_synthetic(SEED)
     prompt = stream_tokens(prompt_len, SEED, PROMPT_STREAM, VOCAB)
     log(f"prefill {prompt_len}")
     first, _, _ = eng.prefill(0, prompt, want_logits=False)
+    grid = eng.resident_grid()
 
+    # Two decode paths over the same K tokens, interleaved over trials:
+    # "resident" (qd_generate_resident: one launch, argmax fed back on the
+    # device) and "step" (qd_step per token with the logits copied to the
+    # host: the reference executor surface's per-token contract).
+    def resident():
+        toks, reason, _ = eng.generate(0, first, K)
+        assert len(toks) == K, (len(toks), reason)
+        return toks.tolist(), eng.last_timing().total_us
+
+    def step():
+        out, tok = [], first
+        for _ in range(K):
+            tok, _, _ = eng.step(0, tok, want_logits=True)
+            out.append(tok)
+        return out, None
+
+    paths = {"resident": resident, "step": step}
     if W:
-        log(f"warmup {W}")
+        log(f"warmup {W} tokens per path")
         eng.generate(0, first, W)
         eng.kv_reset(0, prompt_len)
-
-    log(f"timed {K} decode steps")
-    eng.sync()
-    t0 = time.perf_counter()
-    toks, reason, _ = eng.generate(0, first, K)
-    eng.sync()
-    wall = time.perf_counter() - t0
-    timing = eng.last_timing()
-    assert len(toks) == K, (len(toks), reason)
-    dev_s = timing.total_us * 1e-6
-    tok_s = K / wall
+        tok = first
+        for _ in range(W):
+            tok, _, _ = eng.step(0, tok, want_logits=True)
+    samples = {name: {"wall_ms": [], "device_us": []} for name in paths}
+    tokens = {}
+    log(f"timed: {trials} interleaved trials x {K} tokens per path")
+    for t in range(trials):
+        for name in trial_orders(list(paths))[t % (2 * len(paths))]:
+            eng.kv_reset(0, prompt_len)
+            eng.sync()
+            t0 = time.perf_counter()
+            toks, dev_us = paths[name]()
+            eng.sync()
+            samples[name]["wall_ms"].append((time.perf_counter() - t0) * 1e3)
+            if dev_us is not None:
+                samples[name]["device_us"].append(dev_us)
+            tokens.setdefault(name, toks)
+            assert toks == tokens[name], f"{name}: trial {t} produced other tokens"
+    # The two paths run the same arithmetic: the same greedy chain.
+    assert tokens["resident"] == tokens["step"], "resident and step paths disagree"
+    res_wall = spread(samples["resident"]["wall_ms"])
+    step_wall = spread(samples["step"]["wall_ms"])
     total_bytes = sum(step_bytes(prompt_len + 1 + i) for i in range(K))
-    step_gbs = total_bytes / dev_s / 1e9
+    tok_s = K / (res_wall["median"] * 1e-3)
 
-    grid = eng.resident_grid()
     if grid:
         # One resident launch runs all K tokens: its HIP-event duration on the
         # engine stream is the kernel time, its algorithmic bytes the K steps'.
+        dev = spread(samples["resident"]["device_us"])
         traffic = traffic_per_token * K if traffic_per_token else None
-        roof = roofline_hbm("roles_kernel", timing.total_us, float(total_bytes), traffic)
+        roof = roofline_hbm("roles_kernel", dev["median"], float(total_bytes), traffic)
+        roof["avg_us_min"] = round(dev["min"], 3)
+        roof["avg_us_max"] = round(dev["max"], 3)
     else:
         eng.kv_reset(0, prompt_len)
         prof = eng.profile_kernels(0, first, min(K, 16))
         name, (_, avg_us, avg_bytes, _) = dominant(prof)
         roof = roofline_hbm(name, avg_us, avg_bytes)
-        log("kernel profile: " + ", ".join(f"{n}={v[1]:.1f}us" for n, v in prof.items()))
+    # The step path's kernels, each timed with HIP events.
+    eng.kv_reset(0, prompt_len)
+    prof = eng.profile_kernels(0, first, min(K, 16))
+    log("step-path kernel profile: " + ", ".join(f"{n}={v[1]:.1f}us" for n, v in prof.items()))
+    dname, (_, davg_us, davg_bytes, _) = dominant(prof)
+    log("HBM probe")
+    read_gbs, copy_gbs = qd.probe_hbm(0, 1 << 31, 5)
     eng.close()
+    roof["frac_of_measured_read"] = round(roof["achieved"] / read_gbs, 4) if read_gbs else None
 
     cpu = None
     if not no_cpu:
         steps, el, cores = cpu_decode_baseline(SEED, [prompt_len])
         cpu = {"value": round(steps / el, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
                "sample": f"{steps} decode steps at context {prompt_len + 1}..{prompt_len + steps}, "
-                         f"24 layers + 151936-row LM head, oracle/libqwen_oracle.so FP32 OpenMP"}
+                         f"24 layers + 151936-row LM head, oracle/libqwen_oracle.so FP32 OpenMP "
+                         f"({cores} threads)",
+               "host": host_info()}
     return {
         "metric": METRIC,
         "value": round(tok_s, 2),
         "unit": "tokens/s",
-        "ms_per_step": round(wall * 1e3 / K, 4),
+        "ms_per_step": round(res_wall["median"] / K, 4),
         "higher_is_better": True,
         "dtype": "f32",
         "data": "synthetic: random-init N(0,0.02) weights / N(0,0.01) biases, seed 1; "
@@ -227,11 +303,21 @@ def decode_line(K, W, no_cpu, prompt_len, workload, traffic_per_token):
             "batch": 1, "context": f"{prompt_len + 1}..{prompt_len + K}", "layers": 24,
             "hidden": 896, "vocab": VOCAB,
         },
-        "step_hbm": {"achieved_gbs": round(step_gbs, 1), "peak_gbs": HBM_PEAK_GBS,
-                     "frac": round(step_gbs / HBM_PEAK_GBS, 4),
-                     "bytes_per_token": round(total_bytes / K)},
-        "device_tokens_per_s": round(K / dev_s, 2),
+        "trials": {"count": trials, "order": "interleaved rotations, forwards then backwards",
+                   "resident_ms": {k: round(v, 3) for k, v in res_wall.items()},
+                   "step_ms": {k: round(v, 3) for k, v in step_wall.items()}},
+        "step_hbm": {"achieved_gbs": round(total_bytes / (res_wall["median"] * 1e-3) / 1e9, 1),
+                     "peak_gbs": HBM_PEAK_GBS, "bytes_per_token": round(total_bytes / K)},
+        "device_tokens_per_s": round(K / (roof["avg_us"] * 1e-6), 2) if grid else None,
         "roofline": roof,
+        "hbm_measured": {"read_gbs": round(read_gbs, 1), "copy_gbs": round(copy_gbs, 1),
+                         "probe": "qd_probe_hbm: best of 5 passes over 2 GiB"},
+        "executor_surface": {
+            "path": "qd_step per token: stream-ordered kernels + 607,744-byte logits copy to the host",
+            "tokens_per_s": round(K / (step_wall["median"] * 1e-3), 2),
+            "ms_per_token": round(step_wall["median"] / K, 4),
+            "dominant_kernel": roofline_hbm(dname, davg_us, davg_bytes),
+        },
         "cpu_baseline": cpu,
         "path": f"resident megakernel, {grid} workgroups" if grid else "stream-ordered kernels",
     }
@@ -241,7 +327,7 @@ def batch_lengths():
     return [256 + int(x) for x in stream_tokens(BATCH_ROWS, BATCH_SEED, LEN_STREAM, 2048 - 256 + 1)]
 
 
-def run_batch16(K, W, no_cpu):
+def run_batch16(K, W, no_cpu, trials):
     lengths = batch_lengths()
     slots = list(range(BATCH_ROWS))
     log("engine create + synthetic weights (seed 3, 16 slots)")
@@ -318,7 +404,7 @@ def run_batch16(K, W, no_cpu):
     }
 
 
-def run_prefill(K, W, no_cpu):
+def run_prefill(K, W, no_cpu, trials):
     prompt = stream_tokens(PROMPT, PREFILL_SEED, PROMPT_STREAM, VOCAB)
     log("engine create + synthetic weights (seed 4)")
     eng = qd.Engine(capacity=PROMPT + PREFILL_DECODE + 8, max_batch=1)
@@ -416,6 +502,8 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--trials", type=int, default=7,
+                    help="interleaved timed trials of K steps (decode workloads); value is the median")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB (PMC calibration)")
     args = ap.parse_args()
@@ -429,7 +517,7 @@ def main():
         sys.exit("--steps must be positive")
     run = {"decode": run_decode, "long": run_long, "batch16": run_batch16,
            "prefill": run_prefill}[args.workload]
-    out = run(K, W, args.no_cpu)
+    out = run(K, W, args.no_cpu, max(1, args.trials))
     if args.copy_probe:
         copy_probe(args.copy_probe)
     line = {"metric": out.pop("metric"), "value": out.pop("value"), "unit": out.pop("unit"),

@@ -350,6 +350,15 @@ QD_API qd_status qd_trace_resident(qd_engine *engine, uint32_t seq,
                                    size_t capacity, uint32_t *workgroups,
                                    uint32_t *rows, uint32_t *stages);
 
+/* Measured HBM bandwidth of `device`: the best of `iters` timed passes
+ * (after one warm-up) of a streaming read and of a copy over `bytes`-byte
+ * buffers (temporary, freed before returning), in bytes moved per second /
+ * 1e9 (a copy moves 2 * bytes). The achievable peak the decode roofline is
+ * also reported against. The reference reports achieved bandwidth against
+ * its nominal peak (docs/stateful-graph.md:617-621). */
+QD_API qd_status qd_probe_hbm(int32_t device, uint64_t bytes, uint32_t iters,
+                              double *read_gbs, double *copy_gbs);
+
 /* Timing of the last qd_generate_resident call. */
 QD_API qd_status qd_last_timing(const qd_engine *engine, qd_timing *timing);
 

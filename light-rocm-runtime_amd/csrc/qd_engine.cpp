@@ -670,6 +670,21 @@ qd_status qd_device_count(uint32_t *count) {
   });
 }
 
+qd_status qd_probe_hbm(int32_t device, uint64_t bytes, uint32_t iters, double *read_gbs,
+                       double *copy_gbs) {
+  return guard([&] {
+    if (!read_gbs || !copy_gbs) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
+    if (bytes < (uint64_t(1) << 20) || iters == 0)
+      fail(QD_ERROR_INVALID_ARGUMENT, "probe needs at least 1 MiB and one iteration");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+      fail(QD_ERROR_NOT_SUPPORTED, "no HIP device visible");
+    if (device < 0 || device >= ndev) fail(QD_ERROR_INVALID_ARGUMENT, "device %d out of range", device);
+    check(hipSetDevice(device), "hipSetDevice");
+    check(qd::probe_hbm(device, size_t(bytes), iters, read_gbs, copy_gbs), "HBM probe");
+  });
+}
+
 qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
   return guard([&] {
     if (!config || !out) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");

@@ -365,9 +365,96 @@ __global__ void canonical_nan_kernel(float *__restrict__ x, size_t n) {
   if (tail < n && __builtin_isnan(x[tail])) x[tail] = __builtin_bit_cast(float, 0x7FC00000u);
 }
 
+// HBM bandwidth probe: workgroups stream chunks of kProbeDepth * 256
+// float4s (chunk c by workgroup c mod grid), every lane keeping kProbeDepth
+// non-temporal 16-byte loads in flight; the copy variant stores each float4
+// to `dst`, the read variant folds them into one value per workgroup.
+constexpr int kProbeDepth = 16;
+template <bool kCopy>
+__global__ __launch_bounds__(kBlock) void hbm_probe_kernel(const float4 *__restrict__ src,
+                                                           float4 *__restrict__ dst, size_t n4,
+                                                           float *__restrict__ sink) {
+  typedef float gf4 __attribute__((ext_vector_type(4)));
+  typedef const __attribute__((address_space(1))) gf4 cg4;
+  typedef __attribute__((address_space(1))) gf4 g4;
+  const size_t chunk = static_cast<size_t>(kProbeDepth) * kBlock;
+  float acc = 0.f;
+  for (size_t base = static_cast<size_t>(blockIdx.x) * chunk; base < n4;
+       base += static_cast<size_t>(gridDim.x) * chunk) {
+    gf4 v[kProbeDepth];
+#pragma unroll
+    for (int d = 0; d < kProbeDepth; ++d) {
+      const size_t i = base + static_cast<size_t>(d) * kBlock + threadIdx.x;
+      v[d] = i < n4 ? __builtin_nontemporal_load((cg4 *)(src + i)) : gf4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int d = 0; d < kProbeDepth; ++d) {
+      const size_t i = base + static_cast<size_t>(d) * kBlock + threadIdx.x;
+      if (kCopy) {
+        if (i < n4) __builtin_nontemporal_store(v[d], (g4 *)(dst + i));
+      } else {
+        acc += (v[d].x + v[d].y) + (v[d].z + v[d].w);
+      }
+    }
+  }
+  if (!kCopy && acc == 1.2345e30f) sink[blockIdx.x] = acc;  // keeps the loads
+}
+
 }  // namespace
 
 // ---- host launchers -----------------------------------------------------------
+
+hipError_t probe_hbm(int device, size_t bytes, uint32_t iters, double *read_gbs, double *copy_gbs) {
+  *read_gbs = *copy_gbs = 0.0;
+  int cus = 0;
+  hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+  if (e != hipSuccess) return e;
+  const size_t n4 = bytes / 16;
+  float4 *a = nullptr, *b = nullptr;
+  float *sink = nullptr;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  hipStream_t s = nullptr;
+  auto cleanup = [&] {
+    if (s) (void)hipStreamSynchronize(s);
+    if (t0) (void)hipEventDestroy(t0);
+    if (t1) (void)hipEventDestroy(t1);
+    if (s) (void)hipStreamDestroy(s);
+    if (a) (void)hipFree(a);
+    if (b) (void)hipFree(b);
+    if (sink) (void)hipFree(sink);
+  };
+  const unsigned grid = static_cast<unsigned>(std::max(cus, 1) * 8);
+  if ((e = hipMalloc(&a, n4 * 16)) != hipSuccess || (e = hipMalloc(&b, n4 * 16)) != hipSuccess ||
+      (e = hipMalloc(&sink, grid * sizeof(float))) != hipSuccess ||
+      (e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking)) != hipSuccess ||
+      (e = hipEventCreate(&t0)) != hipSuccess || (e = hipEventCreate(&t1)) != hipSuccess ||
+      (e = hipMemsetAsync(a, 0, n4 * 16, s)) != hipSuccess) {
+    cleanup();
+    return e;
+  }
+  for (int copy = 0; copy < 2; ++copy) {
+    double best = 0.0;
+    for (uint32_t it = 0; it < iters + 1; ++it) {  // the first run warms up
+      (void)hipEventRecord(t0, s);
+      if (copy)
+        hbm_probe_kernel<true><<<grid, kBlock, 0, s>>>(a, b, n4, sink);
+      else
+        hbm_probe_kernel<false><<<grid, kBlock, 0, s>>>(a, b, n4, sink);
+      (void)hipEventRecord(t1, s);
+      if ((e = hipStreamSynchronize(s)) != hipSuccess) {
+        cleanup();
+        return e;
+      }
+      float ms = 0.f;
+      (void)hipEventElapsedTime(&ms, t0, t1);
+      const double gbs = double(n4) * 16.0 * (copy ? 2.0 : 1.0) / (ms * 1e-3) / 1e9;
+      if (it > 0) best = std::max(best, gbs);
+    }
+    (copy ? *copy_gbs : *read_gbs) = best;
+  }
+  cleanup();
+  return hipGetLastError();
+}
 
 hipError_t launch_set_state(hipStream_t s, SeqState *st, uint32_t position, uint32_t token) {
   set_state_kernel<<<1, kWave, 0, s>>>(st, position, token);

@@ -72,6 +72,9 @@ hipError_t launch_embed(hipStream_t s, const float *emb, const SeqState *st,
                         Marker *m = nullptr);
 hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m = nullptr);
 hipError_t launch_tail(hipStream_t s, const TailLaunch &p, Marker *m = nullptr);
+// Best-of-`iters` streaming read and copy bandwidth (GB/s, bytes moved per
+// second) over a `bytes` buffer on `device` (current), with temporary buffers.
+hipError_t probe_hbm(int device, size_t bytes, uint32_t iters, double *read_gbs, double *copy_gbs);
 // Sets a slot's state to a step-mode token at `position` (device side).
 hipError_t launch_set_state(hipStream_t s, SeqState *st, uint32_t position, uint32_t token);
 // Rewrites every NaN of x[0, n) (x 16-byte aligned) as 0x7FC00000.

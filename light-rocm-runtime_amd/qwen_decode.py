@@ -107,6 +107,8 @@ _SIGNATURES = {
     "qd_trace_resident": (C.c_int, [_E, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                     C.POINTER(C.c_uint64), C.c_size_t, _U, _U, _U]),
     "qd_sync": (C.c_int, [_E]),
+    "qd_probe_hbm": (C.c_int, [C.c_int32, C.c_uint64, C.c_uint32, C.POINTER(C.c_double),
+                               C.POINTER(C.c_double)]),
     "qd_bundle_write_layer": (C.c_int, [C.c_char_p, C.c_char_p, _U, C.c_float, _F]),
     "qd_bundle_read_layer": (C.c_int, [C.c_char_p, _U, _F, _F, C.c_size_t, C.POINTER(C.c_size_t)]),
     "qd_bundle_write_tail": (C.c_int, [C.c_char_p, C.c_char_p, C.c_uint32, C.c_uint32, _U,
@@ -156,6 +158,13 @@ def device_count() -> int:
     n = C.c_uint32()
     _check(lib().qd_device_count(C.byref(n)))
     return int(n.value)
+
+
+def probe_hbm(device: int = 0, nbytes: int = 1 << 31, iters: int = 5):
+    """(read GB/s, copy GB/s): best-of-iters streaming read / copy bandwidth."""
+    r, c = C.c_double(), C.c_double()
+    _check(lib().qd_probe_hbm(device, nbytes, iters, C.byref(r), C.byref(c)))
+    return float(r.value), float(c.value)
 
 
 def status_string(status: int) -> str:
