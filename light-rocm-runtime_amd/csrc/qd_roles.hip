@@ -1300,61 +1300,45 @@ struct Roles {
           return false;
       }
       clock.lap(2 * kRoleO);
-      // Merge, in the arithmetic of attn_merge, one wave per head: lane c
-      // holds chunk c's m and l and computes its weight w_c = e^(m_c - M)
-      // (M the head's largest m); the weights and l's go through a small
-      // per-wave LDS area (one wave's LDS accesses run in order) and lane d
-      // sums w_c acc_c[d] and w_c l_c in chunk order, then divides. A
-      // wave's two heads are computed side by side so their latency chains
-      // overlap. The code is specialised on C rounded up to 4 (kCm chunks,
-      // the extra terms discarded by a select); every read is an immediate
+      // Merge, in the arithmetic of attn_merge: wave w takes heads 2w and
+      // 2w + 1, one per half-wave, and lane d of a half computes dims d and
+      // d + 32 of its head: M = the largest of the C chunk maxima, then
+      // w_c = 2^(m_c - M) folded into the denominator and both numerators
+      // in chunk order, then one division per dim. Every lane of a half
+      // reads the same m_c and l_c (LDS broadcasts); no value crosses lanes.
+      // The code is specialised on C rounded up to 4 (kCm chunks, the terms
+      // past C skipped by a wave-uniform test); every read is an immediate
       // offset from the head's record base.
-      static_assert(kT % kHeadDim == 0 && kHeadDim == kWave && kAttnMaxChunks <= kWave &&
-                        kAttnMaxChunks % 4 == 0,
-                    "one wave per head");
-      constexpr int kHeadsPerWave = (NQ + kW - 1) / kW;
-      constexpr int kWl = 2 * kAttnMaxChunks;  // per head: w[16], l[16]
-      float *wl = cm.top + wv * kWl * kHeadsPerWave;
+      static_assert(kHeadDim == kWave && NQ <= 2 * kW && kAttnMaxChunks % 4 == 0,
+                    "two heads per wave");
       auto merge = [&](auto cm_tag) {
         constexpr int kCm = decltype(cm_tag)::value;
-        float mc[kHeadsPerWave], lc[kHeadsPerWave], av[kHeadsPerWave][kCm];
+        const int h = 2 * wv + (lane >> 5);
+        if (h >= NQ) return;
+        const int d = lane & 31;
+        const float *rec = parts + h * kAttnMaxChunks * kRoleRecStride;
+        float mv[kCm], lv[kCm];
 #pragma unroll
-        for (int j = 0; j < kHeadsPerWave; ++j) {
-          const int h = min(wv + j * kW, NQ - 1);
-          const float *rec = parts + h * kAttnMaxChunks * kRoleRecStride;
-          mc[j] = rec[min(lane, kAttnMaxChunks - 1) * kRoleRecStride];
-          lc[j] = rec[min(lane, kAttnMaxChunks - 1) * kRoleRecStride + 1];
-#pragma unroll
-          for (int c = 0; c < kCm; ++c) av[j][c] = rec[c * kRoleRecStride + 4 + lane];
+        for (int c = 0; c < kCm; ++c) {
+          const float2 ml = *reinterpret_cast<const float2 *>(rec + c * kRoleRecStride);
+          mv[c] = ml.x;
+          lv[c] = ml.y;
         }
+        float mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < kHeadsPerWave; ++j) {
-          const float mx = wave_max(lane < C ? mc[j] : -INFINITY);
-          const float w = expf(mc[j] - mx);
-          if (lane < kAttnMaxChunks) {
-            wl[j * kWl + lane] = w;
-            wl[j * kWl + kAttnMaxChunks + lane] = lc[j];
+        for (int c = 0; c < kCm; ++c) mx = c < C ? fmaxf(mx, mv[c]) : mx;
+        float num0 = 0.f, num1 = 0.f, den = 0.f;
+#pragma unroll
+        for (int c = 0; c < kCm; ++c) {
+          if (c < C) {
+            const float w = exp2_fast(mv[c] - mx);
+            den = fmaf(w, lv[c], den);
+            num0 = fmaf(w, rec[c * kRoleRecStride + 4 + d], num0);
+            num1 = fmaf(w, rec[c * kRoleRecStride + 4 + d + 32], num1);
           }
         }
-#pragma unroll
-        for (int j = 0; j < kHeadsPerWave; ++j) {
-          const int h = wv + j * kW;
-          const float4 *w4 = reinterpret_cast<const float4 *>(wl + j * kWl);
-          float wv4[kCm], lv4[kCm];
-#pragma unroll
-          for (int c4 = 0; c4 < kCm / 4; ++c4) {
-            const float4 x = w4[c4], y = w4[kAttnMaxChunks / 4 + c4];
-            wv4[4 * c4] = x.x; wv4[4 * c4 + 1] = x.y; wv4[4 * c4 + 2] = x.z; wv4[4 * c4 + 3] = x.w;
-            lv4[4 * c4] = y.x; lv4[4 * c4 + 1] = y.y; lv4[4 * c4 + 2] = y.z; lv4[4 * c4 + 3] = y.w;
-          }
-          float num = 0.f, dsum = 0.f;
-#pragma unroll
-          for (int c = 0; c < kCm; ++c) {
-            dsum = c < C ? fmaf(wv4[c], lv4[c], dsum) : dsum;
-            num = c < C ? fmaf(wv4[c], av[j][c], num) : num;
-          }
-          if (h < NQ) cm.xn[h * kHeadDim + lane] = num / dsum;
-        }
+        cm.xn[h * kHeadDim + d] = num0 / den;
+        cm.xn[h * kHeadDim + d + 32] = num1 / den;
       };
       switch ((C + 3) / 4) {
         case 1: merge(std::integral_constant<int, 4>{}); break;
