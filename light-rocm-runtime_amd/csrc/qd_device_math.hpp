@@ -67,6 +67,10 @@ __device__ __forceinline__ float fma4(float4 w, float4 x, float acc) {
   return acc;
 }
 
+// SwiGLU of one intermediate row: silu(g) * u with silu(g) = g / (1 + e^-g)
+// (benchmarks/qwen_stateful_graph_kernel.cpp:512).
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
+
 // Greater value wins; equal values go to the lower index; NaN never wins
 // (benchmarks/qwen_stateful_graph_kernel.cpp:225-229).
 __device__ __forceinline__ bool better(float v, uint32_t i, float bv,
@@ -200,29 +204,46 @@ template <int K>
 __device__ __forceinline__ void load_pair_gain(const float *gain,
                                                float4 (&gv)[PairSlots<K>::NJ]) {
   constexpr int K4 = PairSlots<K>::K4;
-  const float4 *g4 = reinterpret_cast<const float4 *>(gain);
+  const global_f32x4 *g4 = (const global_f32x4 *)gain;
   const int lane = lane_id();
 #pragma unroll
   for (int j = 0; j < PairSlots<K>::NJ; ++j) {
     const int f = j * kWave + lane;
     const int c = f < K4 ? f : f - K4;
-    gv[j] = f < 2 * K4 ? g4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const gf32x4 v = f < 2 * K4 ? g4[c] : gf32x4{0.f, 0.f, 0.f, 0.f};
+    gv[j] = make_float4(v.x, v.y, v.z, v.w);
   }
 }
 
-// xv[j] = x[c] * inv * gain[c]: the RMSNorm output in the slot layout.
+// RMSNorm folded past the GEMV: W . (x * inv * g) = inv * (W . (x * g)).
+// Loads the operand as xv[j] = x[c] * gain[c] in the slot layout and
+// returns the sum of squares of x, taken per lane over the slots of the
+// first row (every element of x once) in slot order and then wave-reduced;
+// every wave that loads the same x gets the same bits. The dots of the
+// operand are scaled by norm_scale(ss, K, eps) afterwards, so no
+// workgroup-wide reduction sits between the arrival of x and the dots.
 template <int K, typename Src>
-__device__ __forceinline__ void load_pair_operand_norm(
-    const Src &x, float inv, const float4 (&gv)[PairSlots<K>::NJ],
-    float4 (&xv)[PairSlots<K>::NJ]) {
+__device__ __forceinline__ float load_pair_operand_gain(const Src &x,
+                                                        const float4 (&gv)[PairSlots<K>::NJ],
+                                                        float4 (&xv)[PairSlots<K>::NJ]) {
+  constexpr int K4 = PairSlots<K>::K4;
   load_pair_operand<K>(x, xv);
+  const int lane = lane_id();
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < PairSlots<K>::NJ; ++j)
+    if (j * kWave < K4 && j * kWave + lane < K4) ss = fma4(xv[j], xv[j], ss);
 #pragma unroll
   for (int j = 0; j < PairSlots<K>::NJ; ++j) {
-    xv[j].x = xv[j].x * inv * gv[j].x;
-    xv[j].y = xv[j].y * inv * gv[j].y;
-    xv[j].z = xv[j].z * inv * gv[j].z;
-    xv[j].w = xv[j].w * inv * gv[j].w;
+    xv[j].x *= gv[j].x;
+    xv[j].y *= gv[j].y;
+    xv[j].z *= gv[j].z;
+    xv[j].w *= gv[j].w;
   }
+  return wave_sum(ss);
+}
+__device__ __forceinline__ float norm_scale(float ss, int k, float eps) {
+  return rsqrtf(ss / static_cast<float>(k) + eps);
 }
 
 // Weight slots of a row pair, loaded into registers (separable from the
@@ -316,22 +337,6 @@ __device__ __forceinline__ void pair_dot_lds(const float4 (&w)[PairSlots<K>::NJ]
   }
   sa = wave_sum(accA);
   sb = wave_sum(accB);
-}
-
-// y[c] = x[c] * inv * gain[c] for c < N (float4 c4 = thread index, loaded
-// ahead into g), written by the whole workgroup; the caller synchronises.
-template <int N>
-__device__ __forceinline__ void norm_to_lds(const float *x, float inv, float4 g, float *y) {
-  const int c4 = threadIdx.x;
-  if (c4 < N / 4) {
-    const float4 v = reinterpret_cast<const float4 *>(x)[c4];
-    float4 o;
-    o.x = v.x * inv * g.x;
-    o.y = v.y * inv * g.y;
-    o.z = v.z * inv * g.z;
-    o.w = v.w * inv * g.w;
-    reinterpret_cast<float4 *>(y)[c4] = o;
-  }
 }
 
 // Single-row dot for K a multiple of 256 floats: lane l loads float4 slots

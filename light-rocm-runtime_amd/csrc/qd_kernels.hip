@@ -55,13 +55,11 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
     const SeqState *__restrict__ st, float *__restrict__ q,
     float *__restrict__ k_cache, float *__restrict__ v_cache, int nq, int nkv,
     float eps, int capacity) {
-  __shared__ float red[kWavesPerBlock];
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
   float4 gv[PairSlots<H>::NJ];
   load_pair_gain<H>(gain, gv);
-  const float inv = block_inv_rms<H>(Plain(hidden), eps, red);
   float4 xv[PairSlots<H>::NJ];
-  load_pair_operand_norm<H>(Plain(hidden), inv, gv, xv);
+  const float inv = norm_scale(load_pair_operand_gain<H>(Plain(hidden), gv, xv), H, eps);
   const int position = static_cast<int>(st->position);
   const int kv_dim = nkv * kHeadDim;
   const int units = (nq + 2 * nkv) * kRotary;
@@ -75,8 +73,8 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
     dot_pair<H>(wqkv + static_cast<size_t>(ra) * H,
                 wqkv + static_cast<size_t>(rb) * H, xv, sa, sb);
     if (lane_id() == 0) {
-      const float a = sa + bqkv[ra];
-      const float b = sb + bqkv[rb];
+      const float a = fmaf(sa, inv, bqkv[ra]);
+      const float b = fmaf(sb, inv, bqkv[rb]);
       if (head < nq + nkv) {
         const float c = rope_cos[position * kRotary + i];
         const float s = rope_sin[position * kRotary + i];
@@ -181,19 +179,17 @@ __global__ __launch_bounds__(kBlock) void gateup_silu_kernel(
     const float *__restrict__ wg, const float *__restrict__ wu,
     const SeqState *__restrict__ st, float *__restrict__ act, int inter,
     float eps) {
-  __shared__ float red[kWavesPerBlock];
   if (st->stopped) return;
   float4 gv[PairSlots<H>::NJ];
   load_pair_gain<H>(gain, gv);
-  const float inv = block_inv_rms<H>(Plain(hidden), eps, red);
   float4 xv[PairSlots<H>::NJ];
-  load_pair_operand_norm<H>(Plain(hidden), inv, gv, xv);
+  const float inv = norm_scale(load_pair_operand_gain<H>(Plain(hidden), gv, xv), H, eps);
   for (int r = blockIdx.x * kWavesPerBlock + wave_id(); r < inter;
        r += gridDim.x * kWavesPerBlock) {
-    float g, up;
+    float gs, us;
     dot_pair<H>(wg + static_cast<size_t>(r) * H,
-                wu + static_cast<size_t>(r) * H, xv, g, up);
-    if (lane_id() == 0) act[r] = g / (1.f + expf(-g)) * up;
+                wu + static_cast<size_t>(r) * H, xv, gs, us);
+    if (lane_id() == 0) act[r] = silu_mul(gs * inv, us * inv);
   }
 }
 
@@ -221,15 +217,13 @@ __global__ __launch_bounds__(kBlock) void lmhead_kernel(
     const float *__restrict__ head, const SeqState *__restrict__ st,
     float *__restrict__ logits, int history, int vocab, float eps,
     float *__restrict__ part_val, uint32_t *__restrict__ part_idx) {
-  __shared__ float red[kWavesPerBlock];
   __shared__ float bv[kWavesPerBlock];
   __shared__ uint32_t bi[kWavesPerBlock];
   if (st->stopped) return;
   float4 gv[PairSlots<H>::NJ];
   load_pair_gain<H>(gain, gv);
-  const float inv = block_inv_rms<H>(Plain(hidden), eps, red);
   float4 xv[PairSlots<H>::NJ];
-  load_pair_operand_norm<H>(Plain(hidden), inv, gv, xv);
+  const float inv = norm_scale(load_pair_operand_gain<H>(Plain(hidden), gv, xv), H, eps);
   float *out = logits + (history ? static_cast<size_t>(st->generated) * vocab : 0);
   float best = -INFINITY;
   uint32_t best_i = UINT32_MAX;
@@ -241,6 +235,8 @@ __global__ __launch_bounds__(kBlock) void lmhead_kernel(
     const float *a = head + static_cast<size_t>(r0) * H;
     float sa, sb;
     dot_pair<H>(a, has1 ? a + H : a, xv, sa, sb);
+    sa *= inv;
+    sb *= inv;
     if (lane_id() == 0) {
       out[r0] = sa;
       if (has1) out[r0 + 1] = sb;

@@ -159,8 +159,9 @@ __global__ __launch_bounds__(kBlock) void embed_rows_kernel(const float *__restr
   for (int c = threadIdx.x; c < hidden / 4; c += kBlock) dst[c] = src[c];
 }
 
-// Same arithmetic as the decode kernels' RMSNorm (block_inv_rms, then
-// x * inv * gain).
+// RMSNorm of one prompt row: x * inv * gain with inv from block_inv_rms.
+// (The decode kernels fold the norm past their GEMVs instead, inv * (W .
+// (x * gain)); the two agree to rounding.)
 template <int H>
 __global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float *__restrict__ x,
                                                               const float *__restrict__ gain,

@@ -658,30 +658,6 @@ struct DownRole {
   }
 };
 
-// 1/rms of x[0..N) over the workgroup: the arithmetic of block_inv_rms
-// (per-thread float4 sums, wave sums, then the wave totals in order; the
-// extra waves add zeros) with the barrier above and the thread count known.
-template <int N>
-__device__ float inv_rms(const float *x, float eps, float *red) {
-  const float4 *x4 = reinterpret_cast<const float4 *>(x);
-  float s = 0.f;
-  for (int c = threadIdx.x; c < N / 4; c += kT) {
-    const float4 v = x4[c];
-    s = fmaf(v.x, v.x, s);
-    s = fmaf(v.y, v.y, s);
-    s = fmaf(v.z, v.z, s);
-    s = fmaf(v.w, v.w, s);
-  }
-  s = wave_sum(s);
-  if (lane_id() == 0) red[wave_u()] = s;
-  lds_barrier();
-  float t = 0.f;
-#pragma unroll
-  for (int w = 0; w < kW; ++w) t += red[w];
-  lds_barrier();
-  return rsqrtf(t / static_cast<float>(N) + eps);
-}
-
 // Balanced split of `total` items over `parts`: part r gets [begin, end).
 __device__ __forceinline__ int split_begin(int total, int parts, int r) {
   return static_cast<int>((static_cast<int64_t>(total) * r) / parts);
@@ -872,24 +848,23 @@ struct Roles {
       }
     };
     float4 w0[NJ], w1[NJ], w2[NJ];
-    const float4 g4 = threadIdx.x < H / 4 ? ld_global4(a.final_norm, threadIdx.x)
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 gv[NJ];
+    load_pair_gain<H>(a.final_norm, gv);
     load(gw, w0);
     __builtin_amdgcn_sched_barrier(0);
     if (!gather4c<(H / 4 + kT - 1) / kT>(s_hid(a.layers - 1, t), 0, H / 4, cm.vec, wt(), cm.flags))
       return false;
     clock.lap(2 * kRoleCount);
-    const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
-    norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
-    lds_barrier();
     float4 xv[NJ];
-    load_pair_operand<H>(Lds{cm.xn}, xv);
+    const float inv = norm_scale(load_pair_operand_gain<H>(Lds{cm.vec}, gv, xv), H, a.eps);
     float best = -INFINITY;
     uint32_t best_i = UINT32_MAX;
     float *logits = a.logits + (a.history ? static_cast<size_t>(t) * a.vocab : 0);
     auto step = [&](int u, const float4 (&w)[NJ]) {
       float sa, sb;
       pair_dot<H>(w, xv, sa, sb);
+      sa *= inv;
+      sb *= inv;
       const int r0 = 2 * u;
       const bool has1 = r0 + 1 < a.vocab;
       if (lane == 0) {
@@ -1052,16 +1027,13 @@ struct Roles {
       const LayerPtrs lw = layer(l);
       const Slots out = s_qkv(l, t);
       if (om.q >= 0) clear_quad(s_qkv(l, t + 1), om);
-      const float4 g4 = threadIdx.x < H / 4 ? ld_global4(lw.attn_norm, threadIdx.x)
-                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 gv[NJ];
+      load_pair_gain<H>(lw.attn_norm, gv);
       if (!layer_input(t, l, 0, H / 4, cm.vec)) return false;
       clock.lap(2 * kRoleQkv);
-      const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
-      norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
-      lds_barrier();
-      clock.mark(0);
       float4 xv[NJ];
-      load_pair_operand<H>(Lds{cm.xn}, xv);
+      const float inv = norm_scale(load_pair_operand_gain<H>(Lds{cm.vec}, gv, xv), H, a.eps);
+      clock.mark(0);
       const float *bias = reinterpret_cast<const float *>(q_bias);
       const float *cs = reinterpret_cast<const float *>(q_cs);
       const Coherent kcache(kv_layer(a.k_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
@@ -1075,8 +1047,8 @@ struct Roles {
         const int u = u0 + k;
         const int head = u / kRotary;
         const int slot = head * kHeadDim + u % kRotary - sbase;
-        const float x0 = sa + c.x;
-        const float x1 = sb + c.y;
+        const float x0 = fmaf(sa, inv, c.x);
+        const float x1 = fmaf(sb, inv, c.y);
         if (head < NQ + NKV) {
           const float cv = c.z, sv = c.w;
           stage[slot] = x0 * cv - x1 * sv;
@@ -1396,20 +1368,16 @@ struct Roles {
       const Slots out = s_act(l, t);
       if (om.q >= 0) clear_quad(s_act(l, t + 1), om);
       float *stage = cm.top;  // unit u0 + k at stage[k + (u0 & 3)]
-      const float4 g4 = threadIdx.x < H / 4
-                            ? ld_global4(layer(l).mlp_norm, threadIdx.x)
-                            : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 gv[NJ];
+      load_pair_gain<H>(layer(l).mlp_norm, gv);
       if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), 0, H / 4, cm.vec, wt(), cm.flags)) return false;
       clock.lap(2 * kRoleGate);
-      const float inv = inv_rms<H>(cm.vec, a.eps, cm.red);
-      norm_to_lds<H>(cm.vec, inv, g4, cm.xn);
-      lds_barrier();
       float4 xv[NJ];
-      load_pair_operand<H>(Lds{cm.xn}, xv);
+      const float inv = norm_scale(load_pair_operand_gain<H>(Lds{cm.vec}, gv, xv), H, a.eps);
       clock.mark(0);
       rg.compute(xv, [](int) { return make_float4(0.f, 0.f, 0.f, 0.f); },
-                 [&](int k, float gt, float up, float4) {
-                   stage[k + (u0 & 3)] = gt / (1.f + expf(-gt)) * up;
+                 [&](int k, float gs, float us, float4) {
+                   stage[k + (u0 & 3)] = silu_mul(gs * inv, us * inv);
                  },
                  [&] { clock.mark(1); });
       lds_barrier();
