@@ -44,6 +44,61 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (read_lane(v, 0) + read_lane(v, 16)) + (read_lane(v, 32) + read_lane(v, 48));
 }
 
+// Value of lane l ^ 4 (kX = 4) or l ^ 8 (kX = 8) inside each row of 16: two
+// bank-masked row shifts (a bank is a quarter row). The row shifts only
+// ever read lanes of the same row.
+template <int kX>
+__device__ __forceinline__ float dpp_row_xor(float v) {
+  static_assert(kX == 4 || kX == 8, "row xor");
+  constexpr int kShr = 0x110 + kX, kShl = 0x100 + kX;
+  constexpr int kHiBanks = kX == 4 ? 0xA : 0xC, kLoBanks = kX == 4 ? 0x5 : 0x3;
+  const int x = __builtin_bit_cast(int, v);
+  int t = __builtin_amdgcn_update_dpp(x, x, kShr, 0xf, kHiBanks, false);
+  t = __builtin_amdgcn_update_dpp(t, x, kShl, 0xf, kLoBanks, false);
+  return __builtin_bit_cast(float, t);
+}
+
+// One halving step of wave_sum_multi: pairs of values (2i, 2i + 1); the lane
+// whose bit is set keeps the odd one, its partner the even one, and each
+// adds the partner's copy of the value it keeps.
+template <int N, typename Ex>
+__device__ __forceinline__ void wave_sum_halve(float (&v)[16], bool bit, Ex ex) {
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float keep = bit ? v[2 * i + 1] : v[2 * i];
+    const float send = bit ? v[2 * i] : v[2 * i + 1];
+    v[i] = keep + ex(send);
+  }
+}
+
+// Wave sums of N values at once (N a power of two, at most 16). The lanes
+// are grouped exactly as wave_sum groups them (pairs, quads, octets, rows of
+// 16, then (row 0 + row 1) + (row 2 + row 3)) and addition is commutative,
+// so each sum is bit-identical to wave_sum of that value; the exchanges are
+// shared between the values (about 4 instructions per value instead of
+// about 15). Value k ends in lanes k, k + 16, k + 32 and k + 48 (lane l
+// holds value l mod N).
+template <int N>
+__device__ __forceinline__ float wave_sum_multi(const float (&in)[N]) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "power of two up to 16");
+  const int lane = lane_id();
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = in[i];
+  auto x1 = [](float y) { return dpp<kDppXor1>(y); };
+  auto x2 = [](float y) { return dpp<kDppXor2>(y); };
+  auto x4 = [](float y) { return dpp_row_xor<4>(y); };
+  auto x8 = [](float y) { return dpp_row_xor<8>(y); };
+  if constexpr (N >= 2) wave_sum_halve<N>(v, lane & 1, x1); else v[0] += x1(v[0]);
+  if constexpr (N >= 4) wave_sum_halve<N / 2>(v, lane & 2, x2); else v[0] += x2(v[0]);
+  if constexpr (N >= 8) wave_sum_halve<N / 4>(v, lane & 4, x4); else v[0] += x4(v[0]);
+  if constexpr (N >= 16) wave_sum_halve<N / 8>(v, lane & 8, x8); else v[0] += x8(v[0]);
+  float r = v[0];
+  r += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 16) << 2, __builtin_bit_cast(int, r)));
+  r += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, r)));
+  return r;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<kDppXor1>(v));
   v = fmaxf(v, dpp<kDppXor2>(v));
@@ -269,15 +324,16 @@ __device__ __forceinline__ void load_pair_weights(
   }
 }
 
-// Wave-reduced dot products (every lane gets both sums).
+// Per-lane partial dots of a row pair (the terms pair_dot wave-reduces).
 template <int K>
-__device__ __forceinline__ void pair_dot(const float4 (&w)[PairSlots<K>::NJ],
-                                         const float4 (&xv)[PairSlots<K>::NJ],
-                                         float &sa, float &sb) {
+__device__ __forceinline__ void pair_partial(const float4 (&w)[PairSlots<K>::NJ],
+                                             const float4 (&xv)[PairSlots<K>::NJ],
+                                             float &accA, float &accB) {
   constexpr int K4 = PairSlots<K>::K4;
   constexpr int NJ = PairSlots<K>::NJ;
   const int lane = lane_id();
-  float accA = 0.f, accB = 0.f;
+  accA = 0.f;
+  accB = 0.f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int f = j * kWave + lane;
@@ -294,6 +350,15 @@ __device__ __forceinline__ void pair_dot(const float4 (&w)[PairSlots<K>::NJ],
       }
     }
   }
+}
+
+// Wave-reduced dot products (every lane gets both sums).
+template <int K>
+__device__ __forceinline__ void pair_dot(const float4 (&w)[PairSlots<K>::NJ],
+                                         const float4 (&xv)[PairSlots<K>::NJ],
+                                         float &sa, float &sb) {
+  float accA, accB;
+  pair_partial<K>(w, xv, accA, accB);
   sa = wave_sum(accA);
   sb = wave_sum(accB);
 }

@@ -525,32 +525,35 @@ struct PairRole {
   template <typename Prep, typename Epi, typename Mid>
   __device__ void compute(const float4 (&xv)[NJ], Prep prep, Epi epi, Mid mid) const {
     const int w = wave_u(), lane = lane_id();
-    float sa[S + kLdsPerWave], sb[S + kLdsPerWave];
+    constexpr int kUnits = S + kLdsPerWave;
+    static_assert(kUnits <= 8, "unit sums travel as values 0..7 and 8..15");
+    // Per-lane partials of every unit: unit j's first row as value j, its
+    // second row as value 8 + j (zeros where the wave has no unit).
+    float part[16];
 #pragma unroll
-    for (int j = 0; j < S; ++j) pair_dot<H>(wv[j], xv, sa[j], sb[j]);
+    for (int i = 0; i < 16; ++i) part[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < S; ++j) pair_partial<H>(wv[j], xv, part[j], part[8 + j]);
 #pragma unroll
     for (int i = 0; i < kLdsPerWave; ++i) {
       const int k = kW * S + w + kW * i;
-      sa[S + i] = sb[S + i] = 0.f;
       if (k < n && k - kW * S < Lcap) {
         const float4 *src = units + (k - kW * S) * UnitF4;
         float4 wl[NJ];
 #pragma unroll
         for (int c = 0; c < NJ; ++c) wl[c] = src[c * kWave + lane];
-        pair_dot<H>(wl, xv, sa[S + i], sb[S + i]);
+        pair_partial<H>(wl, xv, part[S + i], part[8 + S + i]);
       }
     }
+    // All the wave's sums at once, each bit-identical to wave_sum (lane l
+    // holds value l mod 16): unit j's sums finish in lane j, where all the
+    // wave's epilogues then run at once.
+    const float tot = wave_sum_multi<16>(part);
     mid();
-    // Unit j of the wave (register slot j, then LDS unit j - S) finishes in
-    // lane j: the sums move there and all the wave's epilogues run at once.
-    constexpr int kUnits = S + kLdsPerWave;
-    static_assert(kUnits <= kWave, "one lane per unit");
-    float ma = 0.f, mb = 0.f;
-#pragma unroll
-    for (int j = 0; j < kUnits; ++j) {
-      ma = lane == j ? sa[j] : ma;
-      mb = lane == j ? sb[j] : mb;
-    }
+    const float ma = tot;
+    const float mb = __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, tot), 0x108 /* row_shl:8 */, 0xf, 0xf,
+                                           false));
     const int k = lane < S ? w + kW * lane : kW * S + w + kW * (lane - S);
     if (lane < kUnits && k < n && (lane < S || k - kW * S < Lcap)) epi(k, ma, mb, prep(k));
   }
