@@ -84,9 +84,13 @@ constexpr int kTagSeqBits = 20;
 // to 0x7FC00000.
 constexpr int kRoleRecStride = 68;
 constexpr uint32_t kSlotEmpty = 0xFFFFFFFFu;
+// The layer output is published in segments: down CU r writes its rows
+// (at most kHidSegment) padded to whole float4s in floats
+// [kHidSegment * r, kHidSegment * (r + 1)), so no float4 has two writers.
+constexpr int kHidSegment = 16;
 constexpr size_t roles_slot_floats(int hidden, int inter, int heads, int kv_heads) {
   return size_t(heads + 2 * kv_heads) * 64 + size_t(heads) * kAttnMaxChunks * kRoleRecStride +
-         2 * size_t(hidden) + size_t(inter);
+         size_t(hidden) + size_t(inter) + size_t(kHidSegment) * kMaxRoleGrid;
 }
 
 int device_cu_count(int device);

@@ -334,6 +334,45 @@ __device__ bool gather4c(const Slots &src, int first4, int n4, float *dst, Wait 
                           });
 }
 
+// Whole-workgroup wait for `items` float4s of hand-off slots, item p =
+// threadIdx.x + k * kT held in the thread's k-th place: live(p, k, s4) names
+// its slot index and returns false for an item with nothing to wait for;
+// put(k, v) consumes a complete float4. Returns false when the wait gave up
+// (error raised).
+template <int kMaxPer, typename Live, typename Put>
+__device__ bool gather4_put(const Slots &src, int items, Wait wait, uint32_t *flags, Live live, Put put) {
+  const int t = threadIdx.x;
+  uint32_t pending = 0;
+  int slot[kMaxPer];
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k) {
+    slot[k] = 0;
+    if (t + k * kT < items && live(t + k * kT, k, slot[k])) pending |= 1u << k;
+  }
+  for (uint32_t spin = 0;; ++spin) {
+    Quad got[kMaxPer];
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k)
+      if ((pending >> k) & 1u) got[k] = __builtin_bit_cast(Quad, src.get4(slot[k]));
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+      const Quad &g = got[k];
+      if (((pending >> k) & 1u) && g.w[0] != kSlotEmpty && g.w[1] != kSlotEmpty &&
+          g.w[2] != kSlotEmpty && g.w[3] != kSlotEmpty) {
+        put(k, make_float4(__uint_as_float(g.w[0]), __uint_as_float(g.w[1]), __uint_as_float(g.w[2]),
+                           __uint_as_float(g.w[3])));
+        pending &= ~(1u << k);
+      }
+    }
+    vm_wait();
+    if (block_all(pending == 0, flags)) return true;
+    if (spin > wait.limit) {
+      if (t == 0) atomicOr(wait.error, kResidentWaitGaveUp);
+      return false;
+    }
+  }
+}
+
 // Publishing a role's outputs. A role CU's outputs are fixed runs of slot
 // elements; each thread owns at most one float4 of them (OutMap, computed
 // once per launch): its float4 index q in the destination, which of its
@@ -640,20 +679,46 @@ struct DownRole {
       }
   }
   // Per-lane slice sums of every row with this wave's activation slice xa:
-  // row r's lands in part[(r * kW + wave) * 64 + lane].
+  // row r's lands in part[(r * kW + wave) * 64 + lane]. The register rows
+  // are computed unconditionally (rows past n hold zeros); the LDS rows go
+  // in batches of kBatch whose reads are all issued before their products,
+  // so a batch waits for LDS once (indices past the last row are clamped to
+  // it and their sums discarded).
+  static constexpr int kBatch = 4;
   template <int Ns>
   __device__ void sums_ns(const float4 (&xa)[kNsHi], float *part) const {
     constexpr int Nr = reg_f4(Ns) / Ns;
     const int lane = lane_id(), w = wave_u();
+    float acc[Nr];
 #pragma unroll
-    for (int r = 0; r < kMaxRows; ++r) {
-      if (r < n) {
-        float acc = 0.f;
+    for (int r = 0; r < Nr; ++r) {
+      acc[r] = 0.f;
 #pragma unroll
-        for (int s = 0; s < Ns; ++s)
-          acc = fma4(r < Nr ? wr[(r < Nr ? r : 0) * Ns + s] : lw[((r - Nr) * Ns + s) * kWave + lane], xa[s], acc);
-        part[(r * kW + w) * kWave + lane] = acc;
+      for (int s = 0; s < Ns; ++s) acc[r] = fma4(wr[r * Ns + s], xa[s], acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < Nr; ++r)
+      if (r < n) part[(r * kW + w) * kWave + lane] = acc[r];
+#pragma unroll
+    for (int b = Nr; b < kMaxRows; b += kBatch) {
+      if (b >= n) break;
+      float4 lr[kBatch][Ns];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int r = min(b + i, n - 1);
+#pragma unroll
+        for (int s = 0; s < Ns; ++s) lr[i][s] = lw[((r - Nr) * Ns + s) * kWave + lane];
       }
+      float bacc[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        bacc[i] = 0.f;
+#pragma unroll
+        for (int s = 0; s < Ns; ++s) bacc[i] = fma4(lr[i][s], xa[s], bacc[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i)
+        if (b + i < n) part[((b + i) * kW + w) * kWave + lane] = bacc[i];
     }
   }
   __device__ void sums(const float4 (&xa)[kNsHi], float *part) const {
@@ -741,7 +806,8 @@ struct Roles {
   static constexpr int kOffH1 = kOffPart + Sh::PartFloats;
   static constexpr int kOffAct = kOffH1 + H;
   static constexpr int kOffHid = kOffAct + I;
-  static constexpr int kSlotFloats = kOffHid + H;
+  static constexpr int kHidFloats = kHidSegment * kMaxRoleGrid;
+  static constexpr int kSlotFloats = kOffHid + kHidFloats;
   static_assert(kSlotFloats == roles_slot_floats(H, I, NQ, NKV) && kOffPart % 4 == 0 && H % 4 == 0 &&
                     I % 4 == 0 && kRoleRecStride % 4 == 0,
                 "slot layout");
@@ -758,7 +824,56 @@ struct Roles {
   __device__ Slots s_part(int l, uint32_t t) const { return slots(l, t, kOffPart, Sh::PartFloats); }
   __device__ Slots s_h1(int l, uint32_t t) const { return slots(l, t, kOffH1, H); }
   __device__ Slots s_act(int l, uint32_t t) const { return slots(l, t, kOffAct, I); }
-  __device__ Slots s_hid(int l, uint32_t t) const { return slots(l, t, kOffHid, H); }
+  __device__ Slots s_hid(int l, uint32_t t) const { return slots(l, t, kOffHid, kHidFloats); }
+  // The down role's split of the layer output: CU r of ndown() owns rows
+  // [down_begin(r), down_begin(r + 1)), published as segment r.
+  __device__ int ndown() const { return a.role_end[kRoleDown] - a.role_end[kRoleGate]; }
+  // split_begin(H, R, r) without an integer division: H r < 2^24 is exact
+  // in float, the product with 1/R is within one of the quotient, and one
+  // correction step makes it exact.
+  __device__ static int down_begin(int r, int R, float inv_r) {
+    const int num = H * r;
+    int q = static_cast<int>(static_cast<float>(num) * inv_r);
+    q -= q * R > num ? 1 : 0;
+    q += (q + 1) * R <= num ? 1 : 0;
+    return q;
+  }
+  static_assert(H * kMaxRoleGrid < (1 << 24), "exact float products");
+  // Rows [row0, row0 + nrows) of layer l's output -> dst[row - row0]: the
+  // segments of the down CUs owning them, whole float4s polled like any
+  // hand-off, each valid row scattered to its place.
+  static constexpr int kHidMaxPer = 2;
+  __device__ bool gather_hid(uint32_t t, int l, int row0, int nrows, float *dst) {
+    const int R = ndown();
+    const float inv_r = 1.f / static_cast<float>(R);
+    // Owner of row i: the largest r with split_begin(H, R, r) <= i
+    // (a division by the constant H).
+    auto owner = [&](int i) { return ((i + 1) * R - 1) / H; };
+    const int r_lo = owner(row0);
+    const int items = 4 * (owner(row0 + nrows - 1) - r_lo + 1);
+    // Item p: float4 q of segment r; rows [b, e) of that float4 land in dst.
+    int first[kHidMaxPer], count[kHidMaxPer];
+    return gather4_put<kHidMaxPer>(
+        s_hid(l, t), items, wt(), cm.flags,
+        [&](int p, int k, int &s4) {
+          const int r = r_lo + p / 4, q = p % 4;
+          s4 = (kHidSegment / 4) * r + q;
+          const int b = down_begin(r, R, inv_r) + 4 * q;
+          const int e = min(down_begin(r + 1, R, inv_r), b + 4);
+          first[k] = b;
+          count[k] = e - b;
+          return e > b;
+        },
+        [&](int k, float4 v) {
+          const int b = first[k], c = count[k];
+          const float x[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int row = b + j;
+            if (j < c && row >= row0 && row < row0 + nrows) dst[row - row0] = x[j];
+          }
+        });
+  }
   // The host plan never gives a CU more units than it holds on chip; a plan
   // that did is reported as an error (the other CUs' waits then give up).
   __device__ bool fits(int n, int capacity) const {
@@ -855,8 +970,7 @@ struct Roles {
     load_pair_gain<H>(a.final_norm, gv);
     load(gw, w0);
     __builtin_amdgcn_sched_barrier(0);
-    if (!gather4c<(H / 4 + kT - 1) / kT>(s_hid(a.layers - 1, t), 0, H / 4, cm.vec, wt(), cm.flags))
-      return false;
+    if (!gather_hid(t, a.layers - 1, 0, H, cm.vec)) return false;
     clock.lap(2 * kRoleCount);
     float4 xv[NJ];
     const float inv = norm_scale(load_pair_operand_gain<H>(Lds{cm.vec}, gv, xv), H, a.eps);
@@ -973,7 +1087,7 @@ struct Roles {
       lds_barrier();
       return true;
     }
-    return gather4c<(H / 4 + kT - 1) / kT>(s_hid(l - 1, t), first4, n4, dst, wt(), cm.flags);
+    return gather_hid(t, l - 1, 4 * first4, min(4 * n4, H - 4 * first4), dst);
   }
 
   // ---- QKV ------------------------------------------------------------------
@@ -1275,51 +1389,93 @@ struct Roles {
           return false;
       }
       clock.lap(2 * kRoleO);
-      // Merge, in the arithmetic of attn_merge: wave w takes heads 2w and
-      // 2w + 1, one per half-wave, and lane d of a half computes dims d and
-      // d + 32 of its head: M = the largest of the C chunk maxima, then
-      // w_c = 2^(m_c - M) folded into the denominator and both numerators
-      // in chunk order, then one division per dim. Every lane of a half
-      // reads the same m_c and l_c (LDS broadcasts); no value crosses lanes.
-      // The code is specialised on C rounded up to 4 (kCm chunks, the terms
-      // past C skipped by a wave-uniform test); every read is an immediate
-      // offset from the head's record base.
-      static_assert(kHeadDim == kWave && NQ <= 2 * kW && kAttnMaxChunks % 4 == 0,
-                    "two heads per wave");
-      auto merge = [&](auto cm_tag) {
-        constexpr int kCm = decltype(cm_tag)::value;
-        const int h = 2 * wv + (lane >> 5);
-        if (h >= NQ) return;
-        const int d = lane & 31;
-        const float *rec = parts + h * kAttnMaxChunks * kRoleRecStride;
-        float mv[kCm], lv[kCm];
+      // Merge, in the arithmetic of attn_merge, in two phases. Phase 1 (the
+      // last wave, lane h = head h): M = the largest of the C chunk maxima,
+      // w_c = 2^(m_c - M), den = the w_c l_c folded in chunk order; w (zero
+      // past C) and den go to LDS. Phase 2 (wave w: heads 2w and 2w + 1, one
+      // per half-wave; lane d of a half: dims d and d + 32): both numerators
+      // folded in chunk order from the broadcast weights, then one division
+      // per dim. Phase 2 is specialised on the exact C, so it carries no
+      // per-chunk test; its record reads are issued before the barrier.
+      static_assert(kHeadDim == kWave && NQ <= 2 * (kW - 1) && NQ <= kWave && kAttnMaxChunks == 16,
+                    "merge layout");
+      float *wsh = cm.top + 2 * kMaxRoleGrid - kAttnMaxChunks * NQ - NQ;  // [h][c], then den[h]
+      static_assert(2 * kMaxRoleGrid - kAttnMaxChunks * NQ - NQ >=
+                        2 * PairRole<QD, kSlotsO, Sh::LO>::capacity() + 4,
+                    "merge weights clear of the output stage");
+      if (wv == kW - 1) {
+        if (lane < NQ) {
+          const float *rec = parts + lane * kAttnMaxChunks * kRoleRecStride;
+          float mv[kAttnMaxChunks], lv[kAttnMaxChunks];
 #pragma unroll
-        for (int c = 0; c < kCm; ++c) {
-          const float2 ml = *reinterpret_cast<const float2 *>(rec + c * kRoleRecStride);
-          mv[c] = ml.x;
-          lv[c] = ml.y;
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int c = 0; c < kCm; ++c) mx = c < C ? fmaxf(mx, mv[c]) : mx;
-        float num0 = 0.f, num1 = 0.f, den = 0.f;
-#pragma unroll
-        for (int c = 0; c < kCm; ++c) {
-          if (c < C) {
-            const float w = exp2_fast(mv[c] - mx);
-            den = fmaf(w, lv[c], den);
-            num0 = fmaf(w, rec[c * kRoleRecStride + 4 + d], num0);
-            num1 = fmaf(w, rec[c * kRoleRecStride + 4 + d + 32], num1);
+          for (int c = 0; c < kAttnMaxChunks; ++c) {
+            const float2 ml = *reinterpret_cast<const float2 *>(rec + c * kRoleRecStride);
+            mv[c] = ml.x;
+            lv[c] = ml.y;
           }
+          float mx = -INFINITY;
+#pragma unroll
+          for (int c = 0; c < kAttnMaxChunks; ++c) mx = c < C ? fmaxf(mx, mv[c]) : mx;
+          float den = 0.f, w[kAttnMaxChunks];
+#pragma unroll
+          for (int c = 0; c < kAttnMaxChunks; ++c) {
+            w[c] = c < C ? exp2_fast(mv[c] - mx) : 0.f;
+            den = c < C ? fmaf(w[c], lv[c], den) : den;
+          }
+#pragma unroll
+          for (int c4 = 0; c4 < kAttnMaxChunks / 4; ++c4)
+            reinterpret_cast<float4 *>(wsh + lane * kAttnMaxChunks)[c4] =
+                make_float4(w[4 * c4], w[4 * c4 + 1], w[4 * c4 + 2], w[4 * c4 + 3]);
+          wsh[kAttnMaxChunks * NQ + lane] = den;
         }
-        cm.xn[h * kHeadDim + d] = num0 / den;
-        cm.xn[h * kHeadDim + d + 32] = num1 / den;
-      };
-      switch ((C + 3) / 4) {
-        case 1: merge(std::integral_constant<int, 4>{}); break;
-        case 2: merge(std::integral_constant<int, 8>{}); break;
-        case 3: merge(std::integral_constant<int, 12>{}); break;
-        default: merge(std::integral_constant<int, 16>{}); break;
+        lds_barrier();
+      } else {
+        auto merge = [&](auto c_tag) {
+          constexpr int kC = decltype(c_tag)::value;
+          const int h = 2 * wv + (lane >> 5);
+          const int d = lane & 31;
+          const bool live = h < NQ;
+          const float *rec = parts + (live ? h : 0) * kAttnMaxChunks * kRoleRecStride;
+          float av[kC], bv[kC];
+#pragma unroll
+          for (int c = 0; c < kC; ++c) {
+            av[c] = rec[c * kRoleRecStride + 4 + d];
+            bv[c] = rec[c * kRoleRecStride + 4 + d + 32];
+          }
+          lds_barrier();
+          if (!live) return;
+          const float *wh = wsh + h * kAttnMaxChunks;
+          float w[kAttnMaxChunks];
+#pragma unroll
+          for (int c4 = 0; c4 < (kC + 3) / 4; ++c4) {
+            const float4 q = reinterpret_cast<const float4 *>(wh)[c4];
+            w[4 * c4] = q.x;
+            w[4 * c4 + 1] = q.y;
+            w[4 * c4 + 2] = q.z;
+            w[4 * c4 + 3] = q.w;
+          }
+          const float den = wsh[kAttnMaxChunks * NQ + h];
+          float num0 = 0.f, num1 = 0.f;
+#pragma unroll
+          for (int c = 0; c < kC; ++c) {
+            num0 = fmaf(w[c], av[c], num0);
+            num1 = fmaf(w[c], bv[c], num1);
+          }
+          cm.xn[h * kHeadDim + d] = num0 / den;
+          cm.xn[h * kHeadDim + d + 32] = num1 / den;
+        };
+        switch (C) {
+#define QD_MERGE_CASE(n) \
+  case n:                \
+    merge(std::integral_constant<int, n>{}); \
+    break;
+          QD_MERGE_CASE(1) QD_MERGE_CASE(2) QD_MERGE_CASE(3) QD_MERGE_CASE(4)
+          QD_MERGE_CASE(5) QD_MERGE_CASE(6) QD_MERGE_CASE(7) QD_MERGE_CASE(8)
+          QD_MERGE_CASE(9) QD_MERGE_CASE(10) QD_MERGE_CASE(11) QD_MERGE_CASE(12)
+          QD_MERGE_CASE(13) QD_MERGE_CASE(14) QD_MERGE_CASE(15)
+          default: merge(std::integral_constant<int, 16>{}); break;
+#undef QD_MERGE_CASE
+        }
       }
       lds_barrier();
       float4 xv[PairSlots<QD>::NJ];
@@ -1350,9 +1506,11 @@ struct Roles {
 
   // ---- gate/up + SiLU -------------------------------------------------------
   __device__ void run_gate() {
-    const int u0 = split_begin(I, nrole, rank);
+    // Whole float4s of the activation per CU, so no float4 has two writers.
+    static_assert(I % 4 == 0, "activation in float4s");
+    const int u0 = 4 * split_begin(I / 4, nrole, rank);
     PairRole<H, kSlotsG, Sh::LG> rg;
-    rg.n = split_begin(I, nrole, rank + 1) - u0;
+    rg.n = 4 * split_begin(I / 4, nrole, rank + 1) - u0;
     rg.units = reinterpret_cast<float4 *>(region);
     if (!fits(rg.n, rg.capacity())) return;
     auto rows = [&](int l) {
@@ -1411,16 +1569,20 @@ struct Roles {
     };
     auto pre_lds = [&](int l, int) { rd.prefetch_lds(row(l)); };
     auto pre_regs = [&](int l) { rd.prefetch_regs(row(l)); };
-    OutMap om;  // rows [u0, u0 + n), staged from u0 rounded down to 4
-    om.take(u0, n, u0 & ~3, threadIdx.x, 0);
+    // This CU's output segment: float4s [seg4, seg4 + 4) of the layer
+    // output, rows u0 + k at element k, padded with zeros; thread q < pub4
+    // publishes float4 q.
+    static_assert(DownRole<I>::kMaxRows <= kHidSegment, "a down CU's rows fit its segment");
+    const int seg4 = (kHidSegment / 4) * rank, pub4 = (n + 3) / 4;
+    const bool pub = static_cast<int>(threadIdx.x) < pub4;
     const int hb4 = u0 / 4;                       // float4s of h1 covering [u0, u0 + n)
     const int hn4 = (u0 + n + 3) / 4 - hb4;
     // Per-lane slice sums [row][wave][lane], after this CU's LDS rows.
     float *part = reinterpret_cast<float *>(region) + DownRole<I>::lds_rows(n) * kWave * 4;
-    float *stage = cm.top;  // row u0 + k at stage[k + (u0 & 3)]
+    float *stage = cm.top;  // row u0 + k at stage[k]
     loop(kRoleDown, true, [&](uint32_t t, int l, int position) {
       const Slots out = s_hid(l, t);
-      if (om.q >= 0) clear_quad(s_hid(l, t + 1), om);
+      if (pub) s_hid(l, t + 1).clear4(seg4 + threadIdx.x);
       if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), hb4, hn4, cm.vec, wt(), cm.flags)) return false;
       // This wave's slice of the activation, straight into registers.
       float4 xa[DownRole<I>::kNsHi];
@@ -1456,15 +1618,26 @@ struct Roles {
       if (ok) rd.sums(xa, part);
       clock.mark(1);
       if (!block_all(ok, cm.flags)) return false;
-      for (int k = wv; k < n; k += kW) {
-        float p[kRowSlices];
+      // Wave w finishes rows w and w + kW (at most kMaxRows = 2 kW rows): the
+      // slice sums of both rows are read at once and reduced together
+      // (wave_sum_multi: row w's sum in lane 0, row w + kW's in lane 1).
+      static_assert(DownRole<I>::kMaxRows <= 2 * kW, "two rows per wave");
+      if (wv < n) {
+        const int k1 = min(wv + kW, n - 1);
+        float p0[kRowSlices], p1[kRowSlices];
 #pragma unroll
-        for (int w = 0; w < kRowSlices; ++w) p[w] = part[(k * kW + w) * kWave + lane];
-        const float sum = wave_sum(combine_slices(p));
-        if (lane == 0) stage[k + (u0 & 3)] = cm.vec[u0 + k - 4 * hb4] + sum;
+        for (int w = 0; w < kRowSlices; ++w) {
+          p0[w] = part[(wv * kW + w) * kWave + lane];
+          p1[w] = part[(k1 * kW + w) * kWave + lane];
+        }
+        const float two[2] = {combine_slices(p0), combine_slices(p1)};
+        const float sum = wave_sum_multi<2>(two);
+        const int k = wv + kW * lane;
+        if (lane < 2 && k < n) stage[k] = cm.vec[u0 + k - 4 * hb4] + sum;
       }
+      if (static_cast<int>(threadIdx.x) >= n && static_cast<int>(threadIdx.x) < 4 * pub4) stage[threadIdx.x] = 0.f;
       lds_barrier();
-      if (om.q >= 0) put_quad(out, om, reinterpret_cast<const float4 *>(stage)[om.soff]);
+      if (pub) out.put4(seg4 + threadIdx.x, reinterpret_cast<const float4 *>(stage)[threadIdx.x]);
       clock.mark(2);
       lds_barrier();
       clock.lap(2 * kRoleDown + 1);
@@ -1557,8 +1730,14 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
   const double bytes[4] = {double(units[0]) * Qwen::UnitBytes, double(units[1]) * Qwen::UnitBytes,
                            double(units[2]) * Qwen::UnitBytes, double(units[3]) * Qwen::RowBytes};
   const double total = bytes[0] + bytes[1] + bytes[2] + bytes[3];
+  // CUs a role needs to hold its units: the gate role splits whole float4s
+  // of the activation (4 units), the others single units.
+  auto need_of = [&](int r) {
+    const int g = r == 2 ? 4 : 1;
+    return ((units[r] + g - 1) / g + cap[r] / g - 1) / (cap[r] / g);
+  };
   int floor_weights = 0;
-  for (int r = 0; r < 4; ++r) floor_weights += (units[r] + cap[r] - 1) / cap[r];
+  for (int r = 0; r < 4; ++r) floor_weights += need_of(r);
   // One attention CU per (KV head, chunk) unit of the longest context, or
   // as many as the weight roles leave (an attention CU then takes several
   // units, the later ones staged after its query arrives).
@@ -1567,7 +1746,7 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
   const int rest = grid - n_attn;
   int n[4], used = 0;
   for (int r = 0; r < 4; ++r) {
-    const int need = (units[r] + cap[r] - 1) / cap[r];
+    const int need = need_of(r);
     n[r] = std::max(need, static_cast<int>(rest * bytes[r] / total));
     n[r] = std::min(n[r], units[r]);
     used += n[r];
@@ -1579,7 +1758,7 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
     double best = used < rest ? -1.0 : 1e30;
     for (int r = 0; r < 4; ++r) {
       const double share = bytes[r] / n[r];
-      const int need = (units[r] + cap[r] - 1) / cap[r];
+      const int need = need_of(r);
       if (used < rest && n[r] < units[r] && share > best) {
         best = share;
         pick = r;
@@ -1598,6 +1777,9 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
   plan->end[kRoleO] = plan->end[kRoleAttn] + n[1];
   plan->end[kRoleGate] = plan->end[kRoleO] + n[2];
   plan->end[kRoleDown] = plan->end[kRoleGate] + n[3];
+  // The layer output's segments are gathered with at most two float4s per
+  // thread (Roles::kHidMaxPer).
+  if (4 * n[3] > 2 * kT) return false;
   return plan->end[kRoleDown] == grid;
 }
 
