@@ -72,17 +72,33 @@ __device__ __forceinline__ void attn_head_window(K4 k4, V v, const float4 (&q)[k
 
 // Merge of one head's partials for output dim d; part(c, k) returns element
 // k of chunk c's record (0: m, base 2; 1: l; 2 + d: acc):
-// out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c. Records are stored head
-// major: record (h, c) at (h * kAttnMaxChunks + c) * kPartStride.
+// out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c. The numerator folds
+// the chunks in order (fma); the denominator sums the products
+// 2^(m_c - M) l_c of all kAttnMaxChunks chunk places (zero past `chunks`) as
+// the pairwise tree of row16_sum, the order the resident role kernel forms
+// it in with one lane per chunk. Records are stored head major: record
+// (h, c) at (h * kAttnMaxChunks + c) * kPartStride.
 template <typename Part>
 __device__ __forceinline__ float attn_merge(const Part &part, int chunks, int d) {
+  static_assert(kAttnMaxChunks == 16, "one 16-lane row per head");
   float mx = -INFINITY;
   for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, part(c, 0));
-  float num = 0.f, den = 0.f;
-  for (int c = 0; c < chunks; ++c) {
-    const float w = exp2_fast(part(c, 0) - mx);
-    den = fmaf(w, part(c, 1), den);
-    num = fmaf(w, part(c, 2 + d), num);
+  float t[kAttnMaxChunks];
+  float num = 0.f;
+  for (int c = 0; c < kAttnMaxChunks; ++c) {
+    t[c] = 0.f;
+    if (c < chunks) {
+      const float w = exp2_fast(part(c, 0) - mx);
+      t[c] = __fmul_rn(w, part(c, 1));  // a rounded product: never contracted into the sums
+      num = fmaf(w, part(c, 2 + d), num);
+    }
+  }
+  float den = 0.f;
+#pragma unroll
+  for (int o = 0; o < kAttnMaxChunks; o += 8) {
+    const float a = (t[o] + t[o + 1]) + (t[o + 2] + t[o + 3]);
+    const float b = (t[o + 4] + t[o + 5]) + (t[o + 6] + t[o + 7]);
+    den = o == 0 ? a + b : den + (a + b);
   }
   return num / den;
 }

@@ -99,6 +99,23 @@ __device__ __forceinline__ float wave_sum_multi(const float (&in)[N]) {
   return r;
 }
 
+// Max and sum over each row of 16 lanes, the result in every lane of the
+// row: wave_max's and wave_sum's first four steps. The sum groups the lanes
+// as a pairwise tree ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)), and
+// likewise for lanes 8..15, then the two halves.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  return fmaxf(v, dpp<kDppMirror>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  return v + dpp<kDppMirror>(v);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<kDppXor1>(v));
   v = fmaxf(v, dpp<kDppXor2>(v));
@@ -340,12 +357,19 @@ __device__ __forceinline__ void pair_partial(const float4 (&w)[PairSlots<K>::NJ]
     if (j * kWave + kWave <= K4) {
       accA = fma4(w[j], xv[j], accA);
     } else if (j * kWave >= K4) {
-      accB = fma4(w[j], xv[j], accB);
+      // Lanes past the pair's 2 K4 float4s (the last slot's padding, which
+      // an LDS-staged unit may hold any finite or non-finite words in) add
+      // nothing.
+      if (j * kWave + kWave <= 2 * K4) {
+        accB = fma4(w[j], xv[j], accB);
+      } else {
+        accB = f < 2 * K4 ? fma4(w[j], xv[j], accB) : accB;
+      }
     } else {
       const float d = fma4(w[j], xv[j], 0.f);
       if (f < K4) {
         accA += d;
-      } else {
+      } else if (f < 2 * K4) {
         accB += d;
       }
     }

@@ -151,23 +151,34 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(
       d);
 }
 
-// hidden[r] += Wo[r,:] . attn; unit u = rows (2u, 2u+1), contiguous.
-template <int H, int QD>
+// hidden[r] += Wo[r,:] . attn; unit u = rows (2u, 2u+1), contiguous. The
+// dot is taken per KV group (columns [g QDG, (g + 1) QDG): the group's
+// query heads) and added in group order, hidden + group 0 first: the
+// resident role kernel's O CUs each hold one group's columns.
+template <int H, int QD, int NKV>
 __global__ __launch_bounds__(kBlock) void oproj_residual_kernel(
     const float *__restrict__ attn, const float *__restrict__ wo,
     const SeqState *__restrict__ st, float *__restrict__ hidden) {
   if (st->stopped) return;
-  float4 xv[PairSlots<QD>::NJ];
-  load_pair_operand<QD>(Plain(attn), xv);
+  constexpr int QDG = QD / NKV;
+  float4 xv[NKV][PairSlots<QDG>::NJ];
+#pragma unroll
+  for (int g = 0; g < NKV; ++g) load_pair_operand<QDG>(Plain(attn + g * QDG), xv[g]);
   constexpr int units = H / 2;
   for (int u = blockIdx.x * kWavesPerBlock + wave_id(); u < units;
        u += gridDim.x * kWavesPerBlock) {
     const float *a = wo + static_cast<size_t>(2 * u) * QD;
-    float sa, sb;
-    dot_pair<QD>(a, a + QD, xv, sa, sb);
+    float ha = hidden[2 * u], hb = hidden[2 * u + 1];
+#pragma unroll
+    for (int g = 0; g < NKV; ++g) {
+      float sa, sb;
+      dot_pair<QDG>(a + g * QDG, a + QD + g * QDG, xv[g], sa, sb);
+      ha += sa;
+      hb += sb;
+    }
     if (lane_id() == 0) {
-      hidden[2 * u] += sa;
-      hidden[2 * u + 1] += sb;
+      hidden[2 * u] = ha;
+      hidden[2 * u + 1] = hb;
     }
   }
 }
@@ -523,9 +534,15 @@ hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
   }
   {
     Scope scope(m, kKOproj);
-    oproj_residual_kernel<H, QD>
-        <<<(H / 2 + kWavesPerBlock - 1) / kWavesPerBlock, kBlock, 0, s>>>(
-            p.attn, p.w.wo, p.st, p.hidden);
+    const dim3 grid((H / 2 + kWavesPerBlock - 1) / kWavesPerBlock);
+    // The KV-group counts of QD / 64 query heads (shape_supported).
+    switch (p.nkv) {
+      case 1: oproj_residual_kernel<H, QD, 1><<<grid, kBlock, 0, s>>>(p.attn, p.w.wo, p.st, p.hidden); break;
+      case 2: oproj_residual_kernel<H, QD, 2><<<grid, kBlock, 0, s>>>(p.attn, p.w.wo, p.st, p.hidden); break;
+      case 7: oproj_residual_kernel<H, QD, 7><<<grid, kBlock, 0, s>>>(p.attn, p.w.wo, p.st, p.hidden); break;
+      case 14: oproj_residual_kernel<H, QD, 14><<<grid, kBlock, 0, s>>>(p.attn, p.w.wo, p.st, p.hidden); break;
+      default: return hipErrorInvalidValue;
+    }
   }
   {
     Scope scope(m, kKGateUp);

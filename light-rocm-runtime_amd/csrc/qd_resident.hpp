@@ -90,7 +90,7 @@ constexpr uint32_t kSlotEmpty = 0xFFFFFFFFu;
 constexpr int kHidSegment = 16;
 constexpr size_t roles_slot_floats(int hidden, int inter, int heads, int kv_heads) {
   return size_t(heads + 2 * kv_heads) * 64 + size_t(heads) * kAttnMaxChunks * kRoleRecStride +
-         size_t(hidden) + size_t(inter) + size_t(kHidSegment) * kMaxRoleGrid;
+         size_t(kv_heads) * hidden + size_t(inter) + size_t(kHidSegment) * kMaxRoleGrid;
 }
 
 int device_cu_count(int device);

@@ -61,7 +61,7 @@ constexpr int kLdsBytes = 160 * 1024 - 512;
 constexpr int kAttnCap = 256;     // positions of an attention window staged in LDS
 
 // Register slots per wave: row-pair units of the K=H roles, rows of DOWN.
-constexpr int kSlotsQ = 2, kSlotsO = 2, kSlotsG = 2;
+constexpr int kSlotsQ = 2, kSlotsO = 4, kSlotsG = 2;
 
 // Wave index as a wave-uniform (scalar) value: unit indices, slot branches
 // and row addresses derived from it stay in SGPRs.
@@ -188,6 +188,8 @@ struct Common {
                                         //   layers, a role's outputs staged for their stores
   ClockLds clock;                       // profiling (profiled variant only)
 };
+static_assert(offsetof(Common, xn) == offsetof(Common, vec) + sizeof(Common::vec),
+              "h1 partials stage in vec and then xn");
 // The kernel's one LDS block, at namespace scope so the per-role functions
 // (called from the kernel) address it as LDS.
 __shared__ __attribute__((aligned(16))) unsigned char roles_lds[kLdsBytes];
@@ -744,9 +746,15 @@ struct Shape {
   // QKV region: units, biases (whole float4 DMA rows), cos|sin row.
   static constexpr int BiasF4 = (QkvRows / 4 + kWave - 1) / kWave * kWave;
   static constexpr int LQ = (kRegionBytes - BiasF4 * 16 - kWave * 16) / UnitBytes;
-  // O region: units, partial records of every head.
+  // Partial records of every head (the slot block's attention outputs).
   static constexpr int PartFloats = NQ * kAttnMaxChunks * kRoleRecStride;
-  static constexpr int LO = (kRegionBytes - PartFloats * 4) / UnitBytes;
+  // O is split by KV group: an O CU of group g takes the g-th QDG columns
+  // (its G query heads) of every row, so its units are row pairs of QDG
+  // columns, and its region holds units and its group's records.
+  static constexpr int QDG = G * kHeadDim;
+  static constexpr int OUnitBytes = PairSlots<QDG>::NJ * kWave * 16;
+  static constexpr int PartFloatsG = G * kAttnMaxChunks * kRoleRecStride;
+  static constexpr int LO = (kRegionBytes - PartFloatsG * 4) / OUnitBytes;
   static constexpr int LG = kRegionBytes / UnitBytes;
   static_assert(QkvRows % 2 == 0 && H % 2 == 0, "row pairs");
   static_assert(G <= kW && NQ % NKV == 0, "one wave per query head of a group");
@@ -804,7 +812,7 @@ struct Roles {
   static constexpr int kOffQkv = 0;
   static constexpr int kOffPart = QD + 2 * KVD;
   static constexpr int kOffH1 = kOffPart + Sh::PartFloats;
-  static constexpr int kOffAct = kOffH1 + H;
+  static constexpr int kOffAct = kOffH1 + NKV * H;
   static constexpr int kOffHid = kOffAct + I;
   static constexpr int kHidFloats = kHidSegment * kMaxRoleGrid;
   static constexpr int kSlotFloats = kOffHid + kHidFloats;
@@ -822,7 +830,32 @@ struct Roles {
   }
   __device__ Slots s_qkv(int l, uint32_t t) const { return slots(l, t, kOffQkv, QD + 2 * KVD); }
   __device__ Slots s_part(int l, uint32_t t) const { return slots(l, t, kOffPart, Sh::PartFloats); }
-  __device__ Slots s_h1(int l, uint32_t t) const { return slots(l, t, kOffH1, H); }
+  // Group g's partial of the attention block's output: the O rows over
+  // group g's heads (group 0's with the residual added); h1 is their sum in
+  // group order.
+  __device__ Slots s_h1(int l, uint32_t t, int g) const { return slots(l, t, kOffH1 + g * H, H); }
+  // Float4s [first4, first4 + n4) of h1 -> dst, summed in group order (dst
+  // and the following NKV - 1 runs of kH1Stride4 float4s are the staging).
+  static constexpr int kH1Stride4 = 256;
+  static_assert(4 * kH1Stride4 >= H && NKV <= 2, "h1 partials staged in Common's vec and xn");
+  __device__ bool gather_h1(uint32_t t, int l, int first4, int n4, float *dst) {
+    if (!gather4<(NKV * H / 4 + kT - 1) / kT>(slots(l, t, kOffH1, NKV * H), NKV * n4,
+                                              reinterpret_cast<float4 *>(dst), wt(),
+                                              cm.flags, [&](int p, int &s4, int &d4) {
+                                                const int g = p / n4, q = p % n4;
+                                                s4 = g * (H / 4) + first4 + q;
+                                                d4 = g * kH1Stride4 + q;
+                                              }))
+      return false;
+    for (int i = threadIdx.x; i < 4 * n4; i += kT) {
+      float v = dst[i];
+#pragma unroll
+      for (int g = 1; g < NKV; ++g) v += dst[g * 4 * kH1Stride4 + i];
+      dst[i] = v;
+    }
+    lds_barrier();
+    return true;
+  }
   __device__ Slots s_act(int l, uint32_t t) const { return slots(l, t, kOffAct, I); }
   __device__ Slots s_hid(int l, uint32_t t) const { return slots(l, t, kOffHid, kHidFloats); }
   // The down role's split of the layer output: CU r of ndown() owns rows
@@ -1340,19 +1373,26 @@ struct Roles {
 
   // ---- O projection ---------------------------------------------------------
   __device__ void run_o() {
-    const int u0 = split_begin(Sh::OUnits, nrole, rank);
-    PairRole<QD, kSlotsO, Sh::LO> ro;
-    ro.n = split_begin(Sh::OUnits, nrole, rank + 1) - u0;
+    // The role's CUs are split by KV group (group g: ranks [split_begin(nrole,
+    // NKV, g), split_begin(nrole, NKV, g + 1))); a group's CUs split every
+    // output row pair, each over the group's QDG columns.
+    constexpr int QDG = Sh::QDG;
+    int g = 0;
+    while (g + 1 < NKV && rank >= split_begin(nrole, NKV, g + 1)) ++g;
+    const int gbeg = split_begin(nrole, NKV, g), gn = split_begin(nrole, NKV, g + 1) - gbeg;
+    const int u0 = split_begin(Sh::OUnits, gn, rank - gbeg);
+    PairRole<QDG, kSlotsO, Sh::LO> ro;
+    ro.n = split_begin(Sh::OUnits, gn, rank - gbeg + 1) - u0;
     ro.units = reinterpret_cast<float4 *>(region);
     if (!fits(ro.n, ro.capacity())) return;
-    // Partial records in LDS as in the slot block: record (h, c) at
-    // (h * kAttnMaxChunks + c) * kRoleRecStride. The merge reads chunks
+    // The group's partial records in LDS: record (head 7g + j, c) at
+    // (j * kAttnMaxChunks + c) * kRoleRecStride. The merge reads chunks
     // beyond the token's count too (discarded by a select); the zero fill
     // keeps what they read finite until some token has gathered them.
-    float *parts = reinterpret_cast<float *>(region + Sh::LO * Sh::UnitBytes);
-    for (int i = threadIdx.x; i < Sh::PartFloats; i += kT) parts[i] = 0.f;
+    float *parts = reinterpret_cast<float *>(region + Sh::LO * Sh::OUnitBytes);
+    for (int i = threadIdx.x; i < Sh::PartFloatsG; i += kT) parts[i] = 0.f;
     auto rows = [&](int l) {
-      const float *base = layer(l).wo;
+      const float *base = layer(l).wo + g * QDG;
       return [=](int k, const float *&ra, const float *&rb) {
         ra = base + static_cast<size_t>(2 * (u0 + k)) * QD;
         rb = ra + QD;
@@ -1364,105 +1404,53 @@ struct Roles {
     om.take(2 * u0, 2 * ro.n, (2 * u0) & ~3, threadIdx.x, 0);
     loop(kRoleO, false, [&](uint32_t t, int l, int position) {
       const int C = attn_chunks(position + 1);
-      const Slots out = s_h1(l, t);
-      if (om.q >= 0) clear_quad(s_h1(l, t + 1), om);
-      // Residual rows [2 u0, 2 u0 + 2 n) of the layer input, in the float4s
-      // covering them (row r at cm.vec[r - 4 f4]).
+      const Slots out = s_h1(l, t, g);
+      if (om.q >= 0) clear_quad(s_h1(l, t + 1, g), om);
+      // Group 0 adds the residual: rows [2 u0, 2 u0 + 2 n) of the layer
+      // input, in the float4s covering them (row r at cm.vec[r - 4 f4]).
       const int f4 = (2 * u0) / 4, e4 = (2 * (u0 + ro.n) + 3) / 4;
       const int roff = 2 * u0 - 4 * f4;
-      if (!layer_input(t, l, f4, e4 - f4, cm.vec)) return false;
-      // The partial records of every head's C chunks; one pass covers nine
-      // chunks per head (later passes find their records already published).
+      if (g == 0 && !layer_input(t, l, f4, e4 - f4, cm.vec)) return false;
+      // The partial records of the group's heads over C chunks; one pass
+      // covers sixteen chunks.
       constexpr int kRec4 = kRoleRecStride / 4;
-      constexpr int kPer = (NQ * 9 * kRec4 + kT - 1) / kT;
-      static_assert(kPer <= 12, "partial gather pass");
+      constexpr int kPer = (GROUP * kAttnMaxChunks * kRec4 + kT - 1) / kT;
+      static_assert(kPer <= 8, "partial gather pass");
       const Slots in = s_part(l, t);
-      const int n4 = NQ * C * kRec4;
-      for (int base = 0; base < n4; base += kPer * kT) {
-        if (!gather4<kPer>(in, min(kPer * kT, n4 - base), reinterpret_cast<float4 *>(parts), wt(),
-                           cm.flags, [&](int p, int &s, int &d) {
-                             const int rec = (base + p) / kRec4, k = (base + p) % kRec4;
-                             const int h = rec / C, c = rec % C;
-                             s = (h * kAttnMaxChunks + c) * kRec4 + k;
-                             d = s;
-                           }))
-          return false;
-      }
+      const int n4 = GROUP * C * kRec4;
+      if (!gather4<kPer>(in, n4, reinterpret_cast<float4 *>(parts), wt(), cm.flags, [&](int p, int &s, int &d) {
+            const int rec = p / kRec4, k = p % kRec4;
+            const int j = rec / C, c = rec % C;
+            s = ((g * GROUP + j) * kAttnMaxChunks + c) * kRec4 + k;
+            d = (j * kAttnMaxChunks + c) * kRec4 + k;
+          }))
+        return false;
       clock.lap(2 * kRoleO);
-      // Merge, in the arithmetic of attn_merge, in two phases. Phase 1 (the
-      // last wave, lane h = head h): M = the largest of the C chunk maxima,
-      // w_c = 2^(m_c - M), den = the w_c l_c folded in chunk order; w (zero
-      // past C) and den go to LDS. Phase 2 (wave w: heads 2w and 2w + 1, one
-      // per half-wave; lane d of a half: dims d and d + 32): both numerators
-      // folded in chunk order from the broadcast weights, then one division
-      // per dim. Phase 2 is specialised on the exact C, so it carries no
-      // per-chunk test; its record reads are issued before the barrier.
-      static_assert(kHeadDim == kWave && NQ <= 2 * (kW - 1) && NQ <= kWave && kAttnMaxChunks == 16,
-                    "merge layout");
-      float *wsh = cm.top + 2 * kMaxRoleGrid - kAttnMaxChunks * NQ - NQ;  // [h][c], then den[h]
-      static_assert(2 * kMaxRoleGrid - kAttnMaxChunks * NQ - NQ >=
-                        2 * PairRole<QD, kSlotsO, Sh::LO>::capacity() + 4,
-                    "merge weights clear of the output stage");
-      if (wv == kW - 1) {
-        if (lane < NQ) {
-          const float *rec = parts + lane * kAttnMaxChunks * kRoleRecStride;
-          float mv[kAttnMaxChunks], lv[kAttnMaxChunks];
-#pragma unroll
-          for (int c = 0; c < kAttnMaxChunks; ++c) {
-            const float2 ml = *reinterpret_cast<const float2 *>(rec + c * kRoleRecStride);
-            mv[c] = ml.x;
-            lv[c] = ml.y;
-          }
-          float mx = -INFINITY;
-#pragma unroll
-          for (int c = 0; c < kAttnMaxChunks; ++c) mx = c < C ? fmaxf(mx, mv[c]) : mx;
-          float den = 0.f, w[kAttnMaxChunks];
-#pragma unroll
-          for (int c = 0; c < kAttnMaxChunks; ++c) {
-            w[c] = c < C ? exp2_fast(mv[c] - mx) : 0.f;
-            den = c < C ? fmaf(w[c], lv[c], den) : den;
-          }
-#pragma unroll
-          for (int c4 = 0; c4 < kAttnMaxChunks / 4; ++c4)
-            reinterpret_cast<float4 *>(wsh + lane * kAttnMaxChunks)[c4] =
-                make_float4(w[4 * c4], w[4 * c4 + 1], w[4 * c4 + 2], w[4 * c4 + 3]);
-          wsh[kAttnMaxChunks * NQ + lane] = den;
-        }
-        lds_barrier();
-      } else {
+      // Merge, in attn_merge's arithmetic: wave j takes the group's head j.
+      // Lane c of each 16-lane row (one per chunk place) forms the head's M
+      // (row16_max), w_c = 2^(m_c - M) (zero past C) and den (row16_sum of
+      // the products w_c l_c, in every lane); lane d then folds its dim's
+      // numerator over the chunks in order, w_c read from lane c. Specialised
+      // on the exact C; the record reads are issued first, and no step waits
+      // for another wave.
+      static_assert(kHeadDim == kWave && GROUP <= kW && kAttnMaxChunks == 16, "merge layout");
+      if (wv < GROUP) {
         auto merge = [&](auto c_tag) {
           constexpr int kC = decltype(c_tag)::value;
-          const int h = 2 * wv + (lane >> 5);
-          const int d = lane & 31;
-          const bool live = h < NQ;
-          const float *rec = parts + (live ? h : 0) * kAttnMaxChunks * kRoleRecStride;
-          float av[kC], bv[kC];
+          const float *rec = parts + wv * kAttnMaxChunks * kRoleRecStride;
+          float av[kC];
 #pragma unroll
-          for (int c = 0; c < kC; ++c) {
-            av[c] = rec[c * kRoleRecStride + 4 + d];
-            bv[c] = rec[c * kRoleRecStride + 4 + d + 32];
-          }
-          lds_barrier();
-          if (!live) return;
-          const float *wh = wsh + h * kAttnMaxChunks;
-          float w[kAttnMaxChunks];
+          for (int c = 0; c < kC; ++c) av[c] = rec[c * kRoleRecStride + 4 + lane];
+          const int c = lane & (kAttnMaxChunks - 1);
+          const float2 ml = *reinterpret_cast<const float2 *>(rec + c * kRoleRecStride);
+          const bool in = c < C;
+          const float mx = row16_max(in ? ml.x : -INFINITY);
+          const float w = in ? exp2_fast(ml.x - mx) : 0.f;
+          const float den = row16_sum(in ? __fmul_rn(w, ml.y) : 0.f);
+          float num = 0.f;
 #pragma unroll
-          for (int c4 = 0; c4 < (kC + 3) / 4; ++c4) {
-            const float4 q = reinterpret_cast<const float4 *>(wh)[c4];
-            w[4 * c4] = q.x;
-            w[4 * c4 + 1] = q.y;
-            w[4 * c4 + 2] = q.z;
-            w[4 * c4 + 3] = q.w;
-          }
-          const float den = wsh[kAttnMaxChunks * NQ + h];
-          float num0 = 0.f, num1 = 0.f;
-#pragma unroll
-          for (int c = 0; c < kC; ++c) {
-            num0 = fmaf(w[c], av[c], num0);
-            num1 = fmaf(w[c], bv[c], num1);
-          }
-          cm.xn[h * kHeadDim + d] = num0 / den;
-          cm.xn[h * kHeadDim + d + 32] = num1 / den;
+          for (int k = 0; k < kC; ++k) num = fmaf(read_lane(w, k), av[k], num);
+          cm.xn[wv * kHeadDim + lane] = num / den;
         };
         switch (C) {
 #define QD_MERGE_CASE(n) \
@@ -1478,15 +1466,18 @@ struct Roles {
         }
       }
       lds_barrier();
-      float4 xv[PairSlots<QD>::NJ];
-      load_pair_operand<QD>(Lds{cm.xn}, xv);
+      float4 xv[PairSlots<QDG>::NJ];
+      load_pair_operand<QDG>(Lds{cm.xn}, xv);
       float *stage = cm.top;  // row 2 u0 + j at stage[j + roff]
       clock.mark(0);
       ro.compute(xv,
-                 [&](int k) { return make_float4(cm.vec[roff + 2 * k], cm.vec[roff + 2 * k + 1], 0.f, 0.f); },
+                 [&](int k) {
+                   return g == 0 ? make_float4(cm.vec[roff + 2 * k], cm.vec[roff + 2 * k + 1], 0.f, 0.f)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+                 },
                  [&](int k, float sa, float sb, float4 c) {
-                   stage[2 * k + roff] = c.x + sa;
-                   stage[2 * k + 1 + roff] = c.y + sb;
+                   stage[2 * k + roff] = g == 0 ? c.x + sa : sa;
+                   stage[2 * k + 1 + roff] = g == 0 ? c.y + sb : sb;
                  },
                  [&] { clock.mark(1); });
       lds_barrier();
@@ -1531,7 +1522,7 @@ struct Roles {
       float *stage = cm.top;  // unit u0 + k at stage[k + (u0 & 3)]
       float4 gv[NJ];
       load_pair_gain<H>(layer(l).mlp_norm, gv);
-      if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), 0, H / 4, cm.vec, wt(), cm.flags)) return false;
+      if (!gather_h1(t, l, 0, H / 4, cm.vec)) return false;
       clock.lap(2 * kRoleGate);
       float4 xv[NJ];
       const float inv = norm_scale(load_pair_operand_gain<H>(Lds{cm.vec}, gv, xv), H, a.eps);
@@ -1583,7 +1574,7 @@ struct Roles {
     loop(kRoleDown, true, [&](uint32_t t, int l, int position) {
       const Slots out = s_hid(l, t);
       if (pub) s_hid(l, t + 1).clear4(seg4 + threadIdx.x);
-      if (!gather4c<(H / 4 + kT - 1) / kT>(s_h1(l, t), hb4, hn4, cm.vec, wt(), cm.flags)) return false;
+      if (!gather_h1(t, l, hb4, hn4, cm.vec)) return false;
       // This wave's slice of the activation, straight into registers.
       float4 xa[DownRole<I>::kNsHi];
       bool ok = true;
@@ -1724,15 +1715,17 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
   if (hidden != 896 || inter != 4864 || heads != 14 || kv_heads != 2) return false;
   if (grid > kMaxRoleGrid || max_length < 1) return false;
   // Units per role, their capacity per CU (LDS + register slots) and bytes.
-  const int units[4] = {Qwen::QkvUnits, Qwen::OUnits, inter, hidden};
+  // O: each of the KV groups covers every row pair (Roles::run_o).
+  const int units[4] = {Qwen::QkvUnits, kv_heads * Qwen::OUnits, inter, hidden};
   const int cap[4] = {Qwen::LQ + kW * kSlotsQ, Qwen::LO + kW * kSlotsO, Qwen::LG + kW * kSlotsG,
                       DownRole<4864>::capacity()};
-  const double bytes[4] = {double(units[0]) * Qwen::UnitBytes, double(units[1]) * Qwen::UnitBytes,
+  const double bytes[4] = {double(units[0]) * Qwen::UnitBytes, double(units[1]) * Qwen::OUnitBytes,
                            double(units[2]) * Qwen::UnitBytes, double(units[3]) * Qwen::RowBytes};
   const double total = bytes[0] + bytes[1] + bytes[2] + bytes[3];
   // CUs a role needs to hold its units: the gate role splits whole float4s
   // of the activation (4 units), the others single units.
   auto need_of = [&](int r) {
+    if (r == 1) return kv_heads * ((Qwen::OUnits + cap[1] - 1) / cap[1]);  // per group
     const int g = r == 2 ? 4 : 1;
     return ((units[r] + g - 1) / g + cap[r] / g - 1) / (cap[r] / g);
   };
