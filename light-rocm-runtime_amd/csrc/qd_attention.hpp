@@ -56,7 +56,7 @@ __device__ __forceinline__ void attn_head_window(K4 k4, V v, const float4 (&q)[k
     float s = 0.f;
 #pragma unroll
     for (int d4 = 0; d4 < kHeadDim / 4; ++d4) s = fma4(kr[d4], q[d4], s);
-    const float sv = lane <= last ? s * kScoreScaleLog2 : -INFINITY;
+    const float sv = lane <= last ? __fmul_rn(s, kScoreScaleLog2) : -INFINITY;
     const float m_new = fmaxf(m, wave_max(sv));
     const float p = m_new == -INFINITY ? 0.f : exp2_fast(sv - m_new);
     const float corr = m_new == -INFINITY ? 1.f : exp2_fast(m - m_new);

@@ -99,6 +99,15 @@ __device__ __forceinline__ float wave_sum_multi(const float (&in)[N]) {
   return r;
 }
 
+// Rotary rotation of the pair (a, b) by (c, s): (a c - b s, b c + a s), each
+// half as one rounded product and one fused multiply-add, so every kernel
+// that rotates gets the same bits whatever its compiler would contract.
+__device__ __forceinline__ void rope_rotate(float a, float b, float c, float s, float &first,
+                                            float &second) {
+  first = fmaf(a, c, -__fmul_rn(b, s));
+  second = fmaf(b, c, __fmul_rn(a, s));
+}
+
 // Max and sum over each row of 16 lanes, the result in every lane of the
 // row: wave_max's and wave_sum's first four steps. The sum groups the lanes
 // as a pairwise tree ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + (v6 + v7)), and

@@ -560,6 +560,8 @@ struct qd_engine {
     ra.epoch = epoch << qd::kTagSeqBits;
     ra.spin_limit = spin_limit;
     for (int r = 0; r < qd::kRoleCount; ++r) ra.role_end[r] = plan.end[r];
+    for (int r = 0; r < 3; ++r) ra.group_cus[r] = plan.group_cus[r];
+    ra.xcd_place = plan.xcd_place;
     check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
     // Every hand-off slot starts empty (all bits set).
     check(hipMemsetAsync(roles_slots, 0xFF, roles_slot_bytes, stream), "memset");
@@ -576,6 +578,11 @@ struct qd_engine {
       fail(QD_ERROR_RUNTIME,
            "resident role plan gives a CU more weight units than it holds on chip (error word 0x%x)",
            err);
+    if (err & qd::kResidentPlacement)
+      fail(QD_ERROR_RUNTIME,
+           "resident kernel: a workgroup ran on another XCD than workgroup b %% %d, which the "
+           "role placement assumes (error word 0x%x)",
+           qd::kXcds, err);
     if (err & qd::kResidentWaitGaveUp)
       fail(QD_ERROR_DEVICE_FAULT,
            "resident kernel: a hand-off wait gave up after %u polls without its producer "

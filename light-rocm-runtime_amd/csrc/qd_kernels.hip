@@ -78,8 +78,8 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
       if (head < nq + nkv) {
         const float c = rope_cos[position * kRotary + i];
         const float s = rope_sin[position * kRotary + i];
-        const float first = a * c - b * s;
-        const float second = b * c + a * s;
+        float first, second;
+        rope_rotate(a, b, c, s, first, second);
         if (head < nq) {
           q[ra] = first;
           q[rb] = second;

@@ -195,8 +195,8 @@ __global__ __launch_bounds__(kBlock) void rope_kv_rows_kernel(float *__restrict_
       const int a = head * kHeadDim + i, b = a + kRotary;
       const float c = rope_cos[p * kRotary + i], s = rope_sin[p * kRotary + i];
       const float x0 = row[a], x1 = row[b];
-      const float first = x0 * c - x1 * s;
-      const float second = x1 * c + x0 * s;
+      float first, second;
+      rope_rotate(x0, x1, c, s, first, second);
       row[a] = first;
       row[b] = second;
       if (head >= nq) {

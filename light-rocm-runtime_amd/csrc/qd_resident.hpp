@@ -15,21 +15,29 @@ namespace qd {
 // sub-phases (K/V staging, math, emit) -> 17 entries.
 constexpr int kResidentStages = 17;
 
-// Role-split resident kernel: one 512-thread workgroup per CU; workgroups
-// [0, end[kRoleQkv]) compute QKV, [end[kRoleQkv], end[kRoleAttn]) attention,
-// then O, gate/up and down.
+// Role-split resident kernel: one 512-thread workgroup per CU. In placement
+// order, positions [0, end[kRoleQkv]) compute QKV, [end[kRoleQkv],
+// end[kRoleAttn]) attention, then O, gate/up and down; the QKV, attention and
+// O ranks come in KV-group blocks of group_cus[] each. Workgroup b takes
+// position b, or, with xcd_place, the position that puts group g's QKV,
+// attention and O CUs on XCD g (Roles' placement()).
 constexpr int kRoleThreads = 512;
 constexpr int kMaxRoleGrid = 512;
 enum ResidentRole : int { kRoleQkv = 0, kRoleAttn, kRoleO, kRoleGate, kRoleDown, kRoleCount };
 struct RolePlan {
-  int end[kRoleCount];  // cumulative workgroup ends per role
+  int end[kRoleCount];  // cumulative role ends in placement order (ResidentArgs::role_end)
+  int group_cus[3];     // QKV, attention and O CUs per KV group (each role has nkv times as many)
+  int xcd_place;        // 1: KV group g's QKV, attention and O CUs all run on XCD g
 };
+// XCDs of the device; workgroup b of a launch runs on XCD b % kXcds.
+constexpr int kXcds = 8;
 
 // Bits of the kernel's error word (zero at launch). A CU that raises one
 // stops; the CUs waiting on it give up after their own bounded polls, so
 // every workgroup exits.
 constexpr uint32_t kResidentWaitGaveUp = 1u;    // a hand-off poll exhausted its spin limit
 constexpr uint32_t kResidentPlanOverfill = 2u;  // the host plan gave a CU more units than it holds
+constexpr uint32_t kResidentPlacement = 4u;     // a workgroup ran on another XCD than the plan placed it on
 // Polls before a hand-off wait gives up (several milliseconds; a healthy
 // hand-off takes a few microseconds).
 constexpr uint32_t kResidentSpinLimit = 1u << 21;
@@ -69,6 +77,8 @@ struct ResidentArgs {
   uint32_t epoch;               // launch epoch << kTagSeqBits, never 0
   uint32_t spin_limit;          // polls before a wait gives up
   int role_end[kRoleCount];     // RolePlan::end
+  int group_cus[3];             // RolePlan::group_cus
+  int xcd_place;                // RolePlan::xcd_place
 };
 
 // Argmax partial tags: epoch << kTagSeqBits | (token * (5 * layers + 1) + stage + 1).

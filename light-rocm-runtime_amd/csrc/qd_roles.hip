@@ -253,23 +253,37 @@ __device__ bool gather(const TagVec &src, uint32_t first, int n, uint32_t tag, f
 // One (layer, token parity) block of hand-off slots: plain floats with
 // device-scope access, kSlotEmpty until written; bounds-checked by the
 // buffer descriptor.
+// Hand-off slots. Loads are sc1 (served by the reader's L2 within its XCD,
+// coherently across XCDs); stores are sc1 (written through to memory) unless
+// the slots are XCD-local: every writer and reader of them runs on one XCD,
+// whose L2 is then the point of coherence and plain stores suffice.
 struct Slots {
   __amdgpu_buffer_rsrc_t r;
-  __device__ Slots(float *base, uint32_t floats)
-      : r(__builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(floats * 4u), kRsrcWord3)) {}
-  __device__ void put(uint32_t i, float v) const {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, i * 4u, 0, kPolicySc1);
+  bool local;
+  __device__ Slots(float *base, uint32_t floats, bool xcd_local = false)
+      : r(__builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(floats * 4u), kRsrcWord3)),
+        local(xcd_local) {}
+  __device__ void st32(uint32_t i, uint32_t v) const {
+    if (local)
+      __builtin_amdgcn_raw_buffer_store_b32(v, r, i * 4u, 0, 0);
+    else
+      __builtin_amdgcn_raw_buffer_store_b32(v, r, i * 4u, 0, kPolicySc1);
   }
-  __device__ void clear(uint32_t i) const {
-    __builtin_amdgcn_raw_buffer_store_b32(kSlotEmpty, r, i * 4u, 0, kPolicySc1);
+  __device__ void st128(uint32_t i4, u32x4 v) const {
+    if (local)
+      __builtin_amdgcn_raw_buffer_store_b128(v, r, i4 * 16u, 0, 0);
+    else
+      __builtin_amdgcn_raw_buffer_store_b128(v, r, i4 * 16u, 0, kPolicySc1);
   }
+  __device__ void put(uint32_t i, float v) const { st32(i, __builtin_bit_cast(unsigned, v)); }
+  __device__ void clear(uint32_t i) const { st32(i, kSlotEmpty); }
   __device__ void put4(uint32_t i4, float4 v) const {
     const f32x4 x = {v.x, v.y, v.z, v.w};
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, i4 * 16u, 0, kPolicySc1);
+    st128(i4, __builtin_bit_cast(u32x4, x));
   }
   __device__ void clear4(uint32_t i4) const {
     const u32x4 x = {kSlotEmpty, kSlotEmpty, kSlotEmpty, kSlotEmpty};
-    __builtin_amdgcn_raw_buffer_store_b128(x, r, i4 * 16u, 0, kPolicySc1);
+    st128(i4, x);
   }
   __device__ void st(uint32_t i, float v) const { put(i, v); }
   __device__ void st4(uint32_t i4, float4 v) const { put4(i4, v); }
@@ -824,12 +838,16 @@ struct Roles {
   // (token t + 1's): every CU has finished token t - 1, whose values it
   // held, before any CU starts token t (each waits for the argmax), and the
   // clears are complete (vmcnt) before the writer's next gather returns.
-  __device__ Slots slots(int l, uint32_t t, int off, int n) const {
+  __device__ Slots slots(int l, uint32_t t, int off, int n, bool xcd_local = false) const {
     return Slots(a.slots + (static_cast<size_t>(l) * 2 + (t & 1u)) * kSlotFloats + off,
-                 static_cast<uint32_t>(n));
+                 static_cast<uint32_t>(n), xcd_local);
   }
-  __device__ Slots s_qkv(int l, uint32_t t) const { return slots(l, t, kOffQkv, QD + 2 * KVD); }
-  __device__ Slots s_part(int l, uint32_t t) const { return slots(l, t, kOffPart, Sh::PartFloats); }
+  // The QKV outputs and the attention records stay inside KV group g's
+  // CUs, which the XCD placement puts on XCD g: XCD-local slots then.
+  __device__ Slots s_qkv(int l, uint32_t t) const { return slots(l, t, kOffQkv, QD + 2 * KVD, a.xcd_place); }
+  __device__ Slots s_part(int l, uint32_t t) const {
+    return slots(l, t, kOffPart, Sh::PartFloats, a.xcd_place);
+  }
   // Group g's partial of the attention block's output: the O rows over
   // group g's heads (group 0's with the residual added); h1 is their sum in
   // group order.
@@ -1125,17 +1143,27 @@ struct Roles {
 
   // ---- QKV ------------------------------------------------------------------
   __device__ void run_qkv() {
-    const int u0 = split_begin(Sh::QkvUnits, nrole, rank);
+    // The role's CUs come in KV-group blocks of group_cus[0]. Group g's
+    // units, in order: its G query heads, then K head g, then V head g (32
+    // units = one packed head each; unit u is rows (u / 32) * 64 + u % 32
+    // and 32 further on); each of the group's CUs takes a run of them.
+    const int gq = a.group_cus[0];
+    const int g = rank / gq, rr = rank % gq;
+    constexpr int GU = (GROUP + 2) * kRotary;
+    const int j0 = split_begin(GU, gq, rr);
     PairRole<H, kSlotsQ, Sh::LQ> rq;
-    rq.n = split_begin(Sh::QkvUnits, nrole, rank + 1) - u0;
+    rq.n = split_begin(GU, gq, rr + 1) - j0;
     rq.units = reinterpret_cast<float4 *>(region);
     if (!fits(rq.n, rq.capacity())) return;
+    // Packed head of the group's local head lh (0..G-1 query, G: K, G+1: V).
+    auto head_of = [&](int lh) { return lh < GROUP ? GROUP * g + lh : (lh == GROUP ? NQ + g : NQ + NKV + g); };
+    auto unit_of = [&](int j) { return head_of(j / kRotary) * kRotary + j % kRotary; };
     float4 *q_bias = reinterpret_cast<float4 *>(region + Sh::LQ * Sh::UnitBytes);
     float4 *q_cs = q_bias + Sh::BiasF4;
     auto rows = [&](int l) {
       const float *base = layer(l).wqkv;
       return [=](int k, const float *&ra, const float *&rb) {
-        const int u = u0 + k;
+        const int u = unit_of(j0 + k);
         const int row = (u / kRotary) * kHeadDim + u % kRotary;
         ra = base + static_cast<size_t>(row) * H;
         rb = ra + static_cast<size_t>(kRotary) * H;
@@ -1158,19 +1186,20 @@ struct Roles {
       dma16<kPolicyNt>(lane < R4 ? c4 + lane : (lane < 2 * R4 ? s4 + (lane - R4) : c4), q_cs);
     };
     auto pre_regs = [&](int l) { rq.prefetch_regs(rows(l)); };
-    // Unit u's rows land at (u / 32) * 64 + u % 32 and 32 further on
-    // (packed head u / 32: the query heads, then the K and V heads), so this
-    // CU's slots are two runs per packed head it touches; thread i owns
+    // Each local head lh this CU touches is two runs of its packed head's
+    // slots (rows ib.. and 32 + ib..), staged at 64 (lh - lh0); thread i owns
     // float4 i of those runs taken in order (tagged with the packed head).
-    const int sbase = (u0 / kRotary) * kHeadDim;
+    const int lh0 = j0 / kRotary;
     OutMap om;
     {
       int item = threadIdx.x;
-      for (int h = u0 / kRotary; h <= (u0 + rq.n - 1) / kRotary; ++h) {
-        const int ib = max(u0, h * kRotary) - h * kRotary;
-        const int ie = min(u0 + rq.n, (h + 1) * kRotary) - h * kRotary;
-        item -= om.take(h * kHeadDim + ib, ie - ib, sbase, item, h);
-        item -= om.take(h * kHeadDim + kRotary + ib, ie - ib, sbase, item, h);
+      for (int lh = lh0; lh <= (j0 + rq.n - 1) / kRotary; ++lh) {
+        const int h = head_of(lh);
+        const int sb = h * kHeadDim - kHeadDim * (lh - lh0);
+        const int ib = max(j0, lh * kRotary) - lh * kRotary;
+        const int ie = min(j0 + rq.n, (lh + 1) * kRotary) - lh * kRotary;
+        item -= om.take(h * kHeadDim + ib, ie - ib, sb, item, h);
+        item -= om.take(h * kHeadDim + kRotary + ib, ie - ib, sb, item, h);
       }
     }
     loop(kRoleQkv, false, [&](uint32_t t, int l, int position) {
@@ -1190,19 +1219,18 @@ struct Roles {
       const Coherent vcache(kv_layer(a.v_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
       float *stage = cm.top;
       rq.compute(xv, [&](int k) {
-        const int u = u0 + k;
+        const int u = unit_of(j0 + k);
         const int ra = (u / kRotary) * kHeadDim + u % kRotary;
         return make_float4(bias[ra], bias[ra + kRotary], cs[u % kRotary], cs[kRotary + u % kRotary]);
       }, [&](int k, float sa, float sb, float4 c) {
-        const int u = u0 + k;
-        const int head = u / kRotary;
-        const int slot = head * kHeadDim + u % kRotary - sbase;
+        const int j = j0 + k;
+        const int head = head_of(j / kRotary);
+        const int slot = kHeadDim * (j / kRotary - lh0) + j % kRotary;
         const float x0 = fmaf(sa, inv, c.x);
         const float x1 = fmaf(sb, inv, c.y);
         if (head < NQ + NKV) {
           const float cv = c.z, sv = c.w;
-          stage[slot] = x0 * cv - x1 * sv;
-          stage[slot + kRotary] = x1 * cv + x0 * sv;
+          rope_rotate(x0, x1, cv, sv, stage[slot], stage[slot + kRotary]);
         } else {
           stage[slot] = x0;
           stage[slot + kRotary] = x1;
@@ -1258,39 +1286,40 @@ struct Roles {
 
   __device__ void run_attn() {
     AttnRegion &ar = *reinterpret_cast<AttnRegion *>(region);
+    // The role's CUs come in KV-group blocks of group_cus[1]: CU rr of group
+    // g takes the group's chunks rr, rr + group_cus[1], ...
+    const int na = a.group_cus[1];
+    const int g = rank / na, rr = rank % na;
     auto pre_lds = [&](int l, int position) {
       const int length = position + 1;
       const int chunks = attn_chunks(length), cl = attn_chunk_len(length);
-      if (rank >= NKV * chunks || position >= a.capacity) return;
-      const int g = rank / chunks, c = rank % chunks;
-      const int begin = c * cl, end = min(length, begin + cl);
+      if (rr >= chunks || position >= a.capacity) return;
+      const int begin = rr * cl, end = min(length, begin + cl);
       attn_dma(l, g, begin, min(end, begin + kAttnCap), ar);
     };
     auto pre_regs = [](int) {};
     loop(kRoleAttn, false, [&](uint32_t t, int l, int position) {
       const int length = position + 1;
       const int chunks = attn_chunks(length), cl = attn_chunk_len(length);
-      const int units = NKV * chunks;
       const Slots in = s_qkv(l, t), out = s_part(l, t);
       // Record (h, c) is kRoleRecStride floats at (h * kAttnMaxChunks + c) *
       // kRoleRecStride: whole float4s.
       constexpr int kRec4 = kRoleRecStride / 4;
       {
-        // The records token t + 1 reads (its own chunk count), spread over
-        // the role's CUs like its units. This holds however the count moves:
-        // it drops when the chunk length grows (context 1024 -> 1025) and
-        // regrows later, which leaves older records in slots beyond it.
+        // The group's records token t + 1 reads (its own chunk count),
+        // spread over the group's CUs like its chunks. This holds however the
+        // count moves: it drops when the chunk length grows (context 1024 ->
+        // 1025) and regrows later, which leaves older records in slots beyond
+        // it.
         const Slots next = s_part(l, t + 1);
         const int chunks_next = attn_chunks(length + 1);
-        for (int u = rank; u < NKV * chunks_next; u += nrole) {
-          const int g = u / chunks_next, c = u % chunks_next;
+        for (int c = rr; c < chunks_next; c += na) {
           for (int e = threadIdx.x; e < GROUP * kRec4; e += kT)
             next.clear4(((g * GROUP + e / kRec4) * kAttnMaxChunks + c) * kRec4 + e % kRec4);
         }
       }
       bool first_unit = true;
-      for (int u = rank; u < units; u += nrole) {
-        const int g = u / chunks, c = u % chunks;
+      for (int c = rr; c < chunks; c += na) {
         const int begin = c * cl;
         const int end = min(length, begin + cl);
         const bool has_new = position >= begin && position < end;
@@ -1373,16 +1402,14 @@ struct Roles {
 
   // ---- O projection ---------------------------------------------------------
   __device__ void run_o() {
-    // The role's CUs are split by KV group (group g: ranks [split_begin(nrole,
-    // NKV, g), split_begin(nrole, NKV, g + 1))); a group's CUs split every
-    // output row pair, each over the group's QDG columns.
+    // The role's CUs come in KV-group blocks of group_cus[2]; a group's CUs
+    // split every output row pair, each over the group's QDG columns.
     constexpr int QDG = Sh::QDG;
-    int g = 0;
-    while (g + 1 < NKV && rank >= split_begin(nrole, NKV, g + 1)) ++g;
-    const int gbeg = split_begin(nrole, NKV, g), gn = split_begin(nrole, NKV, g + 1) - gbeg;
-    const int u0 = split_begin(Sh::OUnits, gn, rank - gbeg);
+    const int gn = a.group_cus[2];
+    const int g = rank / gn, rr = rank % gn;
+    const int u0 = split_begin(Sh::OUnits, gn, rr);
     PairRole<QDG, kSlotsO, Sh::LO> ro;
-    ro.n = split_begin(Sh::OUnits, gn, rank - gbeg + 1) - u0;
+    ro.n = split_begin(Sh::OUnits, gn, rr + 1) - u0;
     ro.units = reinterpret_cast<float4 *>(region);
     if (!fits(ro.n, ro.capacity())) return;
     // The group's partial records in LDS: record (head 7g + j, c) at
@@ -1675,10 +1702,41 @@ __device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank
   if constexpr (kRole == kRoleDown) r.run_down();
 }
 
+// Placement position of workgroup b. With xcd_place, XCD x < nkv holds KV
+// group x's QKV, attention and O CUs as its first G = sum(group_cus)
+// workgroups (b / kXcds < G), in that order; the other workgroups take the
+// gate/up and down positions in workgroup order.
+__device__ __forceinline__ int placement(const ResidentArgs &a, int b) {
+  if (!a.xcd_place) return b;
+  const int n0 = a.group_cus[0], n1 = a.group_cus[1], n2 = a.group_cus[2];
+  const int G = n0 + n1 + n2;
+  const int x = b % kXcds, i = b / kXcds;
+  if (x < a.nkv && i < G) {
+    if (i < n0) return x * n0 + i;
+    if (i < n0 + n1) return a.nkv * n0 + x * n1 + (i - n0);
+    return a.nkv * (n0 + n1) + x * n2 + (i - n0 - n1);
+  }
+  int before = 0;  // group workgroups with a lower index
+  for (int xx = 0; xx < a.nkv; ++xx) before += min(G, b > xx ? (b - xx + kXcds - 1) / kXcds : 0);
+  return a.nkv * G + (b - before);
+}
+
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xFu;
+}
+
 template <int H, int I, int NQ, int NKV, bool kProfile>
 __global__ __launch_bounds__(kT, 1) void roles_kernel(ResidentArgs a) {
   const void *kernarg = (const void *)__builtin_amdgcn_kernarg_segment_ptr();
-  const int b = blockIdx.x;
+  // A workgroup placed for an XCD it does not run on stops (its waiting
+  // peers give up): the intra-XCD hand-offs rely on the placement.
+  if (a.xcd_place && xcc_id() != blockIdx.x % kXcds) {
+    if (threadIdx.x == 0) atomicOr(a.error, kResidentPlacement);
+    return;
+  }
+  const int b = placement(a, blockIdx.x);
   int role = 0;
   while (role < kRoleCount - 1 && b >= a.role_end[role]) ++role;
   const int rbeg = role ? a.role_end[role - 1] : 0;
@@ -1724,8 +1782,11 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
   const double total = bytes[0] + bytes[1] + bytes[2] + bytes[3];
   // CUs a role needs to hold its units: the gate role splits whole float4s
   // of the activation (4 units), the others single units.
+  // QKV and O work in KV groups (Roles::run_qkv, run_o): each group's CUs
+  // hold the group's share.
   auto need_of = [&](int r) {
-    if (r == 1) return kv_heads * ((Qwen::OUnits + cap[1] - 1) / cap[1]);  // per group
+    if (r == 0) return kv_heads * ((units[0] / kv_heads + cap[0] - 1) / cap[0]);
+    if (r == 1) return kv_heads * ((Qwen::OUnits + cap[1] - 1) / cap[1]);
     const int g = r == 2 ? 4 : 1;
     return ((units[r] + g - 1) / g + cap[r] / g - 1) / (cap[r] / g);
   };
@@ -1734,8 +1795,9 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
   // One attention CU per (KV head, chunk) unit of the longest context, or
   // as many as the weight roles leave (an attention CU then takes several
   // units, the later ones staged after its query arrives).
-  const int n_attn = std::min(kv_heads * attn_chunks(max_length), grid - floor_weights);
-  if (n_attn < 1) return false;
+  int n_attn = std::min(kv_heads * attn_chunks(max_length), grid - floor_weights);
+  n_attn -= n_attn % kv_heads;  // whole KV groups
+  if (n_attn < kv_heads) return false;
   const int rest = grid - n_attn;
   int n[4], used = 0;
   for (int r = 0; r < 4; ++r) {
@@ -1765,6 +1827,25 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
     n[pick] += used < rest ? 1 : -1;
     used += used < rest ? 1 : -1;
   }
+  // QKV and O in whole KV groups; the gate role gives or takes the rest.
+  for (int r = 0; r < 2; ++r) {
+    const int d = (kv_heads - n[r] % kv_heads) % kv_heads;
+    if (d == 0) continue;
+    if (n[2] - d >= need_of(2)) {
+      n[r] += d;
+      n[2] -= d;
+    } else if (n[r] - (kv_heads - d) >= need_of(r)) {
+      n[r] -= kv_heads - d;
+      n[2] += kv_heads - d;
+    } else {
+      return false;
+    }
+  }
+  plan->group_cus[0] = n[0] / kv_heads;
+  plan->group_cus[1] = n_attn / kv_heads;
+  plan->group_cus[2] = n[1] / kv_heads;
+  plan->xcd_place = grid % kXcds == 0 && kv_heads <= kXcds &&
+                    plan->group_cus[0] + plan->group_cus[1] + plan->group_cus[2] <= grid / kXcds;
   plan->end[kRoleQkv] = n[0];
   plan->end[kRoleAttn] = n[0] + n_attn;
   plan->end[kRoleO] = plan->end[kRoleAttn] + n[1];
