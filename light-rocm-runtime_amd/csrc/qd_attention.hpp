@@ -31,6 +31,31 @@ constexpr float kScoreScaleLog2 = 0.18033688011112042f;  // log2(e) / 8
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Probabilities of a block handed from lane u (position u) to every lane,
+// four at a time: get(u4) returns those of positions 4 u4 .. 4 u4 + 3.
+// Lane reads (v_readlane), for a kernel without LDS to spare.
+struct PLanes {
+  float p;
+  __device__ void put(float v) { p = v; }
+  __device__ float4 get(int u4) const {
+    return make_float4(read_lane(p, 4 * u4), read_lane(p, 4 * u4 + 1), read_lane(p, 4 * u4 + 2),
+                       read_lane(p, 4 * u4 + 3));
+  }
+};
+// The same through 64 floats of the wave's own LDS: every lane writes its
+// probability, then reads them as float4 broadcasts (no VALU per position).
+struct PLds {
+  float *buf;
+  __device__ void put(float v) {
+    buf[lane_id()] = v;
+    // Lanes of the wave read each other's words: order the writes first.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  __device__ float4 get(int u4) const { return reinterpret_cast<const float4 *>(buf)[u4]; }
+};
+
 // One query head over the positions [0, n) of a chunk, computed by one wave;
 // the resident role kernel (K/V staged in LDS) and the stream-ordered kernel
 // (K/V read from the cache) both run it, so their partials are bit-identical.
@@ -41,11 +66,12 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // sum is added to the rescaled running acc. k4(d4, j) returns float4 d4 of
 // position j's K row and v(j, d) element d of its V row; both are called
 // only with j < n (the positions of a partial last block read row n - 1,
-// with their probabilities masked to 0). q holds the head's 64 query values;
-// (m, l, acc) carry the state across calls, so a chunk may be walked in
-// windows whose lengths are multiples of 64.
-template <typename K4, typename V>
-__device__ __forceinline__ void attn_head_window(K4 k4, V v, const float4 (&q)[kHeadDim / 4], int n,
+// with their probabilities masked to 0). pb hands the probabilities between
+// lanes (PLanes or PLds: same values, same arithmetic). q holds the head's
+// 64 query values; (m, l, acc) carry the state across calls, so a chunk may
+// be walked in windows whose lengths are multiples of 64.
+template <typename K4, typename V, typename PB>
+__device__ __forceinline__ void attn_head_window(K4 k4, V v, PB pb, const float4 (&q)[kHeadDim / 4], int n,
                                                  float &m, float &l, float &acc) {
   const int lane = lane_id();
   for (int base = 0; base < n; base += kWave) {
@@ -62,10 +88,16 @@ __device__ __forceinline__ void attn_head_window(K4 k4, V v, const float4 (&q)[k
     const float corr = m_new == -INFINITY ? 1.f : exp2_fast(m - m_new);
     l = fmaf(l, corr, wave_sum(p));
     m = m_new;
+    pb.put(p);
     float a[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kWave; ++u)
-      a[u & 3] = fmaf(read_lane(p, u), v(base + min(u, last), lane), a[u & 3]);
+    for (int u4 = 0; u4 < kWave / 4; ++u4) {
+      const float4 pp = pb.get(u4);
+      a[0] = fmaf(pp.x, v(base + min(4 * u4, last), lane), a[0]);
+      a[1] = fmaf(pp.y, v(base + min(4 * u4 + 1, last), lane), a[1]);
+      a[2] = fmaf(pp.z, v(base + min(4 * u4 + 2, last), lane), a[2]);
+      a[3] = fmaf(pp.w, v(base + min(4 * u4 + 3, last), lane), a[3]);
+    }
     acc = fmaf(acc, corr, (a[0] + a[1]) + (a[2] + a[3]));
   }
 }

@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kWave) void attn_partial_kernel(
       [&](int d4, int j) {
         return reinterpret_cast<const float4 *>(kb + static_cast<size_t>(j) * kv_dim)[d4];
       },
-      [&](int j, int d) { return vb[static_cast<size_t>(j) * kv_dim + d]; }, qv, n, m, l, acc);
+      [&](int j, int d) { return vb[static_cast<size_t>(j) * kv_dim + d]; }, PLanes{}, qv, n, m, l, acc);
   float *rec = part + (h * kAttnMaxChunks + chunk) * kPartStride;
   rec[2 + threadIdx.x] = acc;
   if (threadIdx.x == 0) {

@@ -1368,23 +1368,19 @@ struct Roles {
             for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
               q[d4] = reinterpret_cast<const float4 *>(ar.qs + wv * kHeadDim)[d4];
             attn_head_window([&](int d4, int j) { return ar.kt[d4 * kAttnCap + j]; },
-                             [&](int j, int d) { return ar.vr[j * kHeadDim + d]; }, q, we - wb, m,
-                             lsum, acc);
+                             [&](int j, int d) { return ar.vr[j * kHeadDim + d]; }, PLds{cm.xn + wv * kWave},
+                             q, we - wb, m, lsum, acc);
           }
         }
         clock.mark(1);
-        // Record: m, l, two pad words, acc[64]; staged, then stored as
-        // whole float4s.
-        float *stage = cm.top;
+        // Each head's wave stores its own record (m, l, two pad words,
+        // acc[64]) word by word: one contiguous 256-byte store of acc and one
+        // of the head words. A reader takes a float4 once none of its words
+        // is kSlotEmpty, so it never sees a partly written one.
         if (wv < GROUP) {
-          stage[wv * kRoleRecStride + 4 + lane] = acc;
-          if (lane < 4) stage[wv * kRoleRecStride + lane] = lane == 0 ? m : lane == 1 ? lsum : 0.f;
-        }
-        lds_barrier();
-        if (threadIdx.x < GROUP * kRec4) {
-          const int j = threadIdx.x / kRec4, q = threadIdx.x % kRec4;
-          out.put4(((g * GROUP + j) * kAttnMaxChunks + c) * kRec4 + q,
-                   reinterpret_cast<const float4 *>(stage)[j * kRec4 + q]);
+          const uint32_t rec = ((g * GROUP + wv) * kAttnMaxChunks + c) * kRoleRecStride;
+          out.put(rec + 4 + lane, acc);
+          if (lane < 4) out.put(rec + lane, lane == 0 ? m : lane == 1 ? lsum : 0.f);
         }
         clock.mark(2);
         first_unit = false;
