@@ -100,9 +100,10 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
 }
 
 // Split-KV decode attention partials (qd_attention.hpp): one wave per
-// (chunk, query head) walks the chunk with attn_head_window, reading K/V
-// from the cache (this step's row was written by qkv_rope_kernel), and
-// writes one record (m, l, acc[64]) into part[head][chunk][66].
+// (chunk, query head) takes the chunk's blocks in order (attn_block, then
+// attn_fold), reading K/V from the cache (this step's row was written by
+// qkv_rope_kernel), and writes one record (m, l, acc[64]) into
+// part[head][chunk][66].
 __global__ __launch_bounds__(kWave) void attn_partial_kernel(
     const float *__restrict__ q, const float *__restrict__ k_cache,
     const float *__restrict__ v_cache, const SeqState *__restrict__ st,
@@ -125,11 +126,18 @@ __global__ __launch_bounds__(kWave) void attn_partial_kernel(
   for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
     qv[d4] = reinterpret_cast<const float4 *>(q + h * kHeadDim)[d4];
   float m = -INFINITY, l = 0.f, acc = 0.f;
-  attn_head_window(
-      [&](int d4, int j) {
-        return reinterpret_cast<const float4 *>(kb + static_cast<size_t>(j) * kv_dim)[d4];
-      },
-      [&](int j, int d) { return vb[static_cast<size_t>(j) * kv_dim + d]; }, PLanes{}, qv, n, m, l, acc);
+  PLanes pb{};
+  for (int base = 0; base < n; base += kWave) {
+    float mb[1], lb[1], ab[1];
+    attn_block<1>(
+        [&](int d4, int j) {
+          return reinterpret_cast<const float4 *>(kb + static_cast<size_t>(j) * kv_dim)[d4];
+        },
+        [&](int, int d4) { return qv[d4]; },
+        [&](int j, int d) { return vb[static_cast<size_t>(j) * kv_dim + d]; }, pb, base,
+        min(kWave - 1, n - 1 - base), mb, lb, ab);
+    attn_fold(mb[0], lb[0], ab[0], m, l, acc);
+  }
   float *rec = part + (h * kAttnMaxChunks + chunk) * kPartStride;
   rec[2 + threadIdx.x] = acc;
   if (threadIdx.x == 0) {

@@ -776,12 +776,17 @@ struct Shape {
   static_assert(H <= 1024 && QD <= 1024, "common vectors");
 };
 
+// A wave's head slots while it computes block partials: slot hh holds the
+// head's probabilities at +4 (PLds), then its partial (m, l, 2 pad, acc[64]).
+constexpr int kAttnSlot = 68;
+constexpr int kAttnHeadsPerWave = 4;
 struct AttnRegion {
   float qs[kW * kHeadDim];
   float kn[kHeadDim];
   float vn[kHeadDim];
   float4 kt[(kHeadDim / 4) * kAttnCap];
   float vr[kAttnCap * kHeadDim];
+  float blk[kW * kAttnHeadsPerWave * kAttnSlot];
 };
 static_assert(sizeof(AttnRegion) <= kRegionBytes, "attention region");
 
@@ -1345,6 +1350,7 @@ struct Roles {
             }))
           return false;
         if (first_unit) clock.lap(2 * kRoleAttn);
+        // The head's running chunk partial (wave h < GROUP holds head h's).
         float m = -INFINITY, lsum = 0.f, acc = 0.f;
         for (int wb = begin; wb < end; wb += kAttnCap) {
           const int we = min(end, wb + kAttnCap);
@@ -1362,14 +1368,69 @@ struct Roles {
           }
           lds_barrier();
           if (wb == begin) clock.mark(0);
-          if (wv < GROUP) {
-            float4 q[kHeadDim / 4];
+          // The window's nb blocks over the waves. A single block: wave h
+          // takes head h (query in registers) and folds its partial
+          // directly. Several: wpb waves per block, each taking hpw of the
+          // group's heads (queries read from LDS, the block's K/V shared),
+          // staging their partials; wave h then folds head h's in block order.
+          const int nb = (we - wb + kWave - 1) / kWave;
+          if (nb == 1) {
+            if (wv < GROUP) {
+              float4 q[kHeadDim / 4];
 #pragma unroll
-            for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
-              q[d4] = reinterpret_cast<const float4 *>(ar.qs + wv * kHeadDim)[d4];
-            attn_head_window([&](int d4, int j) { return ar.kt[d4 * kAttnCap + j]; },
-                             [&](int j, int d) { return ar.vr[j * kHeadDim + d]; }, PLds{cm.xn + wv * kWave},
-                             q, we - wb, m, lsum, acc);
+              for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
+                q[d4] = reinterpret_cast<const float4 *>(ar.qs + wv * kHeadDim)[d4];
+              PLds pb{ar.blk + wv * kAttnHeadsPerWave * kAttnSlot + 4, kAttnSlot};
+              float bm[1], bl[1], ba[1];
+              attn_block<1>([&](int d4, int j) { return ar.kt[d4 * kAttnCap + j]; },
+                            [&](int, int d4) { return q[d4]; },
+                            [&](int j, int d) { return ar.vr[j * kHeadDim + d]; }, pb, 0, we - wb - 1, bm, bl, ba);
+              attn_fold(bm[0], bl[0], ba[0], m, lsum, acc);
+            }
+          } else {
+            const int wpb = kW / nb, hpw = (GROUP + wpb - 1) / wpb;
+            const int b = wv / wpb, h0 = (wv % wpb) * hpw;
+            const int nh = b < nb ? min(GROUP - h0, hpw) : 0;
+            float *slots = ar.blk + wv * kAttnHeadsPerWave * kAttnSlot;
+            auto run = [&](auto tag) {
+              constexpr int N = decltype(tag)::value;
+              PLds pb{slots + 4, kAttnSlot};
+              float bm[N], bl[N], ba[N];
+              attn_block<N>([&](int d4, int j) { return ar.kt[d4 * kAttnCap + j]; },
+                            [&](int hh, int d4) {
+                              return reinterpret_cast<const float4 *>(ar.qs + (h0 + hh) * kHeadDim)[d4];
+                            },
+                            [&](int j, int d) { return ar.vr[j * kHeadDim + d]; }, pb, b * kWave,
+                            min(kWave - 1, we - wb - 1 - b * kWave), bm, bl, ba);
+              // Stage the partials over the probabilities (every lane's
+              // reads of them come first).
+              __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+              __builtin_amdgcn_wave_barrier();
+#pragma unroll
+              for (int hh = 0; hh < N; ++hh) {
+                slots[hh * kAttnSlot + 4 + lane] = ba[hh];
+                if (lane == 0) {
+                  slots[hh * kAttnSlot] = bm[hh];
+                  slots[hh * kAttnSlot + 1] = bl[hh];
+                }
+              }
+            };
+            static_assert(kAttnHeadsPerWave == 4, "head sets of up to four");
+            switch (nh) {
+              case 1: run(std::integral_constant<int, 1>{}); break;
+              case 2: run(std::integral_constant<int, 2>{}); break;
+              case 3: run(std::integral_constant<int, 3>{}); break;
+              case 4: run(std::integral_constant<int, 4>{}); break;
+              default: break;
+            }
+            lds_barrier();
+            if (wv < GROUP) {
+              for (int bb = 0; bb < nb; ++bb) {
+                const float *src =
+                    ar.blk + ((bb * wpb + wv / hpw) * kAttnHeadsPerWave + wv % hpw) * kAttnSlot;
+                attn_fold(src[0], src[1], src[4 + lane], m, lsum, acc);
+              }
+            }
           }
         }
         clock.mark(1);
