@@ -20,14 +20,17 @@ constexpr int kAttnPass = 64;
 constexpr int kAttnMaxChunks = 16;
 constexpr int kPartStride = kHeadDim + 2;
 
-__host__ __device__ inline int attn_chunk_len(int length, int pass = kAttnPass) {
-  const int passes = (length + pass - 1) / pass;
-  const int per_chunk = (passes + kAttnMaxChunks - 1) / kAttnMaxChunks;
-  return per_chunk * pass;
+// Chunks of a context of `length` positions split `parts` ways (parts <=
+// kAttnMaxChunks; the decode engine uses its resident plan's attention CUs
+// per KV group, so that each takes one chunk): whole passes per chunk.
+__host__ __device__ inline int attn_chunk_len(int length, int parts = kAttnMaxChunks) {
+  const int passes = (length + kAttnPass - 1) / kAttnPass;
+  const int per_chunk = (passes + parts - 1) / parts;
+  return per_chunk * kAttnPass;
 }
 
-__host__ __device__ inline int attn_chunks(int length, int pass = kAttnPass) {
-  const int cl = attn_chunk_len(length, pass);
+__host__ __device__ inline int attn_chunks(int length, int parts = kAttnMaxChunks) {
+  const int cl = attn_chunk_len(length, parts);
   return (length + cl - 1) / cl;
 }
 

@@ -130,6 +130,11 @@ struct qd_engine {
   uint32_t *resident_error = nullptr;       // [1]
   uint32_t spin_limit = qd::kResidentSpinLimit;
   int roles_grid = 0;                       // 0: resident path unavailable
+  // Attention chunk geometry of both paths, attn_chunks(length, attn_parts):
+  // the resident plan's attention CUs per KV group at the engine's capacity
+  // (fixed at create, so the stream kernels split a context as the resident
+  // kernel does whether or not it runs), else kAttnMaxChunks.
+  int attn_parts = qd::kAttnMaxChunks;
   std::string resident_off_reason;
   // Prompt workspace (allocated on the first prefill): rows of the hidden
   // states, RMSNorm output, packed QKV, attention output, gate|up and SwiGLU
@@ -245,6 +250,7 @@ struct qd_engine {
     a.k_cache = kv_slice(k_cache, seq, layer);
     a.v_cache = kv_slice(v_cache, seq, layer);
     a.part = part;
+    a.attn_parts = attn_parts;
     a.capacity = static_cast<int>(CAP);
     a.nq = static_cast<int>(NQ);
     a.nkv = static_cast<int>(NKV);
@@ -287,7 +293,7 @@ struct qd_engine {
   // `length` positions: weights, KV rows and activations each moved once.
   double kernel_bytes(int kernel, double length) const {
     const double f = 4.0;
-    const double chunks = qd::attn_chunks(static_cast<int>(length));
+    const double chunks = qd::attn_chunks(static_cast<int>(length), attn_parts);
     switch (kernel) {
       case qd::kKEmbed: return 2 * H * f;
       case qd::kKQkvRope:
@@ -562,6 +568,7 @@ struct qd_engine {
     for (int r = 0; r < qd::kRoleCount; ++r) ra.role_end[r] = plan.end[r];
     for (int r = 0; r < 3; ++r) ra.group_cus[r] = plan.group_cus[r];
     ra.xcd_place = plan.xcd_place;
+    ra.attn_parts = attn_parts;
     check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
     // Every hand-off slot starts empty (all bits set).
     check(hipMemsetAsync(roles_slots, 0xFF, roles_slot_bytes, stream), "memset");
@@ -790,6 +797,12 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     // lowers the polls a hand-off wait makes before it gives up (tests
     // force the give-up path with it).
     const int cus = qd::device_cu_count(c.device);
+    {
+      qd::RolePlan cap_plan{};
+      if (cus >= 64 && cus <= qd::kMaxRoleGrid &&
+          qd::plan_roles(cus, int(e->H), int(e->I), int(e->NQ), int(e->NKV), int(e->CAP), &cap_plan))
+        e->attn_parts = std::min(qd::kAttnMaxChunks, cap_plan.group_cus[1]);
+    }
     const char *env = std::getenv("QD_RESIDENT");
     qd::RolePlan plan{};
     if (env && std::strcmp(env, "0") == 0) {

@@ -107,13 +107,13 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
 __global__ __launch_bounds__(kWave) void attn_partial_kernel(
     const float *__restrict__ q, const float *__restrict__ k_cache,
     const float *__restrict__ v_cache, const SeqState *__restrict__ st,
-    int nq, int nkv, float *__restrict__ part, int capacity) {
+    int nq, int nkv, float *__restrict__ part, int capacity, int parts) {
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
   const int position = static_cast<int>(st->position);
   const int length = position + 1;
   const int chunk = blockIdx.x;
-  if (chunk >= attn_chunks(length)) return;
-  const int chunk_len = attn_chunk_len(length);
+  if (chunk >= attn_chunks(length, parts)) return;
+  const int chunk_len = attn_chunk_len(length, parts);
   const int h = blockIdx.y;
   const int g = h / (nq / nkv);
   const int kv_dim = nkv * kHeadDim;
@@ -149,9 +149,9 @@ __global__ __launch_bounds__(kWave) void attn_partial_kernel(
 // Merges each head's partials into attn[h*64 + d].
 __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(
     const float *__restrict__ part, const SeqState *__restrict__ st, int nq,
-    float *__restrict__ attn, int capacity) {
+    float *__restrict__ attn, int capacity, int parts) {
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
-  const int chunks = attn_chunks(static_cast<int>(st->position) + 1);
+  const int chunks = attn_chunks(static_cast<int>(st->position) + 1, parts);
   const int h = blockIdx.x;
   const int d = threadIdx.x;
   attn[h * kHeadDim + d] = attn_merge(
@@ -532,13 +532,14 @@ hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
   }
   {
     Scope scope(m, kKAttnPartial);
-    attn_partial_kernel<<<dim3(kAttnMaxChunks, p.nq), kWave, 0, s>>>(
-        p.q, p.k_cache, p.v_cache, p.st, p.nq, p.nkv, p.part, p.capacity);
+    if (p.attn_parts < 1 || p.attn_parts > kAttnMaxChunks) return hipErrorInvalidValue;
+    attn_partial_kernel<<<dim3(p.attn_parts, p.nq), kWave, 0, s>>>(
+        p.q, p.k_cache, p.v_cache, p.st, p.nq, p.nkv, p.part, p.capacity, p.attn_parts);
   }
   {
     Scope scope(m, kKAttnCombine);
     attn_combine_kernel<<<p.nq, kHeadDim, 0, s>>>(p.part, p.st, p.nq, p.attn,
-                                                  p.capacity);
+                                                  p.capacity, p.attn_parts);
   }
   {
     Scope scope(m, kKOproj);

@@ -23,6 +23,7 @@ struct LayerLaunch {
   float *v_cache;
   float *part;     // split-KV partials [16][heads][66]
   int capacity;  // KV positions of the slot; kernels skip positions beyond
+  int attn_parts;  // chunk geometry: attn_chunks(length, attn_parts)
   int nq;
   int nkv;
   float eps;

@@ -1267,8 +1267,7 @@ struct Roles {
   }
 
   // ---- attention ----------------------------------------------------------
-  // Units (KV head g, chunk c) -> g * chunks + c, handled by attention CU
-  // unit % nrole. A unit stages its chunk's K (by float4 columns) and V rows
+  // Chunk c of KV group g is handled by the group's attention CU c % na. A unit stages its chunk's K (by float4 columns) and V rows
   // in LDS in windows of kAttnCap positions; the first window of a CU's
   // first unit is loaded ahead with the other roles' weights.
   __device__ void attn_dma(int l, int g, int wb, int we, AttnRegion &ar) {
@@ -1297,7 +1296,7 @@ struct Roles {
     const int g = rank / na, rr = rank % na;
     auto pre_lds = [&](int l, int position) {
       const int length = position + 1;
-      const int chunks = attn_chunks(length), cl = attn_chunk_len(length);
+      const int chunks = attn_chunks(length, a.attn_parts), cl = attn_chunk_len(length, a.attn_parts);
       if (rr >= chunks || position >= a.capacity) return;
       const int begin = rr * cl, end = min(length, begin + cl);
       attn_dma(l, g, begin, min(end, begin + kAttnCap), ar);
@@ -1305,7 +1304,7 @@ struct Roles {
     auto pre_regs = [](int) {};
     loop(kRoleAttn, false, [&](uint32_t t, int l, int position) {
       const int length = position + 1;
-      const int chunks = attn_chunks(length), cl = attn_chunk_len(length);
+      const int chunks = attn_chunks(length, a.attn_parts), cl = attn_chunk_len(length, a.attn_parts);
       const Slots in = s_qkv(l, t), out = s_part(l, t);
       // Record (h, c) is kRoleRecStride floats at (h * kAttnMaxChunks + c) *
       // kRoleRecStride: whole float4s.
@@ -1317,7 +1316,7 @@ struct Roles {
         // 1025) and regrows later, which leaves older records in slots beyond
         // it.
         const Slots next = s_part(l, t + 1);
-        const int chunks_next = attn_chunks(length + 1);
+        const int chunks_next = attn_chunks(length + 1, a.attn_parts);
         for (int c = rr; c < chunks_next; c += na) {
           for (int e = threadIdx.x; e < GROUP * kRec4; e += kT)
             next.clear4(((g * GROUP + e / kRec4) * kAttnMaxChunks + c) * kRec4 + e % kRec4);
@@ -1487,7 +1486,7 @@ struct Roles {
     OutMap om;  // rows [2 u0, 2 u0 + 2 n), staged from element 2 u0 rounded down to 4
     om.take(2 * u0, 2 * ro.n, (2 * u0) & ~3, threadIdx.x, 0);
     loop(kRoleO, false, [&](uint32_t t, int l, int position) {
-      const int C = attn_chunks(position + 1);
+      const int C = attn_chunks(position + 1, a.attn_parts);
       const Slots out = s_h1(l, t, g);
       if (om.q >= 0) clear_quad(s_h1(l, t + 1, g), om);
       // Group 0 adds the residual: rows [2 u0, 2 u0 + 2 n) of the layer
