@@ -1267,9 +1267,10 @@ struct Roles {
   }
 
   // ---- attention ----------------------------------------------------------
-  // Chunk c of KV group g is handled by the group's attention CU c % na. A unit stages its chunk's K (by float4 columns) and V rows
-  // in LDS in windows of kAttnCap positions; the first window of a CU's
-  // first unit is loaded ahead with the other roles' weights.
+  // Chunk c of KV group g is handled by the group's attention CU c % na. A
+  // chunk's K (by float4 columns) and V rows are staged in LDS in windows of
+  // kAttnCap positions; the first window of a CU's first chunk is loaded
+  // ahead with the other roles' weights.
   __device__ void attn_dma(int l, int g, int wb, int we, AttnRegion &ar) {
     const float *kc = kv_layer(a.k_cache, l);
     const float *vc = kv_layer(a.v_cache, l);

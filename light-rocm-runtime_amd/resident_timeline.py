@@ -1,0 +1,88 @@
+"""Per-layer timeline of the resident decode kernel (qd_trace_resident).
+
+Runs one profiled resident launch at a synthetic context and prints, for each
+role, when its input arrived, its three sub-phase stamps and when it
+published its outputs. Each figure is the median over layers 4..19 of the
+role's per-CU median, in microseconds from the layer's first QKV input. Also
+printed: the layer period and the LM head's input-to-done time, overall and
+per XCD (workgroup b runs on XCD b % 8).
+
+    python3 light-rocm-runtime_amd/resident_timeline.py --context 512
+    python3 light-rocm-runtime_amd/resident_timeline.py --context 4096 --save trace.npy
+
+The K/V context is zeros (the timing does not depend on the values). Needs a
+GPU; nothing here computes.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import sys
+
+import numpy as np
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+import qwen_decode as qd  # noqa: E402
+
+ROLES = ("qkv", "attn", "o", "gate", "down")
+
+
+def summarize(tr: np.ndarray, layers: int) -> list[str]:
+    grid = tr.shape[0]
+    # A workgroup's role is the stage pair it stamps.
+    roles = np.array([int(np.argmax(tr[w, min(5, layers - 1), :10] > 0)) // 2 for w in range(grid)])
+    lines = [f"workgroups per role: " + ", ".join(f"{n} {int((roles == r).sum())}" for r, n in enumerate(ROLES))]
+    lo, hi = min(4, layers - 1), max(min(20, layers - 1), min(4, layers - 1) + 1)
+    for r, name in enumerate(ROLES):
+        sel = roles == r
+        if not sel.any():
+            continue
+        vals = []
+        for layer in range(lo, hi):
+            base = np.median(tr[roles == 0, layer, 0])
+            block = tr[sel, layer, :]
+            vals.append((np.median(block[:, 2 * r]) - base, np.median(block[:, 14]) - base,
+                         np.median(block[:, 15]) - base, np.median(block[:, 16]) - base,
+                         np.median(block[:, 2 * r + 1]) - base, block[:, 2 * r + 1].max() - base))
+        v = np.median(np.array(vals), axis=0)
+        lines.append(f"{name:5s} arrived {v[0]:6.2f}  marks {v[1]:6.2f} {v[2]:6.2f} {v[3]:6.2f}  "
+                     f"published {v[4]:6.2f} (max {v[5]:6.2f})")
+    period = [np.median(tr[roles == 0, layer + 1, 0]) - np.median(tr[roles == 0, layer, 0])
+              for layer in range(lo, hi)]
+    lines.append(f"layer period median {np.median(period):.2f} us")
+    lm = tr[:, layers, 10:12]
+    lines.append(f"lm head: input-to-done median {np.median(lm[:, 1] - lm[:, 0]):.1f} us, "
+                 f"max {(lm[:, 1] - np.median(lm[:, 0])).max():.1f} us")
+    xcd = np.arange(grid) % 8
+    lines.append("lm head done by XCD: " + ", ".join(
+        f"{np.median(lm[xcd == x, 1] - lm[xcd == x, 0]):.1f}" for x in range(8)))
+    return lines
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--context", type=int, default=512, help="K/V positions before the traced launch")
+    ap.add_argument("--tokens", type=int, default=16, help="tokens in the traced launch")
+    ap.add_argument("--trace-token", type=int, default=8, help="which token's timeline to record")
+    ap.add_argument("--save", help="write the raw [workgroup, layer, stage] array here (.npy)")
+    args = ap.parse_args()
+    eng = qd.Engine(capacity=args.context + args.tokens + 64, max_batch=1)
+    try:
+        if eng.resident_grid() == 0:
+            print("resident path unavailable on this device", file=sys.stderr)
+            return 1
+        eng.load_synthetic(1)
+        eng.kv_reset(0, args.context)
+        tr = eng.trace_resident(0, 4242, args.tokens, args.trace_token)
+        if args.save:
+            np.save(args.save, tr)
+        print(f"context {args.context}, token {args.trace_token} of {args.tokens}")
+        for line in summarize(tr, eng.config.layers):
+            print(line)
+    finally:
+        eng.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
