@@ -283,6 +283,13 @@ def long_context_generation(full, stream_full, context, steps, token, what):
     say(f"{what}: max logits rel err {max(errs):.3e}")
 
 
+def test_resident_config2_context_512_matches_stream_and_oracle(full, stream_full):
+    """BASELINE config 2's range as the bench runs it: the resident kernel at
+    context 513..528 (9 chunks of 64 positions per KV head), against the
+    stream path bit for bit and the oracle."""
+    long_context_generation(full, stream_full, 512, 16, 31337, "config 2 resident 513..528")
+
+
 def test_resident_config3_context_4096_matches_stream_and_oracle(full, stream_full):
     """BASELINE config 3 as the bench runs it: the resident kernel at context
     4065..4096 (on a 256-CU MI355X, 512-position chunks, 8 per KV head, each
