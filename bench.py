@@ -8,12 +8,16 @@ Workloads (synthetic random-init weights):
   batch16  config 4: 16 independent sequences with contexts uniform in
            [256, 2048] (seed 3) decoded together; one step = one token of
            every sequence (16 tokens).
+  long     config 3: config 2's model decoding at KV context 4065..4096.
   prefill  config 5: the 512-token prompt (seed 4) through the MFMA prompt
            path; one step = one prefill of the 512 tokens. The 128 greedy
            decode steps that follow it in config 5 are reported beside it.
+  bf16     config 2's model and context with BF16 decoder matrices and an FP32
+           tail, on the stream-ordered kernels, timed against the same kernels
+           on FP32 weights.
 
-  python bench.py [--workload decode|batch16|prefill] [--steps K] [--warmup W]
-                  [--gpus 1] [--no-cpu]
+  python bench.py [--workload decode|long|batch16|prefill|bf16] [--steps K]
+                  [--warmup W] [--trials T] [--gpus 1] [--no-cpu]
 """
 import argparse
 import json
@@ -323,6 +327,88 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token):
     }
 
 
+# BF16 decoder matrices: the 24 layers' wqkv, wo, gate, up and down at 2 bytes
+# per element, their biases and norms, the FP32 tail (tied LM head, final norm)
+# as in WEIGHT_BYTES.
+BF16_WEIGHT_BYTES = (24 * (2 * (1152 * 896 + 896 * 896 + 3 * 4864 * 896) + 4 * (1152 + 2 * 896))
+                     + 544_538_624 + 3_584)
+
+
+def run_bf16(K, W, no_cpu, trials):
+    """Config 2's decode with BF16 decoder weights and an FP32 tail (the
+    reference's reduced-precision mode, examples/qwen/README.md:291-300), on the
+    stream-ordered kernels, interleaved with the same path on FP32 weights."""
+    capacity = PROMPT + max(K, W) + 24
+    log("engines: BF16 decoder weights, and FP32 on the stream kernels (QD_RESIDENT=0)")
+    e16 = qd.Engine(capacity=capacity, max_batch=1, decoder_dtype="bf16")
+    saved = os.environ.get("QD_RESIDENT")
+    os.environ["QD_RESIDENT"] = "0"
+    try:
+        e32 = qd.Engine(capacity=capacity, max_batch=1)
+    finally:
+        if saved is None:
+            del os.environ["QD_RESIDENT"]
+        else:
+            os.environ["QD_RESIDENT"] = saved
+    prompt = stream_tokens(PROMPT, SEED, PROMPT_STREAM, VOCAB)
+    firsts = {}
+    for name, eng in (("bf16", e16), ("f32", e32)):
+        eng.load_synthetic(SEED)
+        log(f"{name}: prefill {PROMPT}")
+        firsts[name], _, _ = eng.prefill(0, prompt, want_logits=False)
+        if W:
+            eng.generate(0, firsts[name], W)
+    engines = {"bf16": e16, "f32": e32}
+    samples = {name: [] for name in engines}
+    log(f"timed: {trials} interleaved trials x {K} tokens per engine")
+    for t in range(trials):
+        for name in trial_orders(list(engines))[t % 4]:
+            eng = engines[name]
+            eng.kv_reset(0, PROMPT)
+            eng.sync()
+            t0 = time.perf_counter()
+            toks, _, _ = eng.generate(0, firsts[name], K)
+            eng.sync()
+            samples[name].append((time.perf_counter() - t0) * 1e3)
+            assert len(toks) == K
+    w16, w32 = spread(samples["bf16"]), spread(samples["f32"])
+    e16.kv_reset(0, PROMPT)
+    prof = e16.profile_kernels(0, firsts["bf16"], min(K, 16))
+    log("bf16 step-path kernel profile: " + ", ".join(f"{n}={v[1]:.1f}us" for n, v in prof.items()))
+    name, (_, avg_us, avg_bytes, _) = dominant(prof)
+    e16.close()
+    e32.close()
+    per_token = [BF16_WEIGHT_BYTES + 24_576 * (PROMPT + 1 + i) + 24_576 + 607_744 + 3_584 for i in range(K)]
+    total = float(sum(per_token))
+    return {
+        "metric": "decode tokens/s at batch 1 (Qwen2.5-0.5B shape, BF16 decoder weights + FP32 tail) "
+                  "+ % HBM roofline",
+        "value": round(K / (w16["median"] * 1e-3), 2),
+        "unit": "tokens/s",
+        "ms_per_step": round(w16["median"] / K, 4),
+        "higher_is_better": True,
+        "dtype": "f32",
+        "data": "synthetic: random-init N(0,0.02) weights rounded to BF16 for the decoder matrices, "
+                f"N(0,0.01) biases, seed 1; {PROMPT} uniform random prompt tokens",
+        "config": {
+            "workload": "BASELINE config 2's model and context with BF16 decoder matrices (FP32 "
+                        "compute, FP32 biases, norms, embeddings and LM head), stream-ordered kernels",
+            "batch": 1, "context": f"{PROMPT + 1}..{PROMPT + K}", "layers": 24, "hidden": 896,
+            "vocab": VOCAB, "decoder_weights": "bf16",
+        },
+        "trials": {"count": trials, "order": "interleaved rotations, forwards then backwards",
+                   "bf16_ms": {k: round(v, 3) for k, v in w16.items()},
+                   "f32_stream_ms": {k: round(v, 3) for k, v in w32.items()}},
+        "step_hbm": {"achieved_gbs": round(total / (w16["median"] * 1e-3) / 1e9, 1),
+                     "peak_gbs": HBM_PEAK_GBS, "bytes_per_token": round(total / K)},
+        "f32_stream_tokens_per_s": round(K / (w32["median"] * 1e-3), 2),
+        "roofline": roofline_hbm(name, avg_us, avg_bytes),
+        "kernels_us": {n: round(v[1], 2) for n, v in prof.items()},
+        "cpu_baseline": None,
+        "path": "stream-ordered kernels (BF16 decoder matrices)",
+    }
+
+
 def batch_lengths():
     return [256 + int(x) for x in stream_tokens(BATCH_ROWS, BATCH_SEED, LEN_STREAM, 2048 - 256 + 1)]
 
@@ -492,7 +578,7 @@ def copy_probe(mib: int):
     log(f"copy probe: 3 x {mib} MiB device-to-device")
 
 
-DEFAULTS = {"decode": (64, 8), "long": (32, 4), "batch16": (32, 4), "prefill": (20, 3)}
+DEFAULTS = {"decode": (64, 8), "long": (32, 4), "batch16": (32, 4), "prefill": (20, 3), "bf16": (64, 8)}
 
 
 def main():
@@ -516,7 +602,7 @@ def main():
     if K <= 0:
         sys.exit("--steps must be positive")
     run = {"decode": run_decode, "long": run_long, "batch16": run_batch16,
-           "prefill": run_prefill}[args.workload]
+           "prefill": run_prefill, "bf16": run_bf16}[args.workload]
     out = run(K, W, args.no_cpu, max(1, args.trials))
     if args.copy_probe:
         copy_probe(args.copy_probe)

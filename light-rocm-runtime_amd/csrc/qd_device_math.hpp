@@ -229,6 +229,36 @@ __device__ __forceinline__ float4 ld_weight(const float4 *p) {
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// BF16 weights (the decoder's matrices of an engine created with BF16
+// decoder weights): four consecutive BF16 values, 8 bytes, loaded as one
+// non-temporal load and widened exactly to FP32 (a BF16 value is the top 16
+// bits of its FP32 value). Every GEMV helper below takes its weight rows as
+// float or as Bf16 and runs the same FP32 arithmetic either way.
+struct Bf16 {
+  uint16_t bits;
+};
+struct alignas(8) Bf16x4 {
+  uint32_t lo, hi;  // elements (0, 1) and (2, 3), low half first
+};
+typedef uint32_t gu32x2 __attribute__((ext_vector_type(2)));
+typedef const __attribute__((address_space(1))) gu32x2 global_u32x2;
+__device__ __forceinline__ float4 ld_weight(const Bf16x4 *p) {
+  const gu32x2 v = __builtin_nontemporal_load((global_u32x2 *)p);
+  return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
+                     __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+}
+// The four-element slot type of a weight row of W.
+template <typename W>
+struct WSlot;
+template <>
+struct WSlot<float> {
+  using type = float4;
+};
+template <>
+struct WSlot<Bf16> {
+  using type = Bf16x4;
+};
+
 // ---- RMSNorm ------------------------------------------------------------------
 
 // 1/rms of x[0..N) computed by the whole workgroup (every thread gets it).
@@ -329,13 +359,14 @@ __device__ __forceinline__ float norm_scale(float ss, int k, float eps) {
 
 // Weight slots of a row pair, loaded into registers (separable from the
 // arithmetic so a caller can issue them early).
-template <int K>
+template <int K, typename W = float>
 __device__ __forceinline__ void load_pair_weights(
-    const float *a, const float *b, float4 (&w)[PairSlots<K>::NJ]) {
+    const W *a, const W *b, float4 (&w)[PairSlots<K>::NJ]) {
   constexpr int K4 = PairSlots<K>::K4;
   constexpr int NJ = PairSlots<K>::NJ;
-  const float4 *a4 = reinterpret_cast<const float4 *>(a);
-  const float4 *b4 = reinterpret_cast<const float4 *>(b);
+  using S = typename WSlot<W>::type;
+  const S *a4 = reinterpret_cast<const S *>(a);
+  const S *b4 = reinterpret_cast<const S *>(b);
   const int lane = lane_id();
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -396,12 +427,12 @@ __device__ __forceinline__ void pair_dot(const float4 (&w)[PairSlots<K>::NJ],
   sb = wave_sum(accB);
 }
 
-template <int K>
-__device__ __forceinline__ void dot_pair(const float *a, const float *b,
+template <int K, typename W = float>
+__device__ __forceinline__ void dot_pair(const W *a, const W *b,
                                          const float4 (&xv)[PairSlots<K>::NJ],
                                          float &sa, float &sb) {
   float4 w[PairSlots<K>::NJ];
-  load_pair_weights<K>(a, b, w);
+  load_pair_weights<K, W>(a, b, w);
   pair_dot<K>(w, xv, sa, sb);
 }
 
@@ -453,10 +484,10 @@ __device__ __forceinline__ void load_row_operand(
   for (int j = 0; j < RowSlots<K>::NJ; ++j) xv[j] = x.ld4(j * kWave + lane);
 }
 
-template <int K>
-__device__ __forceinline__ void load_row_weights(const float *a,
+template <int K, typename W = float>
+__device__ __forceinline__ void load_row_weights(const W *a,
                                                  float4 (&w)[RowSlots<K>::NJ]) {
-  const float4 *a4 = reinterpret_cast<const float4 *>(a);
+  const typename WSlot<W>::type *a4 = reinterpret_cast<const typename WSlot<W>::type *>(a);
   const int lane = lane_id();
 #pragma unroll
   for (int j = 0; j < RowSlots<K>::NJ; ++j) w[j] = ld_weight(a4 + j * kWave + lane);
@@ -508,13 +539,13 @@ __host__ __device__ constexpr int row_slice_begin(int nj, int s) { return nj * s
 __device__ __forceinline__ float combine_slices(const float (&p)[kRowSlices]) {
   return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
 }
-template <int K>
-__device__ __forceinline__ float dot_row_sliced(const float *a,
+template <int K, typename W = float>
+__device__ __forceinline__ float dot_row_sliced(const W *a,
                                                 const float4 (&xv)[RowSlots<K>::NJ]) {
   constexpr int NJ = RowSlots<K>::NJ;
   static_assert(kRowSlices == 8, "combine_slices");
   float4 w[NJ];
-  load_row_weights<K>(a, w);
+  load_row_weights<K, W>(a, w);
   float p[kRowSlices];
 #pragma unroll
   for (int s = 0; s < kRowSlices; ++s) {

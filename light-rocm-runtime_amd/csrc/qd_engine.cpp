@@ -94,6 +94,24 @@ void fill_normal(float *out, size_t n, uint64_t first, uint64_t seed,
   for (auto &th : pool) th.join();
 }
 
+// FP32 -> BF16, rounded to nearest even; a NaN becomes the canonical quiet
+// NaN 0x7FC0 (the BF16 half of 0x7FC00000), so no weight equals the
+// resident kernel's empty-slot pattern after widening either.
+uint16_t to_bf16(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu) != 0) return 0x7FC0u;
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+float from_bf16(uint16_t h) {
+  const uint32_t u = uint32_t(h) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
 }  // namespace
 
 struct qd_engine {
@@ -197,6 +215,28 @@ struct qd_engine {
           "hipMemcpyAsync H2D");
   }
 
+  // The decoder matrices (wqkv, wo, wg, wu, wd) hold BF16 on an engine
+  // created with QD_DTYPE_BF16 decoder weights, else FP32. LayerPtrs keeps
+  // their addresses as float pointers either way; element offsets into them
+  // go through mat_at.
+  bool bf16 = false;
+  size_t mat_elem() const { return bf16 ? 2 : 4; }
+  char *mat_at(const float *base, size_t off) const {
+    return reinterpret_cast<char *>(const_cast<float *>(base)) + off * mat_elem();
+  }
+  // n FP32 values into a decoder matrix from element `off` (rounded to BF16
+  // on a BF16 engine; that copy completes before the call returns).
+  void upload_mat(const float *base, size_t off, const float *src, size_t n) {
+    if (!bf16) {
+      upload(reinterpret_cast<float *>(mat_at(base, off)), src, n);
+      return;
+    }
+    std::vector<uint16_t> h(n);
+    for (size_t i = 0; i < n; ++i) h[i] = to_bf16(src[i]);
+    check(hipMemcpyAsync(mat_at(base, off), h.data(), n * 2, hipMemcpyHostToDevice, stream), "H2D");
+    check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  }
+
   void build_rope_tables(float theta) {
     // Same FP32 recipe as the Hugging Face rotary embedding: inv_freq =
     // 1 / theta^(2i/d), angle = p * inv_freq, both rounded to FP32.
@@ -251,6 +291,7 @@ struct qd_engine {
     a.v_cache = kv_slice(v_cache, seq, layer);
     a.part = part;
     a.attn_parts = attn_parts;
+    a.weights_bf16 = bf16 ? 1 : 0;
     a.capacity = static_cast<int>(CAP);
     a.nq = static_cast<int>(NQ);
     a.nkv = static_cast<int>(NKV);
@@ -293,17 +334,18 @@ struct qd_engine {
   // `length` positions: weights, KV rows and activations each moved once.
   double kernel_bytes(int kernel, double length) const {
     const double f = 4.0;
+    const double mf = static_cast<double>(mat_elem());  // bytes per decoder-matrix element
     const double chunks = qd::attn_chunks(static_cast<int>(length), attn_parts);
     switch (kernel) {
       case qd::kKEmbed: return 2 * H * f;
       case qd::kKQkvRope:
-        return (QKV * H + QKV + 2 * H + 2 * qd::kRotary + QD + 2 * KVD) * f;
+        return QKV * H * mf + (QKV + 2 * H + 2 * qd::kRotary + QD + 2 * KVD) * f;
       case qd::kKAttnPartial:
         return (2 * length * KVD + QD + chunks * NQ * (qd::kHeadDim + 2)) * f;
       case qd::kKAttnCombine: return (chunks * NQ * (qd::kHeadDim + 2) + QD) * f;
-      case qd::kKOproj: return (H * QD + QD + 2 * H) * f;
-      case qd::kKGateUp: return (2 * I * H + 2 * H + I) * f;
-      case qd::kKDown: return (H * I + I + 2 * H) * f;
+      case qd::kKOproj: return H * QD * mf + (QD + 2 * H) * f;
+      case qd::kKGateUp: return 2 * I * H * mf + (2 * H + I) * f;
+      case qd::kKDown: return H * I * mf + (I + 2 * H) * f;
       case qd::kKLmHead: return (V * H + 2 * H + V + 2 * 1024) * f;
       case qd::kKArgmax: return 2 * 1024 * f;
     }
@@ -711,6 +753,9 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
       fail(QD_ERROR_INVALID_ARGUMENT, "heads %u not a multiple of kv_heads %u", c.heads, c.kv_heads);
     if (!(c.rms_eps > 0.0f) || !(c.rope_theta > 0.0f))
       fail(QD_ERROR_INVALID_ARGUMENT, "rms_eps and rope_theta must be positive");
+    if (c.decoder_dtype != QD_DTYPE_F32 && c.decoder_dtype != QD_DTYPE_BF16)
+      fail(QD_ERROR_INVALID_ARGUMENT, "decoder_dtype %u is neither QD_DTYPE_F32 nor QD_DTYPE_BF16",
+           c.decoder_dtype);
     if (!qd::shape_supported(static_cast<int>(c.hidden), static_cast<int>(c.intermediate),
                              static_cast<int>(c.heads), static_cast<int>(c.kv_heads),
                              static_cast<int>(c.head_dim)))
@@ -736,30 +781,38 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     e->L = c.layers;
     e->CAP = c.capacity;
     e->B = c.max_batch;
+    e->bf16 = c.decoder_dtype == QD_DTYPE_BF16;
     e->set_device();
     check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
     check(hipEventCreate(&e->ev_begin), "hipEventCreate");
     check(hipEventCreate(&e->ev_end), "hipEventCreate");
 
     // Layer weights in one arena: per layer wqkv | bqkv | wo | wg | wu | wd |
-    // attn_norm | mlp_norm, each 256-byte aligned.
-    auto round = [](size_t n) { return (n + 63) / 64 * 64; };  // floats
-    const size_t per_layer = round(e->QKV * e->H) + round(e->QKV) + round(e->H * e->QD) +
-                             2 * round(e->I * e->H) + round(e->H * e->I) + 2 * round(e->H);
-    e->weights_floats = per_layer * e->L;
+    // attn_norm | mlp_norm, each 256-byte aligned; the five matrices in
+    // mat_elem() bytes per element, biases and norms in FP32.
+    auto round = [](size_t bytes) { return (bytes + 255) / 256 * 256; };
+    const size_t me = e->mat_elem();
+    const size_t per_layer = round(e->QKV * e->H * me) + round(e->QKV * 4) + round(e->H * e->QD * me) +
+                             2 * round(e->I * e->H * me) + round(e->H * e->I * me) + 2 * round(e->H * 4);
+    e->weights_floats = per_layer * e->L / 4;
     e->weights = e->alloc<float>(e->weights_floats);
     e->layers.resize(e->L);
     for (size_t l = 0; l < e->L; ++l) {
-      float *p = e->weights + l * per_layer;
+      char *p = reinterpret_cast<char *>(e->weights) + l * per_layer;
       qd::LayerPtrs &w = e->layers[l];
-      w.wqkv = p; p += round(e->QKV * e->H);
-      w.bqkv = p; p += round(e->QKV);
-      w.wo = p; p += round(e->H * e->QD);
-      w.wg = p; p += round(e->I * e->H);
-      w.wu = p; p += round(e->I * e->H);
-      w.wd = p; p += round(e->H * e->I);
-      w.attn_norm = p; p += round(e->H);
-      w.mlp_norm = p;
+      auto take = [&](size_t bytes) {
+        const float *q = reinterpret_cast<const float *>(p);
+        p += round(bytes);
+        return q;
+      };
+      w.wqkv = take(e->QKV * e->H * me);
+      w.bqkv = take(e->QKV * 4);
+      w.wo = take(e->H * e->QD * me);
+      w.wg = take(e->I * e->H * me);
+      w.wu = take(e->I * e->H * me);
+      w.wd = take(e->H * e->I * me);
+      w.attn_norm = take(e->H * 4);
+      w.mlp_norm = take(e->H * 4);
     }
     e->embed = e->alloc<float>(e->V * e->H);
     e->lm_head = c.tied_lm_head ? e->embed : e->alloc<float>(e->V * e->H);
@@ -805,7 +858,9 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     }
     const char *env = std::getenv("QD_RESIDENT");
     qd::RolePlan plan{};
-    if (env && std::strcmp(env, "0") == 0) {
+    if (e->bf16) {
+      e->resident_off_reason = "BF16 decoder weights run on the stream-ordered kernels";
+    } else if (env && std::strcmp(env, "0") == 0) {
       e->resident_off_reason = "QD_RESIDENT=0";
     } else if (cus < 64 || cus > qd::kMaxRoleGrid || qd::roles_max_grid(c.device) < cus) {
       e->resident_off_reason = "device cannot co-schedule one role workgroup per CU";
@@ -906,27 +961,43 @@ qd_status qd_load_synthetic(qd_engine *e, uint64_t seed, const qd_synthetic_init
           slot ^= 1;
         }
       };
+      // A decoder matrix from element `first`: FP32, or rounded to BF16 in
+      // the staging buffer itself (element i's two bytes land at or below
+      // where its float was read) on a BF16 engine.
+      auto emit_mat = [&](const float *base, size_t first, size_t n, uint64_t stream_id, float stddev) {
+        if (!e->bf16) {
+          emit(reinterpret_cast<float *>(e->mat_at(base, first)), n, stream_id, stddev, false);
+          return;
+        }
+        for (size_t off = 0; off < n; off += chunk) {
+          const size_t m = std::min(chunk, n - off);
+          if (pending[slot]) check(hipEventSynchronize(done[slot]), "stage sync");
+          fill_normal(stage[slot], m, off, seed, stream_id, stddev);
+          uint16_t *h = reinterpret_cast<uint16_t *>(stage[slot]);
+          for (size_t i = 0; i < m; ++i) h[i] = to_bf16(stage[slot][i]);
+          check(hipMemcpyAsync(e->mat_at(base, first + off), h, m * 2, hipMemcpyHostToDevice, e->stream),
+                "H2D");
+          check(hipEventRecord(done[slot], e->stream), "hipEventRecord");
+          pending[slot] = true;
+          slot ^= 1;
+        }
+      };
       namespace b = qd::bundle;
       for (size_t l = 0; l < e->L; ++l) {
         const uint32_t li = static_cast<uint32_t>(l);
         const qd::LayerPtrs &w = e->layers[l];
-        float *wq = const_cast<float *>(w.wqkv);
         float *bq = const_cast<float *>(w.bqkv);
-        emit(wq, e->QD * e->H, qd::rng::layer_stream(li, b::kQW), init->weight_std, false);
-        emit(wq + e->QD * e->H, e->KVD * e->H, qd::rng::layer_stream(li, b::kKW), init->weight_std, false);
-        emit(wq + (e->QD + e->KVD) * e->H, e->KVD * e->H, qd::rng::layer_stream(li, b::kVW),
-             init->weight_std, false);
+        emit_mat(w.wqkv, 0, e->QD * e->H, qd::rng::layer_stream(li, b::kQW), init->weight_std);
+        emit_mat(w.wqkv, e->QD * e->H, e->KVD * e->H, qd::rng::layer_stream(li, b::kKW), init->weight_std);
+        emit_mat(w.wqkv, (e->QD + e->KVD) * e->H, e->KVD * e->H, qd::rng::layer_stream(li, b::kVW),
+                 init->weight_std);
         emit(bq, e->QD, qd::rng::layer_stream(li, b::kQB), init->bias_std, false);
         emit(bq + e->QD, e->KVD, qd::rng::layer_stream(li, b::kKB), init->bias_std, false);
         emit(bq + e->QD + e->KVD, e->KVD, qd::rng::layer_stream(li, b::kVB), init->bias_std, false);
-        emit(const_cast<float *>(w.wo), e->H * e->QD, qd::rng::layer_stream(li, b::kOW),
-             init->weight_std, false);
-        emit(const_cast<float *>(w.wg), e->I * e->H, qd::rng::layer_stream(li, b::kGateW),
-             init->weight_std, false);
-        emit(const_cast<float *>(w.wu), e->I * e->H, qd::rng::layer_stream(li, b::kUpW),
-             init->weight_std, false);
-        emit(const_cast<float *>(w.wd), e->H * e->I, qd::rng::layer_stream(li, b::kDownW),
-             init->weight_std, false);
+        emit_mat(w.wo, 0, e->H * e->QD, qd::rng::layer_stream(li, b::kOW), init->weight_std);
+        emit_mat(w.wg, 0, e->I * e->H, qd::rng::layer_stream(li, b::kGateW), init->weight_std);
+        emit_mat(w.wu, 0, e->I * e->H, qd::rng::layer_stream(li, b::kUpW), init->weight_std);
+        emit_mat(w.wd, 0, e->H * e->I, qd::rng::layer_stream(li, b::kDownW), init->weight_std);
         emit(const_cast<float *>(w.attn_norm), e->H, 0, init->norm_gain, true);
         emit(const_cast<float *>(w.mlp_norm), e->H, 0, init->norm_gain, true);
       }
@@ -962,18 +1033,17 @@ qd_status qd_load_bundle(qd_engine *e, const char *directory) {
       }
       namespace b = qd::bundle;
       const qd::LayerPtrs &p = e->layers[l];
-      float *wq = const_cast<float *>(p.wqkv);
       float *bq = const_cast<float *>(p.bqkv);
-      e->upload(wq, w.tensors[b::kQW].data(), e->QD * e->H);
-      e->upload(wq + e->QD * e->H, w.tensors[b::kKW].data(), e->KVD * e->H);
-      e->upload(wq + (e->QD + e->KVD) * e->H, w.tensors[b::kVW].data(), e->KVD * e->H);
+      e->upload_mat(p.wqkv, 0, w.tensors[b::kQW].data(), e->QD * e->H);
+      e->upload_mat(p.wqkv, e->QD * e->H, w.tensors[b::kKW].data(), e->KVD * e->H);
+      e->upload_mat(p.wqkv, (e->QD + e->KVD) * e->H, w.tensors[b::kVW].data(), e->KVD * e->H);
       e->upload(bq, w.tensors[b::kQB].data(), e->QD);
       e->upload(bq + e->QD, w.tensors[b::kKB].data(), e->KVD);
       e->upload(bq + e->QD + e->KVD, w.tensors[b::kVB].data(), e->KVD);
-      e->upload(const_cast<float *>(p.wo), w.tensors[b::kOW].data(), e->H * e->QD);
-      e->upload(const_cast<float *>(p.wg), w.tensors[b::kGateW].data(), e->I * e->H);
-      e->upload(const_cast<float *>(p.wu), w.tensors[b::kUpW].data(), e->I * e->H);
-      e->upload(const_cast<float *>(p.wd), w.tensors[b::kDownW].data(), e->H * e->I);
+      e->upload_mat(p.wo, 0, w.tensors[b::kOW].data(), e->H * e->QD);
+      e->upload_mat(p.wg, 0, w.tensors[b::kGateW].data(), e->I * e->H);
+      e->upload_mat(p.wu, 0, w.tensors[b::kUpW].data(), e->I * e->H);
+      e->upload_mat(p.wd, 0, w.tensors[b::kDownW].data(), e->H * e->I);
       e->upload(const_cast<float *>(p.attn_norm), w.tensors[b::kAttnNorm].data(), e->H);
       e->upload(const_cast<float *>(p.mlp_norm), w.tensors[b::kMlpNorm].data(), e->H);
       e->sync();  // host vectors die at the end of this iteration
@@ -996,7 +1066,17 @@ qd_status qd_load_bundle(qd_engine *e, const char *directory) {
     e->upload(e->final_norm, t.final_norm_weight.data(), e->H);
     if (e->lm_head != e->embed) e->upload(e->lm_head, t.lm_head_weight.data(), e->V * e->H);
     // No loaded NaN keeps its payload (see launch_canonical_nan).
-    check(qd::launch_canonical_nan(e->stream, e->weights, e->weights_floats), "canonical NaN");
+    // (BF16 matrices were canonicalised by their rounding; their bytes are
+    // not FP32 words, so only the FP32 tensors of such an engine are swept.)
+    if (!e->bf16) {
+      check(qd::launch_canonical_nan(e->stream, e->weights, e->weights_floats), "canonical NaN");
+    } else {
+      for (const qd::LayerPtrs &p : e->layers) {
+        check(qd::launch_canonical_nan(e->stream, const_cast<float *>(p.bqkv), e->QKV), "canonical NaN");
+        check(qd::launch_canonical_nan(e->stream, const_cast<float *>(p.attn_norm), e->H), "canonical NaN");
+        check(qd::launch_canonical_nan(e->stream, const_cast<float *>(p.mlp_norm), e->H), "canonical NaN");
+      }
+    }
     check(qd::launch_canonical_nan(e->stream, e->embed, e->V * e->H), "canonical NaN");
     check(qd::launch_canonical_nan(e->stream, e->final_norm, e->H), "canonical NaN");
     if (e->lm_head != e->embed)
@@ -1011,8 +1091,9 @@ qd_status qd_read_weight(qd_engine *e, uint32_t layer, uint32_t kind, float *out
   return guard([&] {
     if (!e || !out) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
     e->set_device();
-    const float *src = nullptr;
+    const void *src = nullptr;
     size_t n = 0;
+    bool mat = false;  // a decoder matrix: stored in mat_elem() bytes per element
     namespace b = qd::bundle;
     if (kind == 0x100) {
       src = e->embed; n = e->V * e->H;
@@ -1025,20 +1106,28 @@ qd_status qd_read_weight(qd_engine *e, uint32_t layer, uint32_t kind, float *out
       switch (kind) {
         case b::kAttnNorm: src = p.attn_norm; n = e->H; break;
         case b::kMlpNorm: src = p.mlp_norm; n = e->H; break;
-        case b::kQW: src = p.wqkv; n = e->QD * e->H; break;
-        case b::kKW: src = p.wqkv + e->QD * e->H; n = e->KVD * e->H; break;
-        case b::kVW: src = p.wqkv + (e->QD + e->KVD) * e->H; n = e->KVD * e->H; break;
+        case b::kQW: src = e->mat_at(p.wqkv, 0); n = e->QD * e->H; mat = true; break;
+        case b::kKW: src = e->mat_at(p.wqkv, e->QD * e->H); n = e->KVD * e->H; mat = true; break;
+        case b::kVW: src = e->mat_at(p.wqkv, (e->QD + e->KVD) * e->H); n = e->KVD * e->H; mat = true; break;
         case b::kQB: src = p.bqkv; n = e->QD; break;
         case b::kKB: src = p.bqkv + e->QD; n = e->KVD; break;
         case b::kVB: src = p.bqkv + e->QD + e->KVD; n = e->KVD; break;
-        case b::kOW: src = p.wo; n = e->H * e->QD; break;
-        case b::kGateW: src = p.wg; n = e->I * e->H; break;
-        case b::kUpW: src = p.wu; n = e->I * e->H; break;
-        case b::kDownW: src = p.wd; n = e->H * e->I; break;
+        case b::kOW: src = p.wo; n = e->H * e->QD; mat = true; break;
+        case b::kGateW: src = p.wg; n = e->I * e->H; mat = true; break;
+        case b::kUpW: src = p.wu; n = e->I * e->H; mat = true; break;
+        case b::kDownW: src = p.wd; n = e->H * e->I; mat = true; break;
       }
     }
     if (!src) fail(QD_ERROR_INVALID_ARGUMENT, "unknown tensor layer %u kind %u", layer, kind);
     if (count != n) fail(QD_ERROR_INVALID_ARGUMENT, "tensor has %zu elements, caller asked %zu", n, count);
+    if (mat && e->bf16) {
+      // Widened to FP32 exactly, as the kernels read them.
+      std::vector<uint16_t> h(n);
+      check(hipMemcpyAsync(h.data(), src, n * 2, hipMemcpyDeviceToHost, e->stream), "D2H");
+      e->sync();
+      for (size_t i = 0; i < n; ++i) out[i] = from_bf16(h[i]);
+      return;
+    }
     check(hipMemcpyAsync(out, src, n * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
     e->sync();
   });
@@ -1327,7 +1416,8 @@ void check_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t 
   for (uint32_t i = 0; i < n; ++i)
     if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u at %u >= vocab", tokens[i], i);
   e->set_device();
-  if (!e->wg_wu_adjacent()) fail(QD_ERROR_NOT_SUPPORTED, "prefill needs the gate and up weights adjacent");
+  if (!e->bf16 && !e->wg_wu_adjacent())
+    fail(QD_ERROR_NOT_SUPPORTED, "prefill needs the gate and up weights adjacent");
 }
 
 // The prompt in chunks of up to kPrefillRows positions, each through all
@@ -1335,6 +1425,24 @@ void check_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t 
 // on the last position, which advances the slot to pos0 + n. m (nullable)
 // times every launch.
 void run_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t n, EventMarker *m) {
+  if (e->bf16) {
+    // BF16 decoder weights: the prompt runs position by position through the
+    // stream-ordered step kernels (the prompt GEMMs read FP32 matrices),
+    // writing every position's K/V row; then the tail on the last position.
+    for (uint32_t i = 0; i < n; ++i) {
+      check(qd::launch_set_state(e->stream, e->states + seq, e->positions[seq], tokens[i]), "state launch");
+      check(qd::launch_embed(e->stream, e->embed, e->states + seq, e->hidden + size_t(seq) * e->H,
+                             static_cast<int>(e->H), static_cast<int>(e->V)),
+            "embed launch");
+      for (size_t l = 0; l < e->L; ++l) check(qd::launch_layer(e->stream, e->layer_args(seq, l)), "layer launch");
+      if (i + 1 < n) e->positions[seq] += 1;
+    }
+    e->push_state(seq, tokens[n - 1], qd::kModeStep, UINT32_MAX, 0);
+    check(qd::launch_tail(e->stream, e->tail_args(seq, e->logits + seq * e->V, 0, nullptr), nullptr),
+          "tail launch");
+    e->positions[seq] += 1;
+    return;
+  }
   for (uint32_t done = 0; done < n;) {
     const uint32_t rows = std::min<uint32_t>(n - done, uint32_t(qd_engine::kPrefillRows));
     if (m) {
@@ -1363,6 +1471,7 @@ void check_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, const ui
                  uint32_t steps) {
   if (!e || !seq_ids || !tokens) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
   e->check_loaded();
+  if (e->bf16) fail(QD_ERROR_NOT_SUPPORTED, "batched decode needs FP32 decoder weights");
   if (n_seq == 0 || n_seq > e->B) fail(QD_ERROR_INVALID_ARGUMENT, "n_seq %u out of range", n_seq);
   std::vector<bool> seen(e->B, false);
   for (uint32_t i = 0; i < n_seq; ++i) {
@@ -1438,6 +1547,7 @@ qd_status qd_step_batch_noalloc(qd_engine *e, uint32_t n_seq, const uint32_t *se
   return guard([&] {
     if (!e || !seq_ids || !tokens) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
     e->check_loaded();
+    if (e->bf16) fail(QD_ERROR_NOT_SUPPORTED, "batched decode needs FP32 decoder weights");
     if (n_seq == 0 || n_seq > uint32_t(qd::kBatchRows))
       fail(QD_ERROR_INVALID_ARGUMENT,
            "qd_step_batch_noalloc takes 1..%d sequences (its static workspace holds one group), got %u",

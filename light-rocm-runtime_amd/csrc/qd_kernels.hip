@@ -47,10 +47,10 @@ __global__ __launch_bounds__(kBlock) void embed_kernel(
 // Work unit u = (head, i): rows head*64+i and head*64+i+32 of the packed
 // matrix, which are exactly the pair a rotate-half rotation mixes. Heads
 // [0, nq) are queries, [nq, nq+nkv) keys, then values (not rotated).
-template <int H>
+template <int H, typename W>
 __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
     const float *__restrict__ hidden, const float *__restrict__ gain,
-    const float *__restrict__ wqkv, const float *__restrict__ bqkv,
+    const W *__restrict__ wqkv, const float *__restrict__ bqkv,
     const float *__restrict__ rope_cos, const float *__restrict__ rope_sin,
     const SeqState *__restrict__ st, float *__restrict__ q,
     float *__restrict__ k_cache, float *__restrict__ v_cache, int nq, int nkv,
@@ -70,8 +70,8 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
     const int ra = head * kHeadDim + i;
     const int rb = ra + kRotary;
     float sa, sb;
-    dot_pair<H>(wqkv + static_cast<size_t>(ra) * H,
-                wqkv + static_cast<size_t>(rb) * H, xv, sa, sb);
+    dot_pair<H, W>(wqkv + static_cast<size_t>(ra) * H,
+                   wqkv + static_cast<size_t>(rb) * H, xv, sa, sb);
     if (lane_id() == 0) {
       const float a = fmaf(sa, inv, bqkv[ra]);
       const float b = fmaf(sb, inv, bqkv[rb]);
@@ -163,9 +163,9 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(
 // dot is taken per KV group (columns [g QDG, (g + 1) QDG): the group's
 // query heads) and added in group order, hidden + group 0 first: the
 // resident role kernel's O CUs each hold one group's columns.
-template <int H, int QD, int NKV>
+template <int H, int QD, int NKV, typename W>
 __global__ __launch_bounds__(kBlock) void oproj_residual_kernel(
-    const float *__restrict__ attn, const float *__restrict__ wo,
+    const float *__restrict__ attn, const W *__restrict__ wo,
     const SeqState *__restrict__ st, float *__restrict__ hidden) {
   if (st->stopped) return;
   constexpr int QDG = QD / NKV;
@@ -175,12 +175,12 @@ __global__ __launch_bounds__(kBlock) void oproj_residual_kernel(
   constexpr int units = H / 2;
   for (int u = blockIdx.x * kWavesPerBlock + wave_id(); u < units;
        u += gridDim.x * kWavesPerBlock) {
-    const float *a = wo + static_cast<size_t>(2 * u) * QD;
+    const W *a = wo + static_cast<size_t>(2 * u) * QD;
     float ha = hidden[2 * u], hb = hidden[2 * u + 1];
 #pragma unroll
     for (int g = 0; g < NKV; ++g) {
       float sa, sb;
-      dot_pair<QDG>(a + g * QDG, a + QD + g * QDG, xv[g], sa, sb);
+      dot_pair<QDG, W>(a + g * QDG, a + QD + g * QDG, xv[g], sa, sb);
       ha += sa;
       hb += sb;
     }
@@ -192,10 +192,10 @@ __global__ __launch_bounds__(kBlock) void oproj_residual_kernel(
 }
 
 // MLP RMSNorm + gate/up + SiLU: unit r = (gate row r, up row r).
-template <int H>
+template <int H, typename W>
 __global__ __launch_bounds__(kBlock) void gateup_silu_kernel(
     const float *__restrict__ hidden, const float *__restrict__ gain,
-    const float *__restrict__ wg, const float *__restrict__ wu,
+    const W *__restrict__ wg, const W *__restrict__ wu,
     const SeqState *__restrict__ st, float *__restrict__ act, int inter,
     float eps) {
   if (st->stopped) return;
@@ -206,24 +206,24 @@ __global__ __launch_bounds__(kBlock) void gateup_silu_kernel(
   for (int r = blockIdx.x * kWavesPerBlock + wave_id(); r < inter;
        r += gridDim.x * kWavesPerBlock) {
     float gs, us;
-    dot_pair<H>(wg + static_cast<size_t>(r) * H,
-                wu + static_cast<size_t>(r) * H, xv, gs, us);
+    dot_pair<H, W>(wg + static_cast<size_t>(r) * H,
+                   wu + static_cast<size_t>(r) * H, xv, gs, us);
     if (lane_id() == 0) act[r] = silu_mul(gs * inv, us * inv);
   }
 }
 
 // hidden[r] += Wd[r,:] . act; one row per wave, summed in the column slices
 // of dot_row_sliced (the resident role kernel's arithmetic).
-template <int H, int I>
+template <int H, int I, typename W>
 __global__ __launch_bounds__(kBlock) void down_residual_kernel(
-    const float *__restrict__ act, const float *__restrict__ wd,
+    const float *__restrict__ act, const W *__restrict__ wd,
     const SeqState *__restrict__ st, float *__restrict__ hidden) {
   if (st->stopped) return;
   float4 xv[RowSlots<I>::NJ];
   load_row_operand<I>(Plain(act), xv);
   for (int r = blockIdx.x * kWavesPerBlock + wave_id(); r < H;
        r += gridDim.x * kWavesPerBlock) {
-    const float s = dot_row_sliced<I>(wd + static_cast<size_t>(r) * I, xv);
+    const float s = dot_row_sliced<I, W>(wd + static_cast<size_t>(r) * I, xv);
     if (lane_id() == 0) hidden[r] += s;
   }
 }
@@ -520,14 +520,23 @@ hipError_t launch_embed(hipStream_t s, const float *emb, const SeqState *st,
   return hipGetLastError();
 }
 
-hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
+namespace {
+
+// One layer's launches with the decoder matrices read as W (float or Bf16).
+template <typename W>
+hipError_t launch_layer_as(hipStream_t s, const LayerLaunch &p, Marker *m) {
+  const W *wqkv = reinterpret_cast<const W *>(p.w.wqkv);
+  const W *wo = reinterpret_cast<const W *>(p.w.wo);
+  const W *wg = reinterpret_cast<const W *>(p.w.wg);
+  const W *wu = reinterpret_cast<const W *>(p.w.wu);
+  const W *wd = reinterpret_cast<const W *>(p.w.wd);
   constexpr int H = 896, I = 4864, QD = 896;
   const int qkv_units = (p.nq + 2 * p.nkv) * kRotary;
   {
     Scope scope(m, kKQkvRope);
-    qkv_rope_kernel<H><<<(qkv_units + kWavesPerBlock - 1) / kWavesPerBlock,
-                         kBlock, 0, s>>>(
-        p.hidden, p.w.attn_norm, p.w.wqkv, p.w.bqkv, p.rope_cos, p.rope_sin,
+    qkv_rope_kernel<H, W><<<(qkv_units + kWavesPerBlock - 1) / kWavesPerBlock,
+                            kBlock, 0, s>>>(
+        p.hidden, p.w.attn_norm, wqkv, p.w.bqkv, p.rope_cos, p.rope_sin,
         p.st, p.q, p.k_cache, p.v_cache, p.nq, p.nkv, p.eps, p.capacity);
   }
   {
@@ -546,26 +555,30 @@ hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
     const dim3 grid((H / 2 + kWavesPerBlock - 1) / kWavesPerBlock);
     // The KV-group counts of QD / 64 query heads (shape_supported).
     switch (p.nkv) {
-      case 1: oproj_residual_kernel<H, QD, 1><<<grid, kBlock, 0, s>>>(p.attn, p.w.wo, p.st, p.hidden); break;
-      case 2: oproj_residual_kernel<H, QD, 2><<<grid, kBlock, 0, s>>>(p.attn, p.w.wo, p.st, p.hidden); break;
-      case 7: oproj_residual_kernel<H, QD, 7><<<grid, kBlock, 0, s>>>(p.attn, p.w.wo, p.st, p.hidden); break;
-      case 14: oproj_residual_kernel<H, QD, 14><<<grid, kBlock, 0, s>>>(p.attn, p.w.wo, p.st, p.hidden); break;
+      case 1: oproj_residual_kernel<H, QD, 1, W><<<grid, kBlock, 0, s>>>(p.attn, wo, p.st, p.hidden); break;
+      case 2: oproj_residual_kernel<H, QD, 2, W><<<grid, kBlock, 0, s>>>(p.attn, wo, p.st, p.hidden); break;
+      case 7: oproj_residual_kernel<H, QD, 7, W><<<grid, kBlock, 0, s>>>(p.attn, wo, p.st, p.hidden); break;
+      case 14: oproj_residual_kernel<H, QD, 14, W><<<grid, kBlock, 0, s>>>(p.attn, wo, p.st, p.hidden); break;
       default: return hipErrorInvalidValue;
     }
   }
   {
     Scope scope(m, kKGateUp);
-    gateup_silu_kernel<H><<<(I + kWavesPerBlock - 1) / kWavesPerBlock, kBlock,
-                            0, s>>>(p.hidden, p.w.mlp_norm, p.w.wg, p.w.wu,
-                                    p.st, p.act, I, p.eps);
+    gateup_silu_kernel<H, W><<<(I + kWavesPerBlock - 1) / kWavesPerBlock, kBlock,
+                               0, s>>>(p.hidden, p.w.mlp_norm, wg, wu, p.st, p.act, I, p.eps);
   }
   {
     Scope scope(m, kKDown);
-    down_residual_kernel<H, I><<<(H + kWavesPerBlock - 1) / kWavesPerBlock,
-                                 kBlock, 0, s>>>(p.act, p.w.wd, p.st,
-                                                 p.hidden);
+    down_residual_kernel<H, I, W><<<(H + kWavesPerBlock - 1) / kWavesPerBlock,
+                                    kBlock, 0, s>>>(p.act, wd, p.st, p.hidden);
   }
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
+  return p.weights_bf16 ? launch_layer_as<Bf16>(s, p, m) : launch_layer_as<float>(s, p, m);
 }
 
 hipError_t launch_tail(hipStream_t s, const TailLaunch &p, Marker *m) {

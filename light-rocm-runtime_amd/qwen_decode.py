@@ -21,6 +21,7 @@ SUCCESS, INVALID_ARGUMENT, NOT_INITIALIZED, ALREADY_INITIALIZED, NOT_SUPPORTED, 
 STOP_NONE, STOP_MAXIMUM_TOKENS, STOP_EOS_TOKEN = range(3)
 NO_EOS = 0xFFFFFFFF
 EMBED, FINAL_NORM, LM_HEAD = 0x100, 0x101, 0x102
+DTYPE_F32, DTYPE_BF16 = 0, 1
 
 
 class QdError(RuntimeError):
@@ -35,7 +36,7 @@ class Config(C.Structure):
         ("head_dim", C.c_uint32), ("intermediate", C.c_uint32), ("vocab", C.c_uint32),
         ("layers", C.c_uint32), ("capacity", C.c_uint32), ("max_batch", C.c_uint32),
         ("tied_lm_head", C.c_uint32), ("rms_eps", C.c_float), ("rope_theta", C.c_float),
-        ("device", C.c_int32), ("reserved", C.c_uint32),
+        ("device", C.c_int32), ("decoder_dtype", C.c_uint32),
     ]
 
 
@@ -186,11 +187,16 @@ class EngineConfig:
     rms_eps: float = 1e-6
     rope_theta: float = 1e6
     device: int = 0
+    decoder_dtype: str = "f32"  # "f32" or "bf16": storage of the decoder layers' matrices
 
     def c(self) -> Config:
+        dtypes = {"f32": DTYPE_F32, "bf16": DTYPE_BF16}
+        if self.decoder_dtype not in dtypes:
+            raise ValueError(f"decoder_dtype must be one of {sorted(dtypes)}")
         return Config(self.hidden, self.heads, self.kv_heads, self.head_dim, self.intermediate,
                       self.vocab, self.layers, self.capacity, self.max_batch,
-                      1 if self.tied_lm_head else 0, self.rms_eps, self.rope_theta, self.device, 0)
+                      1 if self.tied_lm_head else 0, self.rms_eps, self.rope_theta, self.device,
+                      dtypes[self.decoder_dtype])
 
 
 class Engine:
