@@ -99,50 +99,84 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(
   }
 }
 
-// Split-KV decode attention partials (qd_attention.hpp): one wave per
-// (chunk, query head) takes the chunk's blocks in order (attn_block, then
-// attn_fold), reading K/V from the cache (this step's row was written by
-// qkv_rope_kernel), and writes one record (m, l, acc[64]) into
-// part[head][chunk][66].
-__global__ __launch_bounds__(kWave) void attn_partial_kernel(
+// Split-KV decode attention partials (qd_attention.hpp): one workgroup of
+// kAttnSlots waves per (chunk, KV group), K/V read from the cache (this
+// step's row was written by qkv_rope_kernel). A one-block chunk takes one
+// wave per query head (attn_block_valu); a longer one deals its tiles w,
+// w + kAttnSlots, ... to wave w (attn_tile) and folds the wave partials in
+// slot order. Each head gets one record (m, l, acc[64]) in
+// part[head][chunk][66]: the arithmetic of the resident kernel's attention
+// CUs.
+constexpr int kAttnThreads = kAttnSlots * kWave;
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     const float *__restrict__ q, const float *__restrict__ k_cache,
     const float *__restrict__ v_cache, const SeqState *__restrict__ st,
     int nq, int nkv, float *__restrict__ part, int capacity, int parts) {
+  __shared__ float ps[kAttnSlots * kAttnPsFloats];
+  __shared__ float stage_lds[kAttnStageFloats];
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
   const int position = static_cast<int>(st->position);
   const int length = position + 1;
   const int chunk = blockIdx.x;
   if (chunk >= attn_chunks(length, parts)) return;
   const int chunk_len = attn_chunk_len(length, parts);
-  const int h = blockIdx.y;
-  const int g = h / (nq / nkv);
+  const int g = blockIdx.y;
+  const int group = nq / nkv;
   const int kv_dim = nkv * kHeadDim;
   const int begin = chunk * chunk_len;
-  const int n = min(length, begin + chunk_len) - begin;
-  const float *kb = k_cache + static_cast<size_t>(begin) * kv_dim + g * kHeadDim;
-  const float *vb = v_cache + static_cast<size_t>(begin) * kv_dim + g * kHeadDim;
-  float4 qv[kHeadDim / 4];
+  const int end = min(length, begin + chunk_len);
+  const float *kb = k_cache + g * kHeadDim;
+  const float *vb = v_cache + g * kHeadDim;
+  const int w = wave_id();
+  if (attn_single_block(chunk_len)) {
+    // One block: wave w takes head w of the group.
+    if (w < group) {
+      const int h = g * group + w;
+      const float *kc = kb + static_cast<size_t>(begin) * kv_dim;
+      const float *vc = vb + static_cast<size_t>(begin) * kv_dim;
+      float4 qv[kHeadDim / 4];
 #pragma unroll
-  for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
-    qv[d4] = reinterpret_cast<const float4 *>(q + h * kHeadDim)[d4];
-  float m = -INFINITY, l = 0.f, acc = 0.f;
-  PLanes pb{};
-  for (int base = 0; base < n; base += kWave) {
-    float mb[1], lb[1], ab[1];
-    attn_block<1>(
-        [&](int d4, int j) {
-          return reinterpret_cast<const float4 *>(kb + static_cast<size_t>(j) * kv_dim)[d4];
-        },
-        [&](int, int d4) { return qv[d4]; },
-        [&](int j, int d) { return vb[static_cast<size_t>(j) * kv_dim + d]; }, pb, base,
-        min(kWave - 1, n - 1 - base), mb, lb, ab);
-    attn_fold(mb[0], lb[0], ab[0], m, l, acc);
+      for (int d4 = 0; d4 < kHeadDim / 4; ++d4) qv[d4] = reinterpret_cast<const float4 *>(q + h * kHeadDim)[d4];
+      PLds pb{ps + w * kAttnPsFloats + 4, kAttnPsStride};
+      float mb[1], lb[1], ab[1];
+      attn_block_valu<1>(
+          [&](int d4, int j) { return reinterpret_cast<const float4 *>(kc + static_cast<size_t>(j) * kv_dim)[d4]; },
+          [&](int, int d4) { return qv[d4]; }, [&](int j, int d) { return vc[static_cast<size_t>(j) * kv_dim + d]; },
+          pb, 0, end - begin - 1, mb, lb, ab);
+      float M = -INFINITY, L = 0.f, A = 0.f;
+      attn_fold(mb[0], lb[0], ab[0], M, L, A);
+      float *rec = part + (h * kAttnMaxChunks + chunk) * kPartStride;
+      rec[2 + lane_id()] = A;
+      if (lane_id() == 0) {
+        rec[0] = M;
+        rec[1] = L;
+      }
+    }
+    return;
   }
-  float *rec = part + (h * kAttnMaxChunks + chunk) * kPartStride;
-  rec[2 + threadIdx.x] = acc;
-  if (threadIdx.x == 0) {
-    rec[0] = m;
-    rec[1] = l;
+  float4 qa[4];
+  attn_query([&](int h, int d4) { return reinterpret_cast<const float4 *>(q + (g * group + h) * kHeadDim)[d4]; },
+             group, qa);
+  AttnAcc acc;
+  acc.init();
+  attn_slot_tiles(
+      qa, [&](int pos, int d4) { return reinterpret_cast<const float4 *>(kb + static_cast<size_t>(pos) * kv_dim)[d4]; },
+      [&](int pos, int d) { return vb[static_cast<size_t>(pos) * kv_dim + d]; }, ps + w * kAttnPsFloats, begin,
+      begin, end, end, w, acc);
+  const AttnStage stage{stage_lds, stage_lds + kAttnSlots * kMaxGroup, stage_lds + 2 * kAttnSlots * kMaxGroup};
+  stage.put(w, group, acc);
+  __syncthreads();
+  const int tiles = (end - begin + kAttnTile - 1) / kAttnTile;
+  for (int i = threadIdx.x; i < group * kHeadDim; i += kAttnThreads) {
+    const int h = i / kHeadDim, d = i % kHeadDim;
+    float M, L, A;
+    attn_slot_merge(stage, tiles, h, d, M, L, A);
+    float *rec = part + ((g * group + h) * kAttnMaxChunks + chunk) * kPartStride;
+    rec[2 + d] = A;
+    if (d == 0) {
+      rec[0] = M;
+      rec[1] = L;
+    }
   }
 }
 
@@ -542,7 +576,8 @@ hipError_t launch_layer_as(hipStream_t s, const LayerLaunch &p, Marker *m) {
   {
     Scope scope(m, kKAttnPartial);
     if (p.attn_parts < 1 || p.attn_parts > kAttnMaxChunks) return hipErrorInvalidValue;
-    attn_partial_kernel<<<dim3(p.attn_parts, p.nq), kWave, 0, s>>>(
+    if (p.nq / p.nkv > kMaxGroup) return hipErrorInvalidValue;
+    attn_partial_kernel<<<dim3(p.attn_parts, p.nkv), kAttnThreads, 0, s>>>(
         p.q, p.k_cache, p.v_cache, p.st, p.nq, p.nkv, p.part, p.capacity, p.attn_parts);
   }
   {

@@ -776,19 +776,23 @@ struct Shape {
   static_assert(H <= 1024 && QD <= 1024, "common vectors");
 };
 
-// A wave's head slots while it computes block partials: slot hh holds the
-// head's probabilities at +4 (PLds), then its partial (m, l, 2 pad, acc[64]).
-constexpr int kAttnSlot = 68;
-constexpr int kAttnHeadsPerWave = 4;
+// The attention CU's LDS: the group's queries and this step's K/V row, one
+// window of K (float4 columns) and V rows, and each wave's probability
+// tile. After a chunk's
+// tiles the K window holds the wave partials (AttnStage).
 struct AttnRegion {
   float qs[kW * kHeadDim];
   float kn[kHeadDim];
   float vn[kHeadDim];
   float4 kt[(kHeadDim / 4) * kAttnCap];
   float vr[kAttnCap * kHeadDim];
-  float blk[kW * kAttnHeadsPerWave * kAttnSlot];
+  float ps[kW * kAttnPsFloats];
 };
 static_assert(sizeof(AttnRegion) <= kRegionBytes, "attention region");
+static_assert(kAttnSlots == kW, "one tile slot per wave");
+static_assert(kAttnStageFloats * 4 <= sizeof(AttnRegion::kt), "wave partials staged over the K window");
+// V element d of window row j (rows of kHeadDim floats).
+__device__ __forceinline__ int attn_v_slot(int j, int d) { return j * kHeadDim + d; }
 
 // One role CU's view of the launch: arguments, LDS, tagged vectors, the
 // token state, and the pieces every role shares (the per-token loop, the LM
@@ -1324,6 +1328,9 @@ struct Roles {
         }
       }
       bool first_unit = true;
+      float *ps = ar.ps + wv * kAttnPsFloats;
+      float *kst = reinterpret_cast<float *>(ar.kt);
+      const AttnStage stage{kst, kst + kAttnSlots * kMaxGroup, kst + 2 * kAttnSlots * kMaxGroup};
       for (int c = rr; c < chunks; c += na) {
         const int begin = c * cl;
         const int end = min(length, begin + cl);
@@ -1350,8 +1357,48 @@ struct Roles {
             }))
           return false;
         if (first_unit) clock.lap(2 * kRoleAttn);
-        // The head's running chunk partial (wave h < GROUP holds head h's).
-        float m = -INFINITY, lsum = 0.f, acc = 0.f;
+        if (attn_single_block(cl)) {
+          // One block (the window, loaded ahead): wave h takes head h, its
+          // query in registers, and stores the head's record (m, l, two pad
+          // words, acc[64]) itself: one contiguous 256-byte store of acc and
+          // one of the head words.
+          if (position >= begin && position < end) {
+            const int j = position - begin;
+            if (threadIdx.x < kHeadDim / 4)
+              ar.kt[threadIdx.x * kAttnCap + j] = reinterpret_cast<const float4 *>(ar.kn)[threadIdx.x];
+            if (threadIdx.x < kHeadDim) ar.vr[attn_v_slot(j, threadIdx.x)] = ar.vn[threadIdx.x];
+          }
+          lds_barrier();
+          clock.mark(0);
+          if (wv < GROUP) {
+            float4 q[kHeadDim / 4];
+#pragma unroll
+            for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
+              q[d4] = reinterpret_cast<const float4 *>(ar.qs + wv * kHeadDim)[d4];
+            PLds pb{ps + 4, kAttnPsStride};
+            float bm[1], bl[1], ba[1];
+            attn_block_valu<1>([&](int d4, int j) { return ar.kt[d4 * kAttnCap + j]; },
+                               [&](int, int d4) { return q[d4]; },
+                               [&](int j, int d) { return ar.vr[attn_v_slot(j, d)]; }, pb, 0, end - begin - 1, bm,
+                               bl, ba);
+            float M = -INFINITY, L = 0.f, A = 0.f;
+            attn_fold(bm[0], bl[0], ba[0], M, L, A);
+            clock.mark(1);
+            const uint32_t rec = ((g * GROUP + wv) * kAttnMaxChunks + c) * kRoleRecStride;
+            out.put(rec + 4 + lane, A);
+            if (lane < 4) out.put(rec + lane, lane == 0 ? M : lane == 1 ? L : 0.f);
+          }
+          clock.mark(2);
+          first_unit = false;
+          continue;
+        }
+        float4 qa[4];
+        attn_query([&](int h, int d4) { return reinterpret_cast<const float4 *>(ar.qs + h * kHeadDim)[d4]; },
+                   GROUP, qa);
+        // Wave w's running partial over the chunk's tiles w, w + kW, ...,
+        // window by window.
+        AttnAcc acc;
+        acc.init();
         for (int wb = begin; wb < end; wb += kAttnCap) {
           const int we = min(end, wb + kAttnCap);
           if (wb != begin) {
@@ -1364,84 +1411,29 @@ struct Roles {
             const int j = position - wb;
             if (threadIdx.x < kHeadDim / 4)
               ar.kt[threadIdx.x * kAttnCap + j] = reinterpret_cast<const float4 *>(ar.kn)[threadIdx.x];
-            if (threadIdx.x < kHeadDim) ar.vr[j * kHeadDim + threadIdx.x] = ar.vn[threadIdx.x];
+            if (threadIdx.x < kHeadDim) ar.vr[attn_v_slot(j, threadIdx.x)] = ar.vn[threadIdx.x];
           }
           lds_barrier();
           if (wb == begin) clock.mark(0);
-          // The window's nb blocks over the waves. A single block: wave h
-          // takes head h (query in registers) and folds its partial
-          // directly. Several: wpb waves per block, each taking hpw of the
-          // group's heads (queries read from LDS, the block's K/V shared),
-          // staging their partials; wave h then folds head h's in block order.
-          const int nb = (we - wb + kWave - 1) / kWave;
-          if (nb == 1) {
-            if (wv < GROUP) {
-              float4 q[kHeadDim / 4];
-#pragma unroll
-              for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
-                q[d4] = reinterpret_cast<const float4 *>(ar.qs + wv * kHeadDim)[d4];
-              PLds pb{ar.blk + wv * kAttnHeadsPerWave * kAttnSlot + 4, kAttnSlot};
-              float bm[1], bl[1], ba[1];
-              attn_block<1>([&](int d4, int j) { return ar.kt[d4 * kAttnCap + j]; },
-                            [&](int, int d4) { return q[d4]; },
-                            [&](int j, int d) { return ar.vr[j * kHeadDim + d]; }, pb, 0, we - wb - 1, bm, bl, ba);
-              attn_fold(bm[0], bl[0], ba[0], m, lsum, acc);
-            }
-          } else {
-            const int wpb = kW / nb, hpw = (GROUP + wpb - 1) / wpb;
-            const int b = wv / wpb, h0 = (wv % wpb) * hpw;
-            const int nh = b < nb ? min(GROUP - h0, hpw) : 0;
-            float *slots = ar.blk + wv * kAttnHeadsPerWave * kAttnSlot;
-            auto run = [&](auto tag) {
-              constexpr int N = decltype(tag)::value;
-              PLds pb{slots + 4, kAttnSlot};
-              float bm[N], bl[N], ba[N];
-              attn_block<N>([&](int d4, int j) { return ar.kt[d4 * kAttnCap + j]; },
-                            [&](int hh, int d4) {
-                              return reinterpret_cast<const float4 *>(ar.qs + (h0 + hh) * kHeadDim)[d4];
-                            },
-                            [&](int j, int d) { return ar.vr[j * kHeadDim + d]; }, pb, b * kWave,
-                            min(kWave - 1, we - wb - 1 - b * kWave), bm, bl, ba);
-              // Stage the partials over the probabilities (every lane's
-              // reads of them come first).
-              __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-              __builtin_amdgcn_wave_barrier();
-#pragma unroll
-              for (int hh = 0; hh < N; ++hh) {
-                slots[hh * kAttnSlot + 4 + lane] = ba[hh];
-                if (lane == 0) {
-                  slots[hh * kAttnSlot] = bm[hh];
-                  slots[hh * kAttnSlot + 1] = bl[hh];
-                }
-              }
-            };
-            static_assert(kAttnHeadsPerWave == 4, "head sets of up to four");
-            switch (nh) {
-              case 1: run(std::integral_constant<int, 1>{}); break;
-              case 2: run(std::integral_constant<int, 2>{}); break;
-              case 3: run(std::integral_constant<int, 3>{}); break;
-              case 4: run(std::integral_constant<int, 4>{}); break;
-              default: break;
-            }
-            lds_barrier();
-            if (wv < GROUP) {
-              for (int bb = 0; bb < nb; ++bb) {
-                const float *src =
-                    ar.blk + ((bb * wpb + wv / hpw) * kAttnHeadsPerWave + wv % hpw) * kAttnSlot;
-                attn_fold(src[0], src[1], src[4 + lane], m, lsum, acc);
-              }
-            }
-          }
+          attn_slot_tiles(qa, [&](int pos, int d4) { return ar.kt[d4 * kAttnCap + (pos - wb)]; },
+                          [&](int pos, int d) { return ar.vr[attn_v_slot(pos - wb, d)]; }, ps, begin, wb, we, end,
+                          wv, acc);
         }
         clock.mark(1);
-        // Each head's wave stores its own record (m, l, two pad words,
-        // acc[64]) word by word: one contiguous 256-byte store of acc and one
-        // of the head words. A reader takes a float4 once none of its words
-        // is kSlotEmpty, so it never sees a partly written one.
+        // The wave partials replace the K window, then wave h folds head
+        // h's in slot order (lane = dim) and stores the head's record (m,
+        // l, two pad words, acc[64]): one contiguous 256-byte store of acc
+        // and one of the head words. A reader takes a float4 once none of
+        // its words is kSlotEmpty, so it never sees a partly written one.
+        lds_barrier();
+        stage.put(wv, GROUP, acc);
+        lds_barrier();
         if (wv < GROUP) {
+          float M, L, A;
+          attn_slot_merge(stage, (end - begin + kAttnTile - 1) / kAttnTile, wv, lane, M, L, A);
           const uint32_t rec = ((g * GROUP + wv) * kAttnMaxChunks + c) * kRoleRecStride;
-          out.put(rec + 4 + lane, acc);
-          if (lane < 4) out.put(rec + lane, lane == 0 ? m : lane == 1 ? lsum : 0.f);
+          out.put(rec + 4 + lane, A);
+          if (lane < 4) out.put(rec + lane, lane == 0 ? M : lane == 1 ? L : 0.f);
         }
         clock.mark(2);
         first_unit = false;
