@@ -2,11 +2,13 @@
 // megakernel, so both paths run the same arithmetic in the same order.
 //
 // Split-KV: the attended positions 0..L-1 are cut into chunks of
-// attn_chunk_len(L) positions (a multiple of 64, at most kAttnMaxChunks
-// chunks). A chunk of one KV group is one workgroup's work, computed in
-// one of two ways fixed by the chunk length, so every path agrees:
-//  - one block (64 positions, attn_single_block): one wave per query head
-//    forms the block's softmax partial on the vector ALUs (attn_block_valu);
+// attn_chunk_len(L, parts, kAttnGrain) positions (a multiple of the
+// 16-position tile, at most kAttnMaxChunks chunks). A chunk of one KV group
+// is one workgroup's work, computed in one of two ways fixed by the chunk
+// length, so every path agrees:
+//  - one block (up to 64 positions, attn_single_block): one wave per query
+//    head forms the block's softmax partial on the vector ALUs
+//    (attn_block_valu);
 //  - longer: the chunk is cut into tiles of 16 positions, dealt round-robin
 //    to kAttnSlots waves; each wave keeps an online-softmax partial of all
 //    the group's heads over its tiles (scores and P.V on FP32 MFMA,
@@ -136,12 +138,12 @@ __device__ __forceinline__ void attn_block_valu(K4 k4, Q4 q4, V v, PB &pb, int b
   for (int hh = 0; hh < kNH; ++hh) acc[hh] = (a[hh][0] + a[hh][1]) + (a[hh][2] + a[hh][3]);
 }
 
-// A chunk of exactly one block (chunk length kAttnPass: contexts of up to
-// 64 * parts positions) is computed on the vector ALUs, one query head per
-// wave (attn_block_valu); longer chunks go through the MFMA tiles below.
+// A chunk of at most one block (chunk length up to kAttnPass: contexts of
+// up to 64 * parts positions) is computed on the vector ALUs, one query head
+// per wave (attn_block_valu); longer chunks go through the MFMA tiles below.
 // With one block per chunk the tiles' cross-wave merge would be all
 // overhead, and a wave per head keeps the K/V reads to one block.
-__host__ __device__ inline bool attn_single_block(int chunk_len) { return chunk_len == kAttnPass; }
+__host__ __device__ inline bool attn_single_block(int chunk_len) { return chunk_len <= kAttnPass; }
 
 typedef float attn_f4v __attribute__((ext_vector_type(4)));
 
@@ -278,14 +280,147 @@ __device__ __forceinline__ void attn_tile(const float4 (&qa)[4], K4 k4, V v, flo
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Two tiles [ta, ta + 16) and [tb, tb + 16) of one wave taken together, as
+// one online-softmax step over both (their chains interleave): S of each
+// tile as in attn_tile; m' = max(m, max(tile a max, tile b max)); c and p as
+// in attn_tile; l = l c + (row16_sum(p_a) + row16_sum(p_b)); o = o c, then
+// o += P_a . V_a, then P_b . V_b. ps: one probability tile, as attn_tile's.
+template <typename K4, typename V>
+__device__ __forceinline__ void attn_tile2(const float4 (&qa)[4], K4 k4, V v, float *ps, int ta, int tb, int end,
+                                           AttnAcc &acc) {
+  const int lane = lane_id(), col = lane & 15, quad = lane >> 4;
+  const int t0[2] = {ta, tb};
+  float4 kb[2][4];
+  float vb[2][4][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int pk = min(t0[u] + col, end - 1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kb[u][s] = k4(pk, 4 * s + quad);
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int pv = min(t0[u] + 4 * s + quad, end - 1);
+#pragma unroll
+      for (int n = 0; n < 4; ++n) vb[u][s][n] = v(pv, 16 * n + col);
+    }
+  }
+  attn_f4v sp[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) sp[u][s] = attn_f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        sp[u][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(attn_c(qa[s], c), attn_c(kb[u][s], c), sp[u][s], 0, 0, 0);
+    }
+  }
+  float x[2][4], mx[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const attn_f4v sc = (sp[u][0] + sp[u][1]) + (sp[u][2] + sp[u][3]);
+    const bool valid = t0[u] + col < end;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[u][r] = valid ? __fmul_rn(sc[r], kScoreScaleLog2) : -INFINITY;
+  }
+  // row16_max of each row of both tiles, step by step.
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx[u][r] = fmaxf(x[u][r], dpp<kDppXor1>(x[u][r]));
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx[u][r] = fmaxf(mx[u][r], dpp<kDppXor2>(mx[u][r]));
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx[u][r] = fmaxf(mx[u][r], dpp<kDppHalfMirror>(mx[u][r]));
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx[u][r] = fmaxf(mx[u][r], dpp<kDppMirror>(mx[u][r]));
+  float mn[4], cr[4], p[2][4], sm[2][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    mn[r] = fmaxf(acc.m[r], fmaxf(mx[0][r], mx[1][r]));
+    cr[r] = acc.m[r] == -INFINITY ? 0.f : exp2_fast(acc.m[r] - mn[r]);
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) p[u][r] = exp2_fast(x[u][r] - mn[r]);
+  // The A operands of both tiles through the one probability tile: tile a's
+  // written and read, then tile b's.
+  float pa[2][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ps[(4 * quad + r) * kAttnPsStride + col] = p[u][r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int s = 0; s < 4; ++s) pa[u][s] = ps[col * kAttnPsStride + 4 * s + quad];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  // row16_sum of each row's probabilities of both tiles.
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm[u][r] = p[u][r] + dpp<kDppXor1>(p[u][r]);
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm[u][r] += dpp<kDppXor2>(sm[u][r]);
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm[u][r] += dpp<kDppHalfMirror>(sm[u][r]);
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm[u][r] += dpp<kDppMirror>(sm[u][r]);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    acc.l[r] = fmaf(acc.l[r], cr[r], sm[0][r] + sm[1][r]);
+    acc.m[r] = mn[r];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc.o[n][r] = __fmul_rn(acc.o[n][r], cr[r]);
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        acc.o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[u][s], vb[u][s][n], acc.o[n], 0, 0, 0);
+    }
+  }
+}
+
 // The tiles of slot `slot` that lie in [wb, we) of a chunk starting at
-// `begin` (wb - begin a multiple of kAttnTile), in position order.
+// `begin` (wb - begin a multiple of 2 kAttnSlots tiles), in position order:
+// tiles t and t + kAttnSlots together (attn_tile2) while both exist, a last
+// single one alone (attn_tile).
 template <typename K4, typename V>
 __device__ __forceinline__ void attn_slot_tiles(const float4 (&qa)[4], K4 k4, V v, float *ps, int begin,
                                                 int wb, int we, int end, int slot, AttnAcc &acc) {
   const int t_lo = (wb - begin) / kAttnTile, t_hi = (we - begin + kAttnTile - 1) / kAttnTile;
-  int t = t_lo + ((slot - t_lo % kAttnSlots) % kAttnSlots + kAttnSlots) % kAttnSlots;
-  for (; t < t_hi; t += kAttnSlots) attn_tile(qa, k4, v, ps, begin + t * kAttnTile, end, acc);
+  for (int t = t_lo + slot; t < t_hi; t += 2 * kAttnSlots) {
+    if (t + kAttnSlots < t_hi)
+      attn_tile2(qa, k4, v, ps, begin + t * kAttnTile, begin + (t + kAttnSlots) * kAttnTile, end, acc);
+    else
+      attn_tile(qa, k4, v, ps, begin + t * kAttnTile, end, acc);
+  }
 }
 
 // Wave partials of a chunk staged for the merge: [slot][row] maxima and

@@ -13,24 +13,27 @@ constexpr int kBlock = 256;            // threads per workgroup
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kMaxGroup = 16;          // query heads per KV head
 
-// Split-KV attention geometry (qd_attention.hpp): chunks are multiples of
-// the pass length (16 positions per wave of the unit: 64 with four waves),
-// at most kAttnMaxChunks per head; a partial record is (m, l, acc[64]).
+// Split-KV attention geometry (qd_attention.hpp): chunks are whole grains
+// of positions, at most kAttnMaxChunks per head; a partial record is (m, l,
+// acc[64]). The batch-1 decode paths cut chunks in grains of one attention
+// tile (kAttnGrain, 16 positions); the batched kernel in passes of 64 (16
+// positions per wave of its four-wave unit).
 constexpr int kAttnPass = 64;
+constexpr int kAttnGrain = 16;
 constexpr int kAttnMaxChunks = 16;
 constexpr int kPartStride = kHeadDim + 2;
 
 // Chunks of a context of `length` positions split `parts` ways (parts <=
 // kAttnMaxChunks; the decode engine uses its resident plan's attention CUs
-// per KV group, so that each takes one chunk): whole passes per chunk.
-__host__ __device__ inline int attn_chunk_len(int length, int parts = kAttnMaxChunks) {
-  const int passes = (length + kAttnPass - 1) / kAttnPass;
-  const int per_chunk = (passes + parts - 1) / parts;
-  return per_chunk * kAttnPass;
+// per KV group, so that each takes one chunk): whole grains per chunk.
+__host__ __device__ inline int attn_chunk_len(int length, int parts = kAttnMaxChunks, int grain = kAttnPass) {
+  const int grains = (length + grain - 1) / grain;
+  const int per_chunk = (grains + parts - 1) / parts;
+  return per_chunk * grain;
 }
 
-__host__ __device__ inline int attn_chunks(int length, int parts = kAttnMaxChunks) {
-  const int cl = attn_chunk_len(length, parts);
+__host__ __device__ inline int attn_chunks(int length, int parts = kAttnMaxChunks, int grain = kAttnPass) {
+  const int cl = attn_chunk_len(length, parts, grain);
   return (length + cl - 1) / cl;
 }
 

@@ -148,7 +148,7 @@ struct qd_engine {
   uint32_t *resident_error = nullptr;       // [1]
   uint32_t spin_limit = qd::kResidentSpinLimit;
   int roles_grid = 0;                       // 0: resident path unavailable
-  // Attention chunk geometry of both paths, attn_chunks(length, attn_parts):
+  // Attention chunk geometry of both paths, attn_chunks(length, attn_parts, kAttnGrain):
   // the resident plan's attention CUs per KV group at the engine's capacity
   // (fixed at create, so the stream kernels split a context as the resident
   // kernel does whether or not it runs), else kAttnMaxChunks.
@@ -335,7 +335,7 @@ struct qd_engine {
   double kernel_bytes(int kernel, double length) const {
     const double f = 4.0;
     const double mf = static_cast<double>(mat_elem());  // bytes per decoder-matrix element
-    const double chunks = qd::attn_chunks(static_cast<int>(length), attn_parts);
+    const double chunks = qd::attn_chunks(static_cast<int>(length), attn_parts, qd::kAttnGrain);
     switch (kernel) {
       case qd::kKEmbed: return 2 * H * f;
       case qd::kKQkvRope:

@@ -118,8 +118,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
   const int position = static_cast<int>(st->position);
   const int length = position + 1;
   const int chunk = blockIdx.x;
-  if (chunk >= attn_chunks(length, parts)) return;
-  const int chunk_len = attn_chunk_len(length, parts);
+  if (chunk >= attn_chunks(length, parts, kAttnGrain)) return;
+  const int chunk_len = attn_chunk_len(length, parts, kAttnGrain);
   const int g = blockIdx.y;
   const int group = nq / nkv;
   const int kv_dim = nkv * kHeadDim;
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(
     const float *__restrict__ part, const SeqState *__restrict__ st, int nq,
     float *__restrict__ attn, int capacity, int parts) {
   if (st->stopped || st->position >= static_cast<uint32_t>(capacity)) return;
-  const int chunks = attn_chunks(static_cast<int>(st->position) + 1, parts);
+  const int chunks = attn_chunks(static_cast<int>(st->position) + 1, parts, kAttnGrain);
   const int h = blockIdx.x;
   const int d = threadIdx.x;
   attn[h * kHeadDim + d] = attn_merge(

@@ -23,7 +23,7 @@ struct LayerLaunch {
   float *v_cache;
   float *part;     // split-KV partials [16][heads][66]
   int capacity;  // KV positions of the slot; kernels skip positions beyond
-  int attn_parts;  // chunk geometry: attn_chunks(length, attn_parts)
+  int attn_parts;  // chunk geometry: attn_chunks(length, attn_parts, kAttnGrain)
   int weights_bf16;  // nonzero: w's decoder matrices (wqkv, wo, wg, wu, wd) hold BF16
   int nq;
   int nkv;

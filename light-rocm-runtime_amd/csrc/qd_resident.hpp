@@ -78,7 +78,7 @@ struct ResidentArgs {
   uint32_t spin_limit;          // polls before a wait gives up
   int role_end[kRoleCount];     // RolePlan::end
   int group_cus[3];             // RolePlan::group_cus
-  int attn_parts;               // chunk geometry: attn_chunks(length, attn_parts)
+  int attn_parts;               // chunk geometry: attn_chunks(length, attn_parts, kAttnGrain)
   int xcd_place;                // RolePlan::xcd_place
 };
 

@@ -789,7 +789,7 @@ struct AttnRegion {
   float ps[kW * kAttnPsFloats];
 };
 static_assert(sizeof(AttnRegion) <= kRegionBytes, "attention region");
-static_assert(kAttnSlots == kW, "one tile slot per wave");
+static_assert(kAttnSlots == kW && kAttnCap % (2 * kAttnSlots * kAttnTile) == 0, "tile pairs inside a window");
 static_assert(kAttnStageFloats * 4 <= sizeof(AttnRegion::kt), "wave partials staged over the K window");
 // V element d of window row j (rows of kHeadDim floats).
 __device__ __forceinline__ int attn_v_slot(int j, int d) { return j * kHeadDim + d; }
@@ -1301,7 +1301,7 @@ struct Roles {
     const int g = rank / na, rr = rank % na;
     auto pre_lds = [&](int l, int position) {
       const int length = position + 1;
-      const int chunks = attn_chunks(length, a.attn_parts), cl = attn_chunk_len(length, a.attn_parts);
+      const int chunks = attn_chunks(length, a.attn_parts, kAttnGrain), cl = attn_chunk_len(length, a.attn_parts, kAttnGrain);
       if (rr >= chunks || position >= a.capacity) return;
       const int begin = rr * cl, end = min(length, begin + cl);
       attn_dma(l, g, begin, min(end, begin + kAttnCap), ar);
@@ -1309,7 +1309,7 @@ struct Roles {
     auto pre_regs = [](int) {};
     loop(kRoleAttn, false, [&](uint32_t t, int l, int position) {
       const int length = position + 1;
-      const int chunks = attn_chunks(length, a.attn_parts), cl = attn_chunk_len(length, a.attn_parts);
+      const int chunks = attn_chunks(length, a.attn_parts, kAttnGrain), cl = attn_chunk_len(length, a.attn_parts, kAttnGrain);
       const Slots in = s_qkv(l, t), out = s_part(l, t);
       // Record (h, c) is kRoleRecStride floats at (h * kAttnMaxChunks + c) *
       // kRoleRecStride: whole float4s.
@@ -1321,7 +1321,7 @@ struct Roles {
         // 1025) and regrows later, which leaves older records in slots beyond
         // it.
         const Slots next = s_part(l, t + 1);
-        const int chunks_next = attn_chunks(length + 1, a.attn_parts);
+        const int chunks_next = attn_chunks(length + 1, a.attn_parts, kAttnGrain);
         for (int c = rr; c < chunks_next; c += na) {
           for (int e = threadIdx.x; e < GROUP * kRec4; e += kT)
             next.clear4(((g * GROUP + e / kRec4) * kAttnMaxChunks + c) * kRec4 + e % kRec4);
@@ -1479,7 +1479,7 @@ struct Roles {
     OutMap om;  // rows [2 u0, 2 u0 + 2 n), staged from element 2 u0 rounded down to 4
     om.take(2 * u0, 2 * ro.n, (2 * u0) & ~3, threadIdx.x, 0);
     loop(kRoleO, false, [&](uint32_t t, int l, int position) {
-      const int C = attn_chunks(position + 1, a.attn_parts);
+      const int C = attn_chunks(position + 1, a.attn_parts, kAttnGrain);
       const Slots out = s_h1(l, t, g);
       if (om.q >= 0) clear_quad(s_h1(l, t + 1, g), om);
       // Group 0 adds the residual: rows [2 u0, 2 u0 + 2 n) of the layer

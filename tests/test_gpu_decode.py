@@ -217,12 +217,12 @@ def test_resident_and_stream_generation_agree(full, stream_full):
 
 
 def test_resident_across_chunk_length_changes_matches_stream(full, stream_full):
-    """Attention chunks are whole 64-position passes split over the engine's
-    attention parts (9 on a 256-CU MI355X: chunks of 128 positions from
-    context 577, 192 from 1153): across context 1001..1170 the chunk count
-    grows from 8 to 9 at 1025 and drops to 7 at 1153. A resident generation
-    across both points equals the stream path bit for bit (hand-off slots
-    beyond the chunk count hold older records)."""
+    """Attention chunks are whole 16-position tiles split over the engine's
+    attention parts (9 on a 256-CU MI355X): across context 1001..1170 the
+    chunk length grows from 112 to 128 positions at 1009 and to 144 at 1153,
+    and the chunk count drops from 9 to 8 at 1009 and regrows to 9 at 1025.
+    A resident generation across these points equals the stream path bit
+    for bit (hand-off slots beyond the chunk count hold older records)."""
     eng, _ = full
     prompt = qo.fill_tokens(1000, 1, PROMPT_STREAM + 4, FULL.vocab)
     say("resident vs stream generation, context 1001..1170")
@@ -292,15 +292,16 @@ def test_resident_config2_context_512_matches_stream_and_oracle(full, stream_ful
 
 def test_resident_config3_context_4096_matches_stream_and_oracle(full, stream_full):
     """BASELINE config 3 as the bench runs it: the resident kernel at context
-    4065..4096 (on a 256-CU MI355X, 512-position chunks, 8 per KV head, each
-    walked in two LDS windows of 256 positions spread over the waves)."""
+    4065..4096 (on a 256-CU MI355X, 464-position chunks, 9 per KV head, each
+    walked in two LDS windows, its 16-position tiles spread over the waves
+    on MFMA)."""
     long_context_generation(full, stream_full, 4064, 32, 4242, "config 3 resident 4065..4096")
 
 
 def test_resident_multi_window_beyond_4096_matches_stream_and_oracle(full, stream_full):
-    """Across context 4096 (4091..4130) the chunk count grows from 8 to 9
-    (512-position chunks on a 256-CU MI355X), each chunk walked in LDS
-    windows of at most 256 positions."""
+    """Across context 4096 (4091..4130; 464-position chunks, 9 per KV head,
+    on a 256-CU MI355X), each chunk walked in LDS windows of at most 256
+    positions."""
     long_context_generation(full, stream_full, 4090, 40, 777, "resident 4091..4130 (two windows)")
 
 
