@@ -55,10 +55,10 @@ WEIGHT_BYTES = 1_976_131_072
 # the factors a 1 GiB device copy gives in the same profile
 # (profiles/roles_kernel_config2.md).
 # Re-measured when a kernel changes; None where no measurement exists.
-RESIDENT_TRAFFIC_PER_TOKEN = 2_006_755_521
+RESIDENT_TRAFFIC_PER_TOKEN = 2_006_118_720
 # The role-split kernel on a 64-token launch of the config-3 workload
 # (context 4065..4128; profiles/roles_kernel_config3.md).
-RESIDENT_TRAFFIC_PER_TOKEN_LONG = 2_093_851_768
+RESIDENT_TRAFFIC_PER_TOKEN_LONG = 2_093_356_640
 
 
 def step_bytes(length: int) -> int:
