@@ -155,11 +155,11 @@ struct qd_engine {
   int attn_parts = qd::kAttnMaxChunks;
   std::string resident_off_reason;
   // Prompt workspace (allocated on the first prefill): rows of the hidden
-  // states, RMSNorm output, packed QKV, attention output, gate|up and SwiGLU
+  // states, RMSNorm output, packed QKV, attention output and SwiGLU
   // activation, plus the chunk's token ids.
   static constexpr size_t kPrefillRows = 512;
   float *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr,
-        *pf_gu = nullptr, *pf_act = nullptr, *pf_split = nullptr;
+        *pf_act = nullptr, *pf_split = nullptr;
   // Split-K factors of the narrow GEMMs (QKV, O, down) so they fill the CUs.
   static constexpr int kSplitQkv = 2, kSplitO = 2, kSplitDown = 4;
   uint32_t *pf_tokens = nullptr;
@@ -458,14 +458,14 @@ struct qd_engine {
 
   // Kernels of the prompt path, for per-kernel event timing.
   enum PrefillKernel : int {
-    kPEmbed = 0, kPNorm, kPGemmQkv, kPRope, kPAttn, kPGemmO, kPGemmGateUp, kPSilu, kPGemmDown,
+    kPEmbed = 0, kPNorm, kPGemmQkv, kPRope, kPAttn, kPGemmO, kPGemmGateUp, kPGemmDown,
     kPTail, kPrefillKernels
   };
   static const char *prefill_kernel_name(int id) {
     static const char *const names[kPrefillKernels] = {
         "embed_rows_kernel",    "rmsnorm_rows_kernel",      "gemm_nt_kernel:qkv",
         "rope_kv_rows_kernel",  "attention_prefill_kernel", "gemm_nt_kernel:o",
-        "gemm_nt_kernel:gateup", "silu_mul_rows_kernel",    "gemm_nt_kernel:down",
+        "gemm_nt_kernel:gateup+swiglu", "gemm_nt_kernel:down",
         "lmhead_kernel+argmax"};
     return id >= 0 && id < kPrefillKernels ? names[id] : "unknown";
   }
@@ -484,19 +484,13 @@ struct qd_engine {
         return {(2 * (pos0 + n) * KVD + 2 * n * QD) * f,
                 4 * NQ * qd::kHeadDim * (n * pos0 + n * (n + 1) / 2)};
       case kPGemmO: return {(H * QD + n * (QD + 2 * H)) * f, 2 * n * H * QD};
-      case kPGemmGateUp: return {(2 * I * H + n * (H + 2 * I)) * f, 4 * n * I * H};
-      case kPSilu: return {3 * n * I * f, 0};
+      case kPGemmGateUp: return {(2 * I * H + n * (H + I)) * f, 4 * n * I * H};
       case kPGemmDown: return {(H * I + n * (I + 2 * H)) * f, 2 * n * H * I};
       case kPTail: return {(V * H + H + V) * f, 2 * V * H};
     }
     return {0, 0};
   }
 
-  bool wg_wu_adjacent() const {
-    for (const auto &w : layers)
-      if (w.wu != w.wg + I * H) return false;
-    return true;
-  }
 
   // One chunk of a prompt (n <= kPrefillRows tokens at positions
   // pos0 .. pos0 + n - 1 of slot seq) through every layer with the prompt
@@ -507,7 +501,6 @@ struct qd_engine {
       pf_xn = alloc<float>(kPrefillRows * H);
       pf_qkv = alloc<float>(kPrefillRows * QKV);
       pf_attn = alloc<float>(kPrefillRows * QD);
-      pf_gu = alloc<float>(kPrefillRows * 2 * I);
       pf_act = alloc<float>(kPrefillRows * I);
       pf_tokens = alloc<uint32_t>(kPrefillRows);
       pf_split = alloc<float>(kPrefillRows * std::max({kSplitQkv * QKV, kSplitO * H, kSplitDown * H}));
@@ -543,13 +536,9 @@ struct qd_engine {
       });
       span(kPNorm, "norm",
            [&] { return qd::launch_rmsnorm_rows(stream, pf_h, w.mlp_norm, cfg.rms_eps, n, pf_xn); });
-      // wg and wu are adjacent in the arena: one GEMM over [gate; up] rows.
-      span(kPGemmGateUp, "gate/up gemm", [&] {
-        return qd::launch_gemm_nt(stream, pf_xn, h, w.wg, h, pf_gu, 2 * in, n, 2 * in, h,
-                                  qd::kGemmStore, nullptr);
+      span(kPGemmGateUp, "gate/up gemm + swiglu", [&] {
+        return qd::launch_gemm_swiglu(stream, pf_xn, h, w.wg, w.wu, h, pf_act, in, n, in, h);
       });
-      span(kPSilu, "swiglu",
-           [&] { return qd::launch_silu_mul_rows(stream, pf_gu, n, in, pf_act); });
       span(kPGemmDown, "down gemm", [&] {
         return qd::launch_gemm_nt(stream, pf_act, in, w.wd, in, pf_h, h, n, h, in,
                                   qd::kGemmAccumulate, nullptr, kSplitDown, pf_split);
@@ -1416,8 +1405,6 @@ void check_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t 
   for (uint32_t i = 0; i < n; ++i)
     if (tokens[i] >= e->V) fail(QD_ERROR_INVALID_ARGUMENT, "token %u at %u >= vocab", tokens[i], i);
   e->set_device();
-  if (!e->bf16 && !e->wg_wu_adjacent())
-    fail(QD_ERROR_NOT_SUPPORTED, "prefill needs the gate and up weights adjacent");
 }
 
 // The prompt in chunks of up to kPrefillRows positions, each through all

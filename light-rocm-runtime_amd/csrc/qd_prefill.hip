@@ -29,89 +29,147 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 // ---- GEMM: C = A . W^T --------------------------------------------------------
 // 64 x 64 output tile per workgroup, four waves of 32 x 32 (one
-// v_mfma_f32_32x32x2f32 accumulator each). K is consumed in slices of 32,
-// staged in LDS k-major (padded rows, conflict-free operand reads) and
-// double-buffered: the next slice's global loads are in flight while the
-// current slice feeds the matrix cores.
+// v_mfma_f32_32x32x2f32 accumulator each). K is consumed in slices of 32
+// through a ring of kStages LDS stages filled by global -> LDS DMA
+// (global_load_lds_dwordx4, no register staging): while slice s feeds the
+// matrix cores, slices s + 1 .. s + kStages - 1 are in flight, so the
+// slices' load latency overlaps the MFMA work of the ones before.
 // Operand layout of v_mfma_f32_32x32x2f32: lane l supplies A[l % 32][l / 32]
 // and B[l / 32][l % 32]; accumulator register r of lane l holds
 // D[(r / 4) * 8 + (l / 32) * 4 + r % 4][l % 32].
+// A stage holds the A and W tiles row-major, 32 floats (8 float4 slots) per
+// row, float4 slot p of row r holding the row's k-quad p ^ (r % 8): a DMA
+// instruction writes 8 whole rows (1 KiB) and each lane picks the source
+// quad that lands in its slot; the operand reads (one float4 per lane, rows
+// of eight consecutive lanes at one k-quad) then fall on 32 distinct banks.
+// Lane l reads k-quad 2 j + l / 32 of its row and feeds it to four MFMAs,
+// so MFMA (j, c) takes k = 8 j + 4 (l / 32) + c, in A and in B alike.
 constexpr int kTileM = 64, kTileN = 64, kTileK = 32;
-constexpr int kLdsRow = kTileM + 32;  // floats per k-row of a staged tile
+constexpr int kStages = 4;
+constexpr int kStageFloats = (kTileM + kTileN) * kTileK;
+
+typedef __attribute__((address_space(3))) void gemm_lds_void;
+
+// One 16-byte global -> LDS DMA per lane (lane l's bytes land at the stage
+// offset lds + 16 l). Issued from inline assembly: the compiler would
+// otherwise guard every later LDS read with a wait for all DMAs in flight,
+// serialising the stages; the kernel waits for each slice itself (vmcnt,
+// which counts these loads).
+__device__ __forceinline__ void gemm_dma16(const float *src, const float *lds) {
+  const uint32_t off = static_cast<uint32_t>(
+      __builtin_amdgcn_readfirstlane(static_cast<int>(reinterpret_cast<uintptr_t>((gemm_lds_void *)lds))));
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(off), "v"(src) : "memory", "m0");
+}
+// Workgroup barrier over LDS only: each wave's own LDS operations complete
+// first; its DMAs are waited for explicitly before it.
+__device__ __forceinline__ void gemm_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Split-K: slice z = blockIdx.z of gridDim.z covers k range [z k / Z,
 // (z + 1) k / Z) and, when Z > 1, writes its plain partial product to
 // C + z * m * ldc (the caller's workspace); gemm_reduce_kernel then sums the
 // partials in slice order and applies the epilogue.
+//
+// SwiGLU mode (kGemmSwiGLU): tile x covers outputs [32 x, 32 x + 32) of
+// act = silu(A . wg^T) * (A . wu^T); its W tile's first 32 rows are wg's
+// rows of that range and its last 32 wu's (W2), so waves (wr, 0) hold the
+// gate sums and waves (wr, 1) the up sums of the same elements; the up sums
+// cross through LDS and waves (wr, 0) store silu_mul(gate, up).
 __global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict__ A, int lda,
-                                                         const float *__restrict__ W, int ldw,
+                                                         const float *__restrict__ W,
+                                                         const float *__restrict__ W2, int ldw,
                                                          float *__restrict__ C, int ldc, int m,
                                                          int n, int k, int mode,
                                                          const float *__restrict__ bias) {
-  __shared__ float as[2][kTileK][kLdsRow];
-  __shared__ float ws[2][kTileK][kLdsRow];
-  const int t = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) float stage_lds[kStages * kStageFloats];
   const int lane = lane_id();
   const int w = wave_id();
   const int wr = w >> 1, wc = w & 1;
   const int m0 = blockIdx.y * kTileM, n0 = blockIdx.x * kTileN;
-  // Each thread stages two float4 of A and two of W per slice: float4 f =
-  // t + 256 i covers row f % 64, columns 4 (f / 64) .. +3 of the slice (the
-  // lanes of a wave take consecutive rows: conflict-free LDS writes).
-  float4 ra[2], rw[2];
-  auto fetch = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int f = t + kBlock * i;
-      const int row = f & 63, c4 = f >> 6;
-      const int gm = m0 + row, gn = n0 + row;
-      ra[i] = gm < m ? *reinterpret_cast<const float4 *>(A + static_cast<size_t>(gm) * lda + k0 + 4 * c4)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-      rw[i] = gn < n ? *reinterpret_cast<const float4 *>(W + static_cast<size_t>(gn) * ldw + k0 + 4 * c4)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int f = t + kBlock * i;
-      const int row = f & 63, c4 = f >> 6;
-      as[buf][4 * c4 + 0][row] = ra[i].x;
-      as[buf][4 * c4 + 1][row] = ra[i].y;
-      as[buf][4 * c4 + 2][row] = ra[i].z;
-      as[buf][4 * c4 + 3][row] = ra[i].w;
-      ws[buf][4 * c4 + 0][row] = rw[i].x;
-      ws[buf][4 * c4 + 1][row] = rw[i].y;
-      ws[buf][4 * c4 + 2][row] = rw[i].z;
-      ws[buf][4 * c4 + 3][row] = rw[i].w;
-    }
-  };
-  f16v acc = {};
   const int split = gridDim.z;
   const int slices_all = k / kTileK;
   const int s_begin = static_cast<int>(blockIdx.z) * slices_all / split;
   const int s_end = (static_cast<int>(blockIdx.z) + 1) * slices_all / split;
-  A += s_begin * kTileK;
-  W += s_begin * kTileK;
   if (split > 1) {
     C += static_cast<size_t>(blockIdx.z) * m * ldc;
     mode = kGemmStore;
   }
   const int slices = s_end - s_begin;
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int s = 0; s < slices; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < slices) fetch((s + 1) * kTileK);
+  // DMA of slice s into stage b: instruction i of a tile covers rows
+  // 8 i .. 8 i + 7; this wave issues instructions w and w + 4 of the A tile
+  // and of the W tile. Lane l fills slot l % 8 of row 8 i + l / 8. Rows past
+  // m read row m - 1 (their products are never stored); W has n rows.
+  const int drow = lane >> 3, dslot = (lane & 7) ^ drow;
+  auto issue = [&](int sl, int b) {
+    float *st = stage_lds + b * kStageFloats;
+    const int k0 = (s_begin + sl) * kTileK + 4 * dslot;
 #pragma unroll
-    for (int kk = 0; kk < kTileK / 2; ++kk) {
-      const float a = as[buf][2 * kk + (lane >> 5)][wr * 32 + (lane & 31)];
-      const float b = ws[buf][2 * kk + (lane >> 5)][wc * 32 + (lane & 31)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
+    for (int h = 0; h < 2; ++h) {
+      const int i = w + 4 * h;
+      const int ra = min(m0 + 8 * i + drow, m - 1);
+      const float *wrow;
+      if (mode == kGemmSwiGLU) {
+        const int j = blockIdx.x * (kTileN / 2) + 8 * (i & 3) + drow;
+        wrow = (i < 4 ? W : W2) + static_cast<size_t>(j) * ldw;
+      } else {
+        wrow = W + static_cast<size_t>(min(n0 + 8 * i + drow, n - 1)) * ldw;
+      }
+      gemm_dma16(A + static_cast<size_t>(ra) * lda + k0, st + 8 * i * kTileK);
+      gemm_dma16(wrow + k0, st + kTileM * kTileK + 8 * i * kTileK);
     }
-    if (s + 1 < slices) stash(buf ^ 1);
-    __syncthreads();
+  };
+  // This lane's operand rows and their swizzle.
+  const int ar = wr * 32 + (lane & 31), br = wc * 32 + (lane & 31);
+  const int half = lane >> 5;
+  f16v acc = {};
+#pragma unroll
+  for (int st = 0; st < kStages - 1; ++st)
+    if (st < slices) issue(st, st);
+  for (int sl = 0; sl < slices; ++sl) {
+    // Slice sl's DMA has landed once at most 4 (per later slice in flight)
+    // of this wave's loads are outstanding; the barrier makes every wave's
+    // part visible and retires every wave's reads of the stage refilled next.
+    const int ahead = min(kStages - 2, slices - 1 - sl);
+    if (ahead >= 2)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (ahead == 1)
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    gemm_lds_barrier();
+    if (sl + kStages - 1 < slices) issue(sl + kStages - 1, (sl + kStages - 1) % kStages);
+    const float *st = stage_lds + (sl % kStages) * kStageFloats;
+    float4 av[4], bv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int q = 2 * j + half;
+      av[j] = *reinterpret_cast<const float4 *>(st + ar * kTileK + 4 * (q ^ (ar & 7)));
+      bv[j] = *reinterpret_cast<const float4 *>(st + kTileM * kTileK + br * kTileK + 4 * (q ^ (br & 7)));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j].x, bv[j].x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j].y, bv[j].y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j].z, bv[j].z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j].w, bv[j].w, acc, 0, 0, 0);
+    }
+  }
+  if (mode == kGemmSwiGLU) {
+    float *ex = stage_lds;  // [wr][r][lane] up sums
+    gemm_lds_barrier();     // every wave is done with the last stage
+    if (wc == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ex[(wr * 16 + r) * kWave + lane] = acc[r];
+    }
+    gemm_lds_barrier();
+    if (wc == 0) {
+      const int col = blockIdx.x * (kTileN / 2) + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wr * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (row < m) C[static_cast<size_t>(row) * ldc + col] = silu_mul(acc[r], ex[(wr * 16 + r) * kWave + lane]);
+      }
+    }
+    return;
   }
   const int col = n0 + wc * 32 + (lane & 31);
   if (col >= n) return;
@@ -208,17 +266,6 @@ __global__ __launch_bounds__(kBlock) void rope_kv_rows_kernel(float *__restrict_
       const int o = u - rotations;
       v_cache[static_cast<size_t>(p) * kvd + o] = row[qd + kvd + o];
     }
-  }
-}
-
-__global__ __launch_bounds__(kBlock) void silu_mul_rows_kernel(const float *__restrict__ gu, int inter,
-                                                               float *__restrict__ act) {
-  const int r = blockIdx.x;
-  const float *g = gu + static_cast<size_t>(r) * 2 * inter;
-  float *o = act + static_cast<size_t>(r) * inter;
-  for (int i = threadIdx.x; i < inter; i += kBlock) {
-    const float gv = g[i];
-    o[i] = gv / (1.f + expf(-gv)) * g[inter + i];
   }
 }
 
@@ -410,8 +457,9 @@ hipError_t launch_gemm_nt(hipStream_t s, const float *A, int lda, const float *W
   if (k % kTileK != 0 || m <= 0 || n <= 0 || split < 1 || split > k / kTileK ||
       (split > 1 && !workspace))
     return hipErrorInvalidValue;
+  if (mode == kGemmSwiGLU) return hipErrorInvalidValue;
   const dim3 grid((n + kTileN - 1) / kTileN, (m + kTileM - 1) / kTileM, split);
-  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, W, ldw, split > 1 ? workspace : C, ldc, m, n, k,
+  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, W, nullptr, ldw, split > 1 ? workspace : C, ldc, m, n, k,
                                          mode, bias);
   if (split > 1) {
     const size_t total = static_cast<size_t>(m) * n;
@@ -449,8 +497,11 @@ hipError_t launch_attention_prefill(hipStream_t s, const float *qkv, int rows, i
   return hipGetLastError();
 }
 
-hipError_t launch_silu_mul_rows(hipStream_t s, const float *gu, int rows, int inter, float *act) {
-  silu_mul_rows_kernel<<<rows, kBlock, 0, s>>>(gu, inter, act);
+hipError_t launch_gemm_swiglu(hipStream_t s, const float *A, int lda, const float *wg, const float *wu,
+                              int ldw, float *act, int ldc, int m, int inter, int k) {
+  if (k % kTileK != 0 || m <= 0 || inter <= 0 || inter % (kTileN / 2) != 0) return hipErrorInvalidValue;
+  const dim3 grid(inter / (kTileN / 2), (m + kTileM - 1) / kTileM, 1);
+  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, wg, wu, ldw, act, ldc, m, 2 * inter, k, kGemmSwiGLU, nullptr);
   return hipGetLastError();
 }
 

@@ -11,8 +11,9 @@
 
 namespace qd {
 
-// GEMM epilogues: C = A . W^T (+ bias) or C += A . W^T (residual).
-enum GemmMode : int { kGemmStore = 0, kGemmBias = 1, kGemmAccumulate = 2 };
+// GEMM epilogues: C = A . W^T (+ bias) or C += A . W^T (residual); and the
+// MLP's gate/up GEMM with SwiGLU fused (launch_gemm_swiglu).
+enum GemmMode : int { kGemmStore = 0, kGemmBias = 1, kGemmAccumulate = 2, kGemmSwiGLU = 3 };
 
 // C[m][n] (row stride ldc) for A [m][k] (stride lda) and W [n][k] (stride
 // ldw), all FP32 row-major. m, n any size (edges masked); k a multiple of 32.
@@ -43,7 +44,10 @@ hipError_t launch_attention_prefill(hipStream_t s, const float *qkv, int rows, i
                                     int nkv, const float *k_cache, const float *v_cache,
                                     float *out);
 
-// act[r][i] = silu(gu[r][i]) * gu[r][inter + i].
-hipError_t launch_silu_mul_rows(hipStream_t s, const float *gu, int rows, int inter, float *act);
+// act[r][i] = silu(A[r] . wg[i]) * (A[r] . wu[i]) for r < m, i < inter
+// (act row stride ldc; wg and wu [inter][k] with row stride ldw; inter a
+// multiple of 32, k of 32): the gate and up GEMMs and SwiGLU in one launch.
+hipError_t launch_gemm_swiglu(hipStream_t s, const float *A, int lda, const float *wg, const float *wu,
+                              int ldw, float *act, int ldc, int m, int inter, int k);
 
 }  // namespace qd
