@@ -344,19 +344,30 @@ __global__ __launch_bounds__(kBlock) void attention_prefill_kernel(
   float (*ks)[kKRow] = sh.k[w];
   float (*vs)[kVRow] = sh.v[w];
   float (*ps)[kPRow] = sh.p[w];
+  // The block's K and V rows in registers: lane covers rows lane / 16 +
+  // 4 i, float4 column lane % 16 (zeros past the causal extent). The wave's
+  // next block is loaded while the current one is computed.
+  float4 kr[kKBlock / 4], vr[kKBlock / 4];
+  auto load_block = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < kKBlock / 4; ++i) {
+      const int j = kb * kKBlock + lg + 4 * i;
+      kr[i] = vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (j < keys) {
+        kr[i] = *reinterpret_cast<const float4 *>(k_cache + static_cast<size_t>(j) * kvd + g * kHeadDim + 4 * lr);
+        vr[i] = *reinterpret_cast<const float4 *>(v_cache + static_cast<size_t>(j) * kvd + g * kHeadDim + 4 * lr);
+      }
+    }
+  };
+  if (w < kblocks) load_block(w);
   for (int kb = w; kb < kblocks; kb += kWavesPerBlock) {
     const int k0 = kb * kKBlock;
-    // Stage the block's K and V rows: lane covers rows lane / 16 + 4 i,
-    // float4 column lane % 16.
+    // Stage the block's rows in the wave's LDS, then start the next block's
+    // loads.
 #pragma unroll
     for (int i = 0; i < kKBlock / 4; ++i) {
       const int row = lg + 4 * i;
-      const int j = k0 + row;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (j < keys) {
-        kv = *reinterpret_cast<const float4 *>(k_cache + static_cast<size_t>(j) * kvd + g * kHeadDim + 4 * lr);
-        vv = *reinterpret_cast<const float4 *>(v_cache + static_cast<size_t>(j) * kvd + g * kHeadDim + 4 * lr);
-      }
+      const float4 kv = kr[i], vv = vr[i];
       ks[row][4 * lr + 0] = kv.x;
       ks[row][4 * lr + 1] = kv.y;
       ks[row][4 * lr + 2] = kv.z;
@@ -366,6 +377,7 @@ __global__ __launch_bounds__(kBlock) void attention_prefill_kernel(
       vs[row][4 * lr + 2] = vv.z;
       vs[row][4 * lr + 3] = vv.w;
     }
+    if (kb + kWavesPerBlock < kblocks) load_block(kb + kWavesPerBlock);
     // S tiles: keys k0 + 16 tt + lr.
     f4v s[2];
 #pragma unroll
