@@ -2,17 +2,18 @@
 // megakernel, so both paths run the same arithmetic in the same order.
 //
 // Split-KV: the attended positions 0..L-1 are cut into chunks of
-// attn_chunk_len(L, parts, kAttnGrain) positions (a multiple of the
-// 16-position tile, at most kAttnMaxChunks chunks). A chunk of one KV group
-// is one workgroup's work, computed in one of two ways fixed by the chunk
-// length, so every path agrees:
+// attn_chunk_len(L, parts, kAttnGrain) positions (a multiple of 16, at most
+// kAttnMaxChunks chunks). A chunk of one KV group is one workgroup's work,
+// computed in one of two ways fixed by the chunk length, so every path
+// agrees:
 //  - one block (up to 64 positions, attn_single_block): one wave per query
 //    head forms the block's softmax partial on the vector ALUs
 //    (attn_block_valu);
-//  - longer: the chunk is cut into tiles of 16 positions, dealt round-robin
+//  - longer: the chunk is cut into tiles of 32 positions, dealt round-robin
 //    to kAttnSlots waves; each wave keeps an online-softmax partial of all
-//    the group's heads over its tiles (scores and P.V on FP32 MFMA,
-//    attn_tile), and the wave partials are folded in slot order.
+//    the group's heads (up to kAttnMaxGroup) over its tiles (scores and P.V
+//    on FP32 MFMA in 4x4 blocks, attn_tile), and the wave partials are
+//    folded in slot order.
 // Either way each head gets one record (max m, sum l, acc[64]) per chunk. A
 // merge combines the records of a head:
 // out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c (scores and maxima
@@ -147,298 +148,192 @@ __host__ __device__ inline bool attn_single_block(int chunk_len) { return chunk_
 
 typedef float attn_f4v __attribute__((ext_vector_type(4)));
 
-// Positions per tile: the N (scores) and K (P.V) extent of one
-// v_mfma_f32_16x16x4f32 pass. A chunk's tiles start at the chunk's first
-// position; tile i of a chunk belongs to tile slot i % kAttnSlots.
-constexpr int kAttnTile = 16;
 // Tile slots per (chunk, KV group): the waves of one attention workgroup.
+// Tile i of a chunk belongs to tile slot i % kAttnSlots.
 constexpr int kAttnSlots = 8;
-// Probability tile of one wave in LDS: [16 heads][16 positions], rows
-// padded to 17 floats so the column reads of the P.V operand do not collide.
-constexpr int kAttnPsStride = 17;
-constexpr int kAttnPsFloats = 16 * kAttnPsStride;
 
-// One wave's running softmax partial over its tiles (base-2 units). Lane l
-// holds query rows 4 (l / 16) + r (r = 0..3; rows past the group's heads are
-// padding): max m[r], sum l[r], and o[n][r], the row's output dim 16 n + l % 16.
+// Component c of a float4.
+__device__ __forceinline__ float attn_c(float4 v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }
+
+// ---- Tiles of a longer chunk (groups of up to 8 heads) ---------------------
+// One v_mfma_f32_4x4x1f32 is 16 independent 4x4 outer products: block b =
+// lane / 4; lane 4 b + i gives row i of A and column i of B; register r of
+// lane 4 b + j receives element (r, j) of the block's D. Eight heads are two
+// head quads, so the 16 blocks cover 8 heads by 32 positions (or 32 dims),
+// and 7 of the 8 rows do work for a group of 7, where a 16x16x4 MFMA would use 7
+// of 16. Lane l: head quad hq = l / 32, m = l % 32, x = l % 4.
+// Both halves of the wave need the same K and V operands, so each half
+// loads one half of them and the MFMA's B broadcast (BLGP 1: lanes 0-31's B
+// for all 64 lanes; BLGP 2: lanes 32-63's) hands them to the other: each K
+// and V element is read from LDS once per tile.
+//   scores: block b has head rows 4 hq + 0..3 and positions 4 (b % 8) +
+//           0..3; lanes 0-31 hold K dims 0-31 of position t0 + m, lanes
+//           32-63 dims 32-63 of the same position; lane l ends holding
+//           position t0 + m of rows 4 hq + r (register r);
+//   P.V:    the same blocks with output dims as columns; lane l holds
+//           element l of each V row; lane l ends holding rows 4 hq + r of
+//           dims m (BLGP 1) and 32 + m (BLGP 2).
+constexpr int kAttnTile = 32;
+constexpr int kAttnMaxGroup = 8;
+// Probability tile of one wave in LDS: [8 rows][32 positions], rows 36 floats
+// apart (16-byte aligned, the 8 rows' float4 reads on distinct banks).
+constexpr int kAttnTilePsStride = 36;
+constexpr int kAttnTilePsFloats = kAttnMaxGroup * kAttnTilePsStride;
+// LDS of one wave for its probabilities: a tile's [8][36], or the 64 of a
+// one-block chunk's head (PLds at offset 4).
+constexpr int kAttnPsFloats = kAttnTilePsFloats;
+static_assert(kAttnPsFloats >= 4 + kWave, "one-block probabilities fit the wave's LDS");
+
+// One wave's running softmax partial over its tiles (base-2
+// units): m[r], the running max of row 4 hq + r (equal on the half's 32
+// lanes); l[r], this lane's share of the row's running sum (the
+// probabilities of position m of each tile; the half's 32 shares sum to the
+// row's sum); o[s][r], row 4 hq + r of output dim 32 s + m.
 struct AttnAcc {
   float m[4], l[4];
-  attn_f4v o[4];
+  attn_f4v o[2];
   __device__ __forceinline__ void init() {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       m[r] = -INFINITY;
       l[r] = 0.f;
-      o[r] = attn_f4v{0.f, 0.f, 0.f, 0.f};
     }
+    o[0] = o[1] = attn_f4v{0.f, 0.f, 0.f, 0.f};
   }
 };
 
-// Query operand of a group of up to 16 heads: qa[s] = float4 (4 s + l / 16)
-// of head l % 16's query (zero past the group's `heads`). q4(h, d4) returns
-// float4 d4 of head h's query.
+// Query operand of a group of up to 8 heads: q[d4] = float4 d4 of the query
+// of head 4 (l / 32) + l % 4 (zero past the group's `heads`). q4(h, d4)
+// returns float4 d4 of head h's query.
 template <typename Q4>
-__device__ __forceinline__ void attn_query(Q4 q4, int heads, float4 (&qa)[4]) {
-  const int col = lane_id() & 15, quad = lane_id() >> 4;
+__device__ __forceinline__ void attn_query(Q4 q4, int heads, float4 (&q)[kHeadDim / 4]) {
+  const int row = 4 * (lane_id() >> 5) + (lane_id() & 3);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) qa[s] = col < heads ? q4(col, 4 * s + quad) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int d4 = 0; d4 < kHeadDim / 4; ++d4) q[d4] = row < heads ? q4(row, d4) : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-// Component c of a float4.
-__device__ __forceinline__ float attn_c(float4 v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }
-
-// One tile of 16 positions [t0, t0 + 16) for every head of a KV group, on
-// MFMA (the group's heads are the M rows, padded to 16; K and V are read
-// once for all of them). Positions >= end are masked: their score is -inf
-// and their K/V reads take position end - 1, so no value read past the
-// context reaches the sums. k4(pos, d4): float4 d4 of position pos's K row;
-// v(pos, d): element d of its V row; ps: this wave's kAttnPsFloats of LDS.
-//   S[h][j] = q_h . k_j over 64 dims: 16 MFMAs in four chains, chain s
-//             taking dims 16 s + 4 (l / 16) + c of lane l at its k-step c
-//             (c = 0..3), the chains summed as (s0 + s1) + (s2 + s3);
-//             scaled into base-2 units by kScoreScaleLog2;
-//   online softmax per row: m' = max(m, row16_max of the tile), c =
-//             2^(m - m') (0 for the first tile), p = 2^(s - m'),
-//             l = l c + row16_sum(p), o = o c (rounded products);
-//   o += P . V: k-step s covers positions 4 s .. 4 s + 3, N tile n dims
-//             16 n .. 16 n + 15 (16 MFMAs).
-// The four rows' reductions go step by step together, so their exchanges
-// interleave. The resident kernel and the stream-ordered kernel both run
-// it, so their partials are bit-identical.
-template <typename K4, typename V>
-__device__ __forceinline__ void attn_tile(const float4 (&qa)[4], K4 k4, V v, float *ps, int t0, int end,
-                                          AttnAcc &acc) {
-  const int lane = lane_id(), col = lane & 15, quad = lane >> 4;
-  const int pk = min(t0 + col, end - 1);
-  float4 kb[4];
+// One tile of 32 positions [t0, t0 + 32) for every head of a KV group of up
+// to 8. Positions >= end are masked (score -inf). kl(i): float4 i of this
+// lane's half of its position's K row (dims 32 hq + 4 i .. 32 hq + 4 i + 3 of
+// position min(t0 + m, end - 1)); vl(k): element `lane` of the V row of
+// position min(t0 + k, end - 1) (k = 0..31); ps: this wave's
+// kAttnTilePsFloats of LDS.
+//   S[h][j] = q_h . k_j: 64 MFMAs in four chains: dims 4 i + c (i < 8,
+//             BLGP 1) and 32 + 4 i + c (BLGP 2) at step (i, c), chain
+//             2 (i % 2) + half; the chains summed as (s0 + s1) + (s2 + s3);
+//             scaled by kScoreScaleLog2;
+//   online softmax per row: m' = max(m, half_max of the tile's scores),
+//             c = 2^(m - m') (0 for the first tile), p = 2^(s - m'),
+//             l = l c + p (per lane), o = o c (rounded products);
+//   o += P . V: positions in order, one MFMA per position and dim half.
+template <typename KL, typename VL>
+__device__ __forceinline__ void attn_tile_ops(const float4 (&q)[kHeadDim / 4], KL kl, VL vl, float *ps, int t0,
+                                              int end, AttnAcc &acc) {
+  const int lane = lane_id(), hq = lane >> 5, m = lane & 31, x = lane & 3;
+  float4 kv[kHeadDim / 8];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) kb[s] = k4(pk, 4 * s + quad);
-  float vb[4][4];
+  for (int i = 0; i < kHeadDim / 8; ++i) kv[i] = kl(i);
+  attn_f4v s[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int pv = min(t0 + 4 * s + quad, end - 1);
+  for (int u = 0; u < 4; ++u) s[u] = attn_f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int n = 0; n < 4; ++n) vb[s][n] = v(pv, 16 * n + col);
+  for (int i = 0; i < kHeadDim / 8; ++i) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float b = attn_c(kv[i], c);
+      s[2 * (i & 1)] = __builtin_amdgcn_mfma_f32_4x4x1f32(attn_c(q[i], c), b, s[2 * (i & 1)], 0, 0, 1);
+      s[2 * (i & 1) + 1] =
+          __builtin_amdgcn_mfma_f32_4x4x1f32(attn_c(q[kHeadDim / 8 + i], c), b, s[2 * (i & 1) + 1], 0, 0, 2);
+    }
   }
-  attn_f4v sp[4];
+  const attn_f4v sc = (s[0] + s[1]) + (s[2] + s[3]);
+  const bool valid = t0 + m < end;
+  float xs[4], mx[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) sp[s] = attn_f4v{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < 4; ++r) xs[r] = valid ? __fmul_rn(sc[r], kScoreScaleLog2) : -INFINITY;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      sp[s] = __builtin_amdgcn_mfma_f32_16x16x4f32(attn_c(qa[s], c), attn_c(kb[s], c), sp[s], 0, 0, 0);
-  }
-  const attn_f4v sc = (sp[0] + sp[1]) + (sp[2] + sp[3]);
-  const bool valid = t0 + col < end;
-  float x[4], mx[4], cr[4], p[4], sm[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) x[r] = valid ? __fmul_rn(sc[r], kScoreScaleLog2) : -INFINITY;
-  // row16_max of each row, then with the running max.
-#pragma unroll
-  for (int r = 0; r < 4; ++r) mx[r] = fmaxf(x[r], dpp<kDppXor1>(x[r]));
+  for (int r = 0; r < 4; ++r) mx[r] = fmaxf(xs[r], dpp<kDppXor1>(xs[r]));
 #pragma unroll
   for (int r = 0; r < 4; ++r) mx[r] = fmaxf(mx[r], dpp<kDppXor2>(mx[r]));
 #pragma unroll
   for (int r = 0; r < 4; ++r) mx[r] = fmaxf(mx[r], dpp<kDppHalfMirror>(mx[r]));
 #pragma unroll
-  for (int r = 0; r < 4; ++r) mx[r] = fmaxf(acc.m[r], fmaxf(mx[r], dpp<kDppMirror>(mx[r])));
+  for (int r = 0; r < 4; ++r) mx[r] = fmaxf(mx[r], dpp<kDppMirror>(mx[r]));
+#pragma unroll
+  for (int r = 0; r < 4; ++r) mx[r] = fmaxf(acc.m[r], row_pair_max(mx[r]));
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    cr[r] = acc.m[r] == -INFINITY ? 0.f : exp2_fast(acc.m[r] - mx[r]);
-    p[r] = exp2_fast(x[r] - mx[r]);
-    ps[(4 * quad + r) * kAttnPsStride + col] = p[r];
-  }
-  // row16_sum of each row's probabilities.
-#pragma unroll
-  for (int r = 0; r < 4; ++r) sm[r] = p[r] + dpp<kDppXor1>(p[r]);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) sm[r] += dpp<kDppXor2>(sm[r]);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) sm[r] += dpp<kDppHalfMirror>(sm[r]);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    sm[r] += dpp<kDppMirror>(sm[r]);
-    acc.l[r] = fmaf(acc.l[r], cr[r], sm[r]);
+    const float cr = acc.m[r] == -INFINITY ? 0.f : exp2_fast(acc.m[r] - mx[r]);
+    const float p = exp2_fast(xs[r] - mx[r]);
+    ps[(4 * hq + r) * kAttnTilePsStride + m] = p;
+    acc.l[r] = fmaf(acc.l[r], cr, p);
     acc.m[r] = mx[r];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) acc.o[n][r] = __fmul_rn(acc.o[n][r], cr[r]);
+    acc.o[0][r] = __fmul_rn(acc.o[0][r], cr);
+    acc.o[1][r] = __fmul_rn(acc.o[1][r], cr);
   }
   // Lanes read each other's probabilities: order the wave's LDS writes.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float4 pa[kAttnTile / 4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const float a = ps[col * kAttnPsStride + 4 * s + quad];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) acc.o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vb[s][n], acc.o[n], 0, 0, 0);
-  }
+  for (int k4 = 0; k4 < kAttnTile / 4; ++k4)
+    pa[k4] = reinterpret_cast<const float4 *>(ps + (4 * hq + x) * kAttnTilePsStride)[k4];
   // The next tile rewrites ps only after every lane has read it.
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Two tiles [ta, ta + 16) and [tb, tb + 16) of one wave taken together, as
-// one online-softmax step over both (their chains interleave): S of each
-// tile as in attn_tile; m' = max(m, max(tile a max, tile b max)); c and p as
-// in attn_tile; l = l c + (row16_sum(p_a) + row16_sum(p_b)); o = o c, then
-// o += P_a . V_a, then P_b . V_b. ps: one probability tile, as attn_tile's.
-template <typename K4, typename V>
-__device__ __forceinline__ void attn_tile2(const float4 (&qa)[4], K4 k4, V v, float *ps, int ta, int tb, int end,
-                                           AttnAcc &acc) {
-  const int lane = lane_id(), col = lane & 15, quad = lane >> 4;
-  const int t0[2] = {ta, tb};
-  float4 kb[2][4];
-  float vb[2][4][4];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int pk = min(t0[u] + col, end - 1);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) kb[u][s] = k4(pk, 4 * s + quad);
-  }
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int pv = min(t0[u] + 4 * s + quad, end - 1);
-#pragma unroll
-      for (int n = 0; n < 4; ++n) vb[u][s][n] = v(pv, 16 * n + col);
-    }
-  }
-  attn_f4v sp[2][4];
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int s = 0; s < 4; ++s) sp[u][s] = attn_f4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-        sp[u][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(attn_c(qa[s], c), attn_c(kb[u][s], c), sp[u][s], 0, 0, 0);
-    }
-  }
-  float x[2][4], mx[2][4];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const attn_f4v sc = (sp[u][0] + sp[u][1]) + (sp[u][2] + sp[u][3]);
-    const bool valid = t0[u] + col < end;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) x[u][r] = valid ? __fmul_rn(sc[r], kScoreScaleLog2) : -INFINITY;
-  }
-  // row16_max of each row of both tiles, step by step.
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mx[u][r] = fmaxf(x[u][r], dpp<kDppXor1>(x[u][r]));
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mx[u][r] = fmaxf(mx[u][r], dpp<kDppXor2>(mx[u][r]));
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mx[u][r] = fmaxf(mx[u][r], dpp<kDppHalfMirror>(mx[u][r]));
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mx[u][r] = fmaxf(mx[u][r], dpp<kDppMirror>(mx[u][r]));
-  float mn[4], cr[4], p[2][4], sm[2][4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    mn[r] = fmaxf(acc.m[r], fmaxf(mx[0][r], mx[1][r]));
-    cr[r] = acc.m[r] == -INFINITY ? 0.f : exp2_fast(acc.m[r] - mn[r]);
-  }
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) p[u][r] = exp2_fast(x[u][r] - mn[r]);
-  // The A operands of both tiles through the one probability tile: tile a's
-  // written and read, then tile b's.
-  float pa[2][4];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) ps[(4 * quad + r) * kAttnPsStride + col] = p[u][r];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int s = 0; s < 4; ++s) pa[u][s] = ps[col * kAttnPsStride + 4 * s + quad];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-  // row16_sum of each row's probabilities of both tiles.
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sm[u][r] = p[u][r] + dpp<kDppXor1>(p[u][r]);
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sm[u][r] += dpp<kDppXor2>(sm[u][r]);
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sm[u][r] += dpp<kDppHalfMirror>(sm[u][r]);
-#pragma unroll
-  for (int u = 0; u < 2; ++u)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sm[u][r] += dpp<kDppMirror>(sm[u][r]);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    acc.l[r] = fmaf(acc.l[r], cr[r], sm[0][r] + sm[1][r]);
-    acc.m[r] = mn[r];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) acc.o[n][r] = __fmul_rn(acc.o[n][r], cr[r]);
-  }
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int n = 0; n < 4; ++n)
-        acc.o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[u][s], vb[u][s][n], acc.o[n], 0, 0, 0);
-    }
+  for (int k = 0; k < kAttnTile; ++k) {
+    const float vv = vl(k);
+    const float a = attn_c(pa[k / 4], k % 4);
+    acc.o[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, vv, acc.o[0], 0, 0, 1);
+    acc.o[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, vv, acc.o[1], 0, 0, 2);
   }
 }
 
-// The tiles of slot `slot` that lie in [wb, we) of a chunk starting at
-// `begin` (wb - begin a multiple of 2 kAttnSlots tiles), in position order:
-// tiles t and t + kAttnSlots together (attn_tile2) while both exist, a last
-// single one alone (attn_tile).
+// attn_tile_ops with K and V read through k4(pos, d4) (float4 d4 of position
+// pos's K row) and v(pos, d) (element d of its V row).
 template <typename K4, typename V>
-__device__ __forceinline__ void attn_slot_tiles(const float4 (&qa)[4], K4 k4, V v, float *ps, int begin,
-                                                int wb, int we, int end, int slot, AttnAcc &acc) {
+__device__ __forceinline__ void attn_tile(const float4 (&q)[kHeadDim / 4], K4 k4, V v, float *ps, int t0, int end,
+                                          AttnAcc &acc) {
+  const int lane = lane_id(), hq = lane >> 5;
+  const int pk = min(t0 + (lane & 31), end - 1);
+  attn_tile_ops(
+      q, [&](int i) { return k4(pk, (kHeadDim / 8) * hq + i); }, [&](int k) { return v(min(t0 + k, end - 1), lane); },
+      ps, t0, end, acc);
+}
+
+// The tiles of slot `slot` that lie in [wb, we) of a chunk
+// starting at `begin` (wb - begin a multiple of kAttnTile), in position
+// order: tiles slot, slot + kAttnSlots, ... of the chunk.
+template <typename K4, typename V>
+__device__ __forceinline__ void attn_slot_tiles(const float4 (&q)[kHeadDim / 4], K4 k4, V v, float *ps,
+                                                     int begin, int wb, int we, int end, int slot,
+                                                     AttnAcc &acc) {
   const int t_lo = (wb - begin) / kAttnTile, t_hi = (we - begin + kAttnTile - 1) / kAttnTile;
-  for (int t = t_lo + slot; t < t_hi; t += 2 * kAttnSlots) {
-    if (t + kAttnSlots < t_hi)
-      attn_tile2(qa, k4, v, ps, begin + t * kAttnTile, begin + (t + kAttnSlots) * kAttnTile, end, acc);
-    else
-      attn_tile(qa, k4, v, ps, begin + t * kAttnTile, end, acc);
-  }
+  for (int t = t_lo + slot; t < t_hi; t += kAttnSlots)
+    attn_tile(q, k4, v, ps, begin + t * kAttnTile, end, acc);
 }
 
 // Wave partials of a chunk staged for the merge: [slot][row] maxima and
 // sums, [slot][row][64] outputs, for the group's first `heads` rows.
 struct AttnStage {
   float *m, *l, *o;  // m, l: kAttnSlots * kMaxGroup floats; o: kAttnSlots * kMaxGroup * 64
+  // Each row's sum is the half_sum of its lanes' shares.
   __device__ __forceinline__ void put(int slot, int heads, const AttnAcc &acc) const {
-    const int lane = lane_id(), col = lane & 15, quad = lane >> 4;
+    const int lane = lane_id(), hq = lane >> 5, mm = lane & 31;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 4 * quad + r;
+      const float lsum = half_sum(acc.l[r]);
+      const int row = 4 * hq + r;
       if (row < heads) {
-        if (col == 0) {
+        if (mm == 0) {
           m[slot * kMaxGroup + row] = acc.m[r];
-          l[slot * kMaxGroup + row] = acc.l[r];
+          l[slot * kMaxGroup + row] = lsum;
         }
-#pragma unroll
-        for (int n = 0; n < 4; ++n) o[(slot * kMaxGroup + row) * kHeadDim + 16 * n + col] = acc.o[n][r];
+        o[(slot * kMaxGroup + row) * kHeadDim + mm] = acc.o[0][r];
+        o[(slot * kMaxGroup + row) * kHeadDim + kHeadDim / 2 + mm] = acc.o[1][r];
       }
     }
   }

@@ -125,6 +125,32 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp<kDppMirror>(v);
 }
 
+// Max and sum over each half of the wave (32 lanes: rows 0-1 and rows 2-3),
+// the result in every lane of the half: row16_max / row16_sum, then the two
+// rows of a half exchanged by v_permlane16_swap_b32 on two copies of the
+// value (row 1 of the first <-> row 0 of the second, row 3 <-> row 2). The
+// swap is issued from inline assembly: the compiler's intrinsic for it
+// folds the second result into the first at -O3. The s_nop gives the two
+// wait states the swap needs after a VALU write of its operands.
+__device__ __forceinline__ void row_pair_swap(float v, float &a, float &b) {
+  unsigned x = __builtin_bit_cast(unsigned, v), y = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  a = __builtin_bit_cast(float, x);
+  b = __builtin_bit_cast(float, y);
+}
+__device__ __forceinline__ float row_pair_max(float v) {
+  float a, b;
+  row_pair_swap(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float row_pair_sum(float v) {
+  float a, b;
+  row_pair_swap(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float half_max(float v) { return row_pair_max(row16_max(v)); }
+__device__ __forceinline__ float half_sum(float v) { return row_pair_sum(row16_sum(v)); }
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<kDppXor1>(v));
   v = fmaxf(v, dpp<kDppXor2>(v));

@@ -137,7 +137,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
       float4 qv[kHeadDim / 4];
 #pragma unroll
       for (int d4 = 0; d4 < kHeadDim / 4; ++d4) qv[d4] = reinterpret_cast<const float4 *>(q + h * kHeadDim)[d4];
-      PLds pb{ps + w * kAttnPsFloats + 4, kAttnPsStride};
+      PLds pb{ps + w * kAttnPsFloats + 4, kWave};
       float mb[1], lb[1], ab[1];
       attn_block_valu<1>(
           [&](int d4, int j) { return reinterpret_cast<const float4 *>(kc + static_cast<size_t>(j) * kv_dim)[d4]; },
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     }
     return;
   }
-  float4 qa[4];
+  float4 qa[kHeadDim / 4];
   attn_query([&](int h, int d4) { return reinterpret_cast<const float4 *>(q + (g * group + h) * kHeadDim)[d4]; },
              group, qa);
   AttnAcc acc;
@@ -529,7 +529,7 @@ const char *kernel_name(int id) {
 bool shape_supported(int hidden, int intermediate, int heads, int kv_heads,
                      int head_dim) {
   return hidden == 896 && intermediate == 4864 && head_dim == kHeadDim &&
-         kv_heads > 0 && heads % kv_heads == 0 && heads / kv_heads <= kMaxGroup &&
+         kv_heads > 0 && heads % kv_heads == 0 && heads / kv_heads <= kAttnMaxGroup &&
          heads * head_dim == 896;
 }
 
@@ -576,7 +576,7 @@ hipError_t launch_layer_as(hipStream_t s, const LayerLaunch &p, Marker *m) {
   {
     Scope scope(m, kKAttnPartial);
     if (p.attn_parts < 1 || p.attn_parts > kAttnMaxChunks) return hipErrorInvalidValue;
-    if (p.nq / p.nkv > kMaxGroup) return hipErrorInvalidValue;
+    if (p.nq / p.nkv > kAttnMaxGroup) return hipErrorInvalidValue;
     attn_partial_kernel<<<dim3(p.attn_parts, p.nkv), kAttnThreads, 0, s>>>(
         p.q, p.k_cache, p.v_cache, p.st, p.nq, p.nkv, p.part, p.capacity, p.attn_parts);
   }

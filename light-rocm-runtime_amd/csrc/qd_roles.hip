@@ -789,7 +789,7 @@ struct AttnRegion {
   float ps[kW * kAttnPsFloats];
 };
 static_assert(sizeof(AttnRegion) <= kRegionBytes, "attention region");
-static_assert(kAttnSlots == kW && kAttnCap % (2 * kAttnSlots * kAttnTile) == 0, "tile pairs inside a window");
+static_assert(kAttnSlots == kW && kAttnCap % (kAttnSlots * kAttnTile) == 0, "a window holds whole rounds of tiles");
 static_assert(kAttnStageFloats * 4 <= sizeof(AttnRegion::kt), "wave partials staged over the K window");
 // V element d of window row j (rows of kHeadDim floats).
 __device__ __forceinline__ int attn_v_slot(int j, int d) { return j * kHeadDim + d; }
@@ -1294,17 +1294,36 @@ struct Roles {
   }
 
   __device__ void run_attn() {
+    static_assert(GROUP <= kAttnMaxGroup, "an attention tile takes up to 8 heads per KV group");
     AttnRegion &ar = *reinterpret_cast<AttnRegion *>(region);
     // The role's CUs come in KV-group blocks of group_cus[1]: CU rr of group
     // g takes the group's chunks rr, rr + group_cus[1], ...
     const int na = a.group_cus[1];
     const int g = rank / na, rr = rank % na;
+    // The second window of a CU's first chunk is loaded a layer ahead too,
+    // into registers: wave w's tile of it (tile kAttnSlots + w of the chunk),
+    // this lane's K half (kw2) and its V element of each position (vw2), the
+    // tile's arithmetic being attn_tile's (attn_tile_ops).
+    float4 kw2[kHeadDim / 8];
+    float vw2[kAttnTile];
     auto pre_lds = [&](int l, int position) {
       const int length = position + 1;
       const int chunks = attn_chunks(length, a.attn_parts, kAttnGrain), cl = attn_chunk_len(length, a.attn_parts, kAttnGrain);
       if (rr >= chunks || position >= a.capacity) return;
       const int begin = rr * cl, end = min(length, begin + cl);
       attn_dma(l, g, begin, min(end, begin + kAttnCap), ar);
+      const int t0 = begin + kAttnCap + wv * kAttnTile;
+      if (t0 < end) {
+        const Coherent kc(kv_layer(a.k_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
+        const Coherent vc(kv_layer(a.v_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
+        const int pk = min(t0 + (lane & 31), end - 1);
+        const uint32_t k4 = (static_cast<uint32_t>(pk) * KVD + g * kHeadDim + (kHeadDim / 2) * (lane >> 5)) / 4;
+#pragma unroll
+        for (int i = 0; i < kHeadDim / 8; ++i) kw2[i] = kc.ld4(k4 + i);
+#pragma unroll
+        for (int k = 0; k < kAttnTile; ++k)
+          vw2[k] = vc.ld(static_cast<uint32_t>(min(t0 + k, end - 1)) * KVD + g * kHeadDim + lane);
+      }
     };
     auto pre_regs = [](int) {};
     loop(kRoleAttn, false, [&](uint32_t t, int l, int position) {
@@ -1375,7 +1394,7 @@ struct Roles {
 #pragma unroll
             for (int d4 = 0; d4 < kHeadDim / 4; ++d4)
               q[d4] = reinterpret_cast<const float4 *>(ar.qs + wv * kHeadDim)[d4];
-            PLds pb{ps + 4, kAttnPsStride};
+            PLds pb{ps + 4, kWave};
             float bm[1], bl[1], ba[1];
             attn_block_valu<1>([&](int d4, int j) { return ar.kt[d4 * kAttnCap + j]; },
                                [&](int, int d4) { return q[d4]; },
@@ -1392,7 +1411,7 @@ struct Roles {
           first_unit = false;
           continue;
         }
-        float4 qa[4];
+        float4 qa[kHeadDim / 4];
         attn_query([&](int h, int d4) { return reinterpret_cast<const float4 *>(ar.qs + h * kHeadDim)[d4]; },
                    GROUP, qa);
         // Wave w's running partial over the chunk's tiles w, w + kW, ...,
@@ -1401,6 +1420,27 @@ struct Roles {
         acc.init();
         for (int wb = begin; wb < end; wb += kAttnCap) {
           const int we = min(end, wb + kAttnCap);
+          if (first_unit && wb == begin + kAttnCap) {
+            // The second window from registers (no LDS, no barrier). When
+            // the new position lies in this chunk it is the chunk's last
+            // (end - 1), where the tile's reads past the end are clamped
+            // too: those take the gathered row instead of the prefetched
+            // cache row, as the LDS windows do.
+            const int t0 = wb + wv * kAttnTile;
+            if (t0 < end) {
+              const int knew = has_new ? position - t0 : kAttnTile;
+              const int hq = lane >> 5;
+              const bool kfresh = (lane & 31) >= knew;
+              const float vfresh = ar.vn[lane];
+              attn_tile_ops(
+                  qa,
+                  [&](int i) {
+                    return kfresh ? reinterpret_cast<const float4 *>(ar.kn)[(kHeadDim / 8) * hq + i] : kw2[i];
+                  },
+                  [&](int k) { return k >= knew ? vfresh : vw2[k]; }, ps, t0, end, acc);
+            }
+            continue;
+          }
           if (wb != begin) {
             lds_barrier();
             attn_dma(l, g, wb, we, ar);
