@@ -458,14 +458,14 @@ struct qd_engine {
 
   // Kernels of the prompt path, for per-kernel event timing.
   enum PrefillKernel : int {
-    kPEmbed = 0, kPNorm, kPGemmQkv, kPRope, kPAttn, kPGemmO, kPGemmGateUp, kPGemmDown,
+    kPEmbed = 0, kPNorm, kPGemmQkv, kPAttn, kPGemmO, kPGemmGateUp, kPGemmDown,
     kPTail, kPrefillKernels
   };
   static const char *prefill_kernel_name(int id) {
     static const char *const names[kPrefillKernels] = {
-        "embed_rows_kernel",    "rmsnorm_rows_kernel",      "gemm_nt_kernel:qkv",
-        "rope_kv_rows_kernel",  "attention_prefill_kernel", "gemm_nt_kernel:o",
-        "gemm_nt_kernel:gateup+swiglu", "gemm_nt_kernel:down",
+        "embed_rows_kernel",    "rmsnorm_rows_kernel",      "gemm_nt_kernel:qkv+rope",
+        "attention_prefill_kernel", "gemm_nt_kernel:o+norm",
+        "gemm_nt_kernel:gateup+swiglu", "gemm_nt_kernel:down+norm",
         "lmhead_kernel+argmax"};
     return id >= 0 && id < kPrefillKernels ? names[id] : "unknown";
   }
@@ -478,14 +478,13 @@ struct qd_engine {
     switch (kernel) {
       case kPEmbed: return {2 * n * H * f, 0};
       case kPNorm: return {(2 * n * H + H) * f, 0};
-      case kPGemmQkv: return {(QKV * H + QKV + n * (H + QKV)) * f, 2 * n * QKV * H};
-      case kPRope: return {n * (2 * QD + 4 * KVD) * f, 0};
+      case kPGemmQkv: return {(QKV * H + QKV + n * (H + QKV + 2 * QD + 4 * KVD)) * f, 2 * n * QKV * H};
       case kPAttn:
         return {(2 * (pos0 + n) * KVD + 2 * n * QD) * f,
                 4 * NQ * qd::kHeadDim * (n * pos0 + n * (n + 1) / 2)};
-      case kPGemmO: return {(H * QD + n * (QD + 2 * H)) * f, 2 * n * H * QD};
+      case kPGemmO: return {(H * QD + H + n * (QD + 3 * H)) * f, 2 * n * H * QD};
       case kPGemmGateUp: return {(2 * I * H + n * (H + I)) * f, 4 * n * I * H};
-      case kPGemmDown: return {(H * I + n * (I + 2 * H)) * f, 2 * n * H * I};
+      case kPGemmDown: return {(H * I + H + n * (I + 3 * H)) * f, 2 * n * H * I};
       case kPTail: return {(V * H + H + V) * f, 2 * V * H};
     }
     return {0, 0};
@@ -518,30 +517,50 @@ struct qd_engine {
     for (size_t l = 0; l < L; ++l) {
       const qd::LayerPtrs &w = layers[l];
       float *kc = kv_slice(k_cache, seq, l), *vc = kv_slice(v_cache, seq, l);
-      span(kPNorm, "norm",
-           [&] { return qd::launch_rmsnorm_rows(stream, pf_h, w.attn_norm, cfg.rms_eps, n, pf_xn); });
-      span(kPGemmQkv, "qkv gemm", [&] {
+      // The attention norm of layer 0 runs on its own; every other norm and
+      // the RoPE run in the reduction of the split-K GEMM before them.
+      if (l == 0)
+        span(kPNorm, "norm",
+             [&] { return qd::launch_rmsnorm_rows(stream, pf_h, w.attn_norm, cfg.rms_eps, n, pf_xn); });
+      span(kPGemmQkv, "qkv gemm + rope", [&] {
+        qd::RowEpilogue rope;
+        rope.kind = qd::kRowRope;
+        rope.pos0 = pos0;
+        rope.nq = nq;
+        rope.nkv = nkv;
+        rope.rope_cos = rope_cos;
+        rope.rope_sin = rope_sin;
+        rope.k_cache = kc;
+        rope.v_cache = vc;
         return qd::launch_gemm_nt(stream, pf_xn, h, w.wqkv, h, pf_qkv, qkv, n, qkv, h, qd::kGemmBias,
-                                  w.bqkv, kSplitQkv, pf_split);
-      });
-      span(kPRope, "rope", [&] {
-        return qd::launch_rope_kv_rows(stream, pf_qkv, n, pos0, nq, nkv, rope_cos, rope_sin, kc, vc);
+                                  w.bqkv, kSplitQkv, pf_split, &rope);
       });
       span(kPAttn, "attention", [&] {
         return qd::launch_attention_prefill(stream, pf_qkv, n, pos0, nq, nkv, kc, vc, pf_attn);
       });
-      span(kPGemmO, "o gemm", [&] {
+      span(kPGemmO, "o gemm + norm", [&] {
+        qd::RowEpilogue norm;
+        norm.kind = qd::kRowNorm;
+        norm.gain = w.mlp_norm;
+        norm.eps = cfg.rms_eps;
+        norm.y = pf_xn;
         return qd::launch_gemm_nt(stream, pf_attn, qd, w.wo, qd, pf_h, h, n, h, qd,
-                                  qd::kGemmAccumulate, nullptr, kSplitO, pf_split);
+                                  qd::kGemmAccumulate, nullptr, kSplitO, pf_split, &norm);
       });
-      span(kPNorm, "norm",
-           [&] { return qd::launch_rmsnorm_rows(stream, pf_h, w.mlp_norm, cfg.rms_eps, n, pf_xn); });
       span(kPGemmGateUp, "gate/up gemm + swiglu", [&] {
         return qd::launch_gemm_swiglu(stream, pf_xn, h, w.wg, w.wu, h, pf_act, in, n, in, h);
       });
       span(kPGemmDown, "down gemm", [&] {
+        qd::RowEpilogue norm;
+        if (l + 1 < L) {
+          norm.kind = qd::kRowNorm;
+          norm.gain = layers[l + 1].attn_norm;
+          norm.eps = cfg.rms_eps;
+          norm.y = pf_xn;
+        }
         return qd::launch_gemm_nt(stream, pf_act, in, w.wd, in, pf_h, h, n, h, in,
-                                  qd::kGemmAccumulate, nullptr, kSplitDown, pf_split);
+                                  qd::kGemmAccumulate, nullptr, kSplitDown, pf_split,
+                                  l + 1 < L ? &norm : nullptr);
       });
     }
   }

@@ -217,35 +217,37 @@ __global__ __launch_bounds__(kBlock) void embed_rows_kernel(const float *__restr
   for (int c = threadIdx.x; c < hidden / 4; c += kBlock) dst[c] = src[c];
 }
 
-// RMSNorm of one prompt row: x * inv * gain with inv from block_inv_rms.
-// (The decode kernels fold the norm past their GEMVs instead, inv * (W .
-// (x * gain)); the two agree to rounding.)
+// RMSNorm of one prompt row: x * inv * gain with inv from block_inv_rms
+// (the whole workgroup). (The decode kernels fold the norm past their
+// GEMVs instead, inv * (W . (x * gain)); the two agree to rounding.)
 template <int H>
-__global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float *__restrict__ x,
-                                                              const float *__restrict__ gain,
-                                                              float eps, float *__restrict__ y) {
-  __shared__ float red[kWavesPerBlock];
-  const int r = blockIdx.x;
-  const float *xr = x + static_cast<size_t>(r) * H;
+__device__ __forceinline__ void rmsnorm_row(const float *xr, const float *__restrict__ gain, float eps, float *yr,
+                                            float *red) {
   const float inv = block_inv_rms<H>(Plain(xr), eps, red);
   const float4 *x4 = reinterpret_cast<const float4 *>(xr);
   const float4 *g4 = reinterpret_cast<const float4 *>(gain);
-  float4 *y4 = reinterpret_cast<float4 *>(y + static_cast<size_t>(r) * H);
+  float4 *y4 = reinterpret_cast<float4 *>(yr);
   for (int c = threadIdx.x; c < H / 4; c += kBlock) {
     const float4 v = x4[c], g = g4[c];
     y4[c] = make_float4(v.x * inv * g.x, v.y * inv * g.y, v.z * inv * g.z, v.w * inv * g.w);
   }
 }
 
-__global__ __launch_bounds__(kBlock) void rope_kv_rows_kernel(float *__restrict__ qkv, int pos0, int nq,
-                                                              int nkv, const float *__restrict__ rope_cos,
-                                                              const float *__restrict__ rope_sin,
-                                                              float *__restrict__ k_cache,
-                                                              float *__restrict__ v_cache) {
+template <int H>
+__global__ __launch_bounds__(kBlock) void rmsnorm_rows_kernel(const float *__restrict__ x,
+                                                              const float *__restrict__ gain,
+                                                              float eps, float *__restrict__ y) {
+  __shared__ float red[kWavesPerBlock];
   const int r = blockIdx.x;
-  const int p = pos0 + r;
+  rmsnorm_row<H>(x + static_cast<size_t>(r) * H, gain, eps, y + static_cast<size_t>(r) * H, red);
+}
+
+// RoPE of one packed QKV row at position p (query and key heads rotated in
+// place) and its K/V rows written to the cache (the whole workgroup).
+__device__ __forceinline__ void rope_kv_row(float *row, int p, int nq, int nkv, const float *__restrict__ rope_cos,
+                                            const float *__restrict__ rope_sin, float *__restrict__ k_cache,
+                                            float *__restrict__ v_cache) {
   const int qd = nq * kHeadDim, kvd = nkv * kHeadDim;
-  float *row = qkv + static_cast<size_t>(r) * (qd + 2 * kvd);
   const int rotations = (nq + nkv) * kRotary;
   for (int u = threadIdx.x; u < rotations + kvd; u += kBlock) {
     if (u < rotations) {
@@ -267,6 +269,43 @@ __global__ __launch_bounds__(kBlock) void rope_kv_rows_kernel(float *__restrict_
       v_cache[static_cast<size_t>(p) * kvd + o] = row[qd + kvd + o];
     }
   }
+}
+
+__global__ __launch_bounds__(kBlock) void rope_kv_rows_kernel(float *__restrict__ qkv, int pos0, int nq,
+                                                              int nkv, const float *__restrict__ rope_cos,
+                                                              const float *__restrict__ rope_sin,
+                                                              float *__restrict__ k_cache,
+                                                              float *__restrict__ v_cache) {
+  const int r = blockIdx.x;
+  rope_kv_row(qkv + static_cast<size_t>(r) * (nq + 2 * nkv) * kHeadDim, pos0 + r, nq, nkv, rope_cos, rope_sin,
+              k_cache, v_cache);
+}
+
+// gemm_reduce_kernel's sums and epilogue for one row per workgroup, then the
+// row epilogue on the finished row: RMSNorm into epi.y (kRowNorm) or RoPE
+// with the K/V cache rows (kRowRope), with the arithmetic of
+// rmsnorm_rows_kernel / rope_kv_rows_kernel, so the results are the same
+// bits as those kernels after gemm_reduce_kernel.
+__global__ __launch_bounds__(kBlock) void gemm_reduce_rows_kernel(const float *__restrict__ part, int split,
+                                                                  float *__restrict__ C, int ldc, int m, int n,
+                                                                  int mode, const float *__restrict__ bias,
+                                                                  RowEpilogue epi) {
+  __shared__ float red[kWavesPerBlock];
+  const int r = blockIdx.x;
+  float *row = C + static_cast<size_t>(r) * ldc;
+  for (int c = threadIdx.x; c < n; c += kBlock) {
+    float v = part[static_cast<size_t>(r) * ldc + c];
+    for (int z = 1; z < split; ++z) v += part[(static_cast<size_t>(z) * m + r) * ldc + c];
+    if (mode == kGemmAccumulate)
+      row[c] += v;
+    else
+      row[c] = mode == kGemmBias ? v + bias[c] : v;
+  }
+  __syncthreads();
+  if (epi.kind == kRowNorm)
+    rmsnorm_row<896>(row, epi.gain, epi.eps, epi.y + static_cast<size_t>(r) * n, red);
+  else if (epi.kind == kRowRope)
+    rope_kv_row(row, epi.pos0 + r, epi.nq, epi.nkv, epi.rope_cos, epi.rope_sin, epi.k_cache, epi.v_cache);
 }
 
 // ---- causal GQA flash attention ---------------------------------------------------
@@ -465,15 +504,21 @@ __global__ __launch_bounds__(kBlock) void attention_prefill_kernel(
 
 hipError_t launch_gemm_nt(hipStream_t s, const float *A, int lda, const float *W, int ldw,
                           float *C, int ldc, int m, int n, int k, GemmMode mode,
-                          const float *bias, int split, float *workspace) {
+                          const float *bias, int split, float *workspace, const RowEpilogue *epi) {
   if (k % kTileK != 0 || m <= 0 || n <= 0 || split < 1 || split > k / kTileK ||
       (split > 1 && !workspace))
+    return hipErrorInvalidValue;
+  // A row epilogue runs in the split-K reduction, one workgroup per row.
+  if (epi && (split < 2 || ldc != n || (epi->kind == kRowNorm && (n != 896 || !epi->y || !epi->gain)) ||
+              (epi->kind == kRowRope && n != (epi->nq + 2 * epi->nkv) * kHeadDim)))
     return hipErrorInvalidValue;
   if (mode == kGemmSwiGLU) return hipErrorInvalidValue;
   const dim3 grid((n + kTileN - 1) / kTileN, (m + kTileM - 1) / kTileM, split);
   gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, W, nullptr, ldw, split > 1 ? workspace : C, ldc, m, n, k,
                                          mode, bias);
-  if (split > 1) {
+  if (split > 1 && epi) {
+    gemm_reduce_rows_kernel<<<m, kBlock, 0, s>>>(workspace, split, C, ldc, m, n, mode, bias, *epi);
+  } else if (split > 1) {
     const size_t total = static_cast<size_t>(m) * n;
     const int blocks = static_cast<int>(std::min<size_t>((total + kBlock - 1) / kBlock, 4096));
     gemm_reduce_kernel<<<blocks, kBlock, 0, s>>>(workspace, split, C, ldc, m, n, mode, bias);

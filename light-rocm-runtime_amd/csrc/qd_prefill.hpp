@@ -15,13 +15,29 @@ namespace qd {
 // MLP's gate/up GEMM with SwiGLU fused (launch_gemm_swiglu).
 enum GemmMode : int { kGemmStore = 0, kGemmBias = 1, kGemmAccumulate = 2, kGemmSwiGLU = 3 };
 
+// Work on each finished row of a split-K GEMM, run by its reduction: the
+// RMSNorm of the row into y (rows of 896, gain, eps), or RoPE of a packed
+// QKV row at position pos0 + r with its K/V rows written to the cache.
+enum RowEpilogueKind : int { kRowNone = 0, kRowNorm = 1, kRowRope = 2 };
+struct RowEpilogue {
+  int kind = kRowNone;
+  const float *gain = nullptr;
+  float eps = 0.f;
+  float *y = nullptr;
+  int pos0 = 0, nq = 0, nkv = 0;
+  const float *rope_cos = nullptr, *rope_sin = nullptr;
+  float *k_cache = nullptr, *v_cache = nullptr;
+};
+
 // C[m][n] (row stride ldc) for A [m][k] (stride lda) and W [n][k] (stride
 // ldw), all FP32 row-major. m, n any size (edges masked); k a multiple of 32.
 // split > 1 divides k over that many workgroup slices whose partials go to
-// workspace (split * m * ldc floats) and are summed in a fixed order.
+// workspace (split * m * ldc floats) and are summed in a fixed order. epi
+// (split > 1, ldc == n) runs a row epilogue in that reduction.
 hipError_t launch_gemm_nt(hipStream_t s, const float *A, int lda, const float *W, int ldw,
                           float *C, int ldc, int m, int n, int k, GemmMode mode,
-                          const float *bias, int split = 1, float *workspace = nullptr);
+                          const float *bias, int split = 1, float *workspace = nullptr,
+                          const RowEpilogue *epi = nullptr);
 
 // out[r] = embed[tokens[r]] for r < rows (hidden floats each).
 hipError_t launch_embed_rows(hipStream_t s, const float *embed, const uint32_t *tokens, int rows,

@@ -430,8 +430,8 @@ def test_profile_prefill_matches_prefill(full):
         k1, v1 = eng.read_kv(1, layer, 0, 96)
         assert np.array_equal(k0, k1) and np.array_equal(v0, v1), layer
     h, i, qkv = FULL.hidden, FULL.intermediate, (FULL.heads + 2 * FULL.kv_heads) * FULL.head_dim
-    expect = {"gemm_nt_kernel:qkv": 2 * 96 * qkv * h, "gemm_nt_kernel:gateup+swiglu": 4 * 96 * i * h,
-              "gemm_nt_kernel:down": 2 * 96 * h * i}
+    expect = {"gemm_nt_kernel:qkv+rope": 2 * 96 * qkv * h, "gemm_nt_kernel:gateup+swiglu": 4 * 96 * i * h,
+              "gemm_nt_kernel:down+norm": 2 * 96 * h * i}
     for name, flops in expect.items():
         launches, avg_us, _, avg_flops = prof[name]
         assert launches == FULL.layers and avg_us > 0 and avg_flops == flops, name
