@@ -58,7 +58,7 @@ WEIGHT_BYTES = 1_976_131_072
 RESIDENT_TRAFFIC_PER_TOKEN = 2_006_118_720
 # The role-split kernel on a 64-token launch of the config-3 workload
 # (context 4065..4128; profiles/roles_kernel_config3.md).
-RESIDENT_TRAFFIC_PER_TOKEN_LONG = 2_093_356_640
+RESIDENT_TRAFFIC_PER_TOKEN_LONG = 2_114_254_998
 
 
 def step_bytes(length: int) -> int:
