@@ -217,7 +217,7 @@ def test_resident_and_stream_generation_agree(full, stream_full):
 
 
 def test_resident_across_chunk_length_changes_matches_stream(full, stream_full):
-    """Attention chunks are whole 16-position tiles split over the engine's
+    """Attention chunks are whole multiples of 16 positions split over the engine's
     attention parts (9 on a 256-CU MI355X): across context 1001..1170 the
     chunk length grows from 112 to 128 positions at 1009 and to 144 at 1153,
     and the chunk count drops from 9 to 8 at 1009 and regrows to 9 at 1025.
@@ -293,8 +293,8 @@ def test_resident_config2_context_512_matches_stream_and_oracle(full, stream_ful
 def test_resident_config3_context_4096_matches_stream_and_oracle(full, stream_full):
     """BASELINE config 3 as the bench runs it: the resident kernel at context
     4065..4096 (on a 256-CU MI355X, 464-position chunks, 9 per KV head, each
-    walked in two LDS windows, its 16-position tiles spread over the waves
-    on MFMA)."""
+    walked in two windows, the first in LDS and the second in the waves'
+    registers, its 32-position tiles spread over the waves on MFMA)."""
     long_context_generation(full, stream_full, 4064, 32, 4242, "config 3 resident 4065..4096")
 
 
