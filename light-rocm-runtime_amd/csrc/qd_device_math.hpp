@@ -1,5 +1,5 @@
 // Device helpers shared by the stream-ordered kernels (qd_kernels.hip) and
-// the resident megakernel (qd_resident.hip): wave64 reductions, the float4
+// the resident megakernel (qd_roles.hip): wave64 reductions, the float4
 // slot layout of the row-pair GEMV, and device-coherent buffer access.
 #pragma once
 
