@@ -13,10 +13,11 @@ Workloads (synthetic random-init weights):
            path; one step = one prefill of the 512 tokens. The 128 greedy
            decode steps that follow it in config 5 are reported beside it.
   bf16     config 2's model and context with BF16 decoder matrices and an FP32
-           tail, on the stream-ordered kernels, timed against the same kernels
-           on FP32 weights.
+           tail, on the resident kernel, timed against the FP32 default line's
+           engine (interleaved).
+  f16      the same with IEEE FP16 decoder matrices.
 
-  python bench.py [--workload decode|long|batch16|prefill|bf16] [--steps K]
+  python bench.py [--workload decode|long|batch16|prefill|bf16|f16] [--steps K]
                   [--warmup W] [--trials T] [--gpus 1] [--no-cpu]
 """
 import argparse
@@ -327,39 +328,32 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token):
     }
 
 
-# BF16 decoder matrices: the 24 layers' wqkv, wo, gate, up and down at 2 bytes
-# per element, their biases and norms, the FP32 tail (tied LM head, final norm)
-# as in WEIGHT_BYTES.
-BF16_WEIGHT_BYTES = (24 * (2 * (1152 * 896 + 896 * 896 + 3 * 4864 * 896) + 4 * (1152 + 2 * 896))
+# Half-width decoder matrices (BF16 or FP16): the 24 layers' wqkv, wo, gate,
+# up and down at 2 bytes per element, their biases and norms, the FP32 tail
+# (tied LM head, final norm) as in WEIGHT_BYTES.
+HALF_WEIGHT_BYTES = (24 * (2 * (1152 * 896 + 896 * 896 + 3 * 4864 * 896) + 4 * (1152 + 2 * 896))
                      + 544_538_624 + 3_584)
+HALF_NAMES = {"bf16": "BF16", "f16": "FP16"}
 
 
-def run_bf16(K, W, no_cpu, trials):
-    """Config 2's decode with BF16 decoder weights and an FP32 tail (the
-    reference's reduced-precision mode, examples/qwen/README.md:291-300), on the
-    stream-ordered kernels, interleaved with the same path on FP32 weights."""
+def run_half(dtype, K, W, no_cpu, trials):
+    """Config 2's decode with BF16 or FP16 decoder weights and an FP32 tail
+    (the reference's reduced-precision modes, examples/qwen/README.md:291-300),
+    on the resident kernel, interleaved with the FP32 default line's engine."""
+    label = HALF_NAMES[dtype]
     capacity = PROMPT + max(K, W) + 24
-    log("engines: BF16 decoder weights, and FP32 on the stream kernels (QD_RESIDENT=0)")
-    e16 = qd.Engine(capacity=capacity, max_batch=1, decoder_dtype="bf16")
-    saved = os.environ.get("QD_RESIDENT")
-    os.environ["QD_RESIDENT"] = "0"
-    try:
-        e32 = qd.Engine(capacity=capacity, max_batch=1)
-    finally:
-        if saved is None:
-            del os.environ["QD_RESIDENT"]
-        else:
-            os.environ["QD_RESIDENT"] = saved
+    log(f"engines: {label} decoder weights and FP32, both on the resident kernel")
+    engines = {dtype: qd.Engine(capacity=capacity, max_batch=1, decoder_dtype=dtype),
+               "f32": qd.Engine(capacity=capacity, max_batch=1)}
     prompt = stream_tokens(PROMPT, SEED, PROMPT_STREAM, VOCAB)
     firsts = {}
-    for name, eng in (("bf16", e16), ("f32", e32)):
+    for name, eng in engines.items():
         eng.load_synthetic(SEED)
         log(f"{name}: prefill {PROMPT}")
         firsts[name], _, _ = eng.prefill(0, prompt, want_logits=False)
         if W:
             eng.generate(0, firsts[name], W)
-    engines = {"bf16": e16, "f32": e32}
-    samples = {name: [] for name in engines}
+    samples = {name: {"wall_ms": [], "device_us": []} for name in engines}
     log(f"timed: {trials} interleaved trials x {K} tokens per engine")
     for t in range(trials):
         for name in trial_orders(list(engines))[t % 4]:
@@ -369,44 +363,51 @@ def run_bf16(K, W, no_cpu, trials):
             t0 = time.perf_counter()
             toks, _, _ = eng.generate(0, firsts[name], K)
             eng.sync()
-            samples[name].append((time.perf_counter() - t0) * 1e3)
+            samples[name]["wall_ms"].append((time.perf_counter() - t0) * 1e3)
+            samples[name]["device_us"].append(eng.last_timing().total_us)
             assert len(toks) == K
-    w16, w32 = spread(samples["bf16"]), spread(samples["f32"])
-    e16.kv_reset(0, PROMPT)
-    prof = e16.profile_kernels(0, firsts["bf16"], min(K, 16))
-    log("bf16 step-path kernel profile: " + ", ".join(f"{n}={v[1]:.1f}us" for n, v in prof.items()))
-    name, (_, avg_us, avg_bytes, _) = dominant(prof)
-    e16.close()
-    e32.close()
-    per_token = [BF16_WEIGHT_BYTES + 24_576 * (PROMPT + 1 + i) + 24_576 + 607_744 + 3_584 for i in range(K)]
+    grid = engines[dtype].resident_grid()
+    wh, w32 = spread(samples[dtype]["wall_ms"]), spread(samples["f32"]["wall_ms"])
+    dev = spread(samples[dtype]["device_us"])
+    for eng in engines.values():
+        eng.close()
+    per_token = [HALF_WEIGHT_BYTES + 24_576 * (PROMPT + 1 + i) + 24_576 + 607_744 + 3_584 for i in range(K)]
     total = float(sum(per_token))
+    roof = roofline_hbm("roles_kernel", dev["median"], total)
     return {
-        "metric": "decode tokens/s at batch 1 (Qwen2.5-0.5B shape, BF16 decoder weights + FP32 tail) "
+        "metric": f"decode tokens/s at batch 1 (Qwen2.5-0.5B shape, {label} decoder weights + FP32 tail) "
                   "+ % HBM roofline",
-        "value": round(K / (w16["median"] * 1e-3), 2),
+        "value": round(K / (wh["median"] * 1e-3), 2),
         "unit": "tokens/s",
-        "ms_per_step": round(w16["median"] / K, 4),
+        "ms_per_step": round(wh["median"] / K, 4),
         "higher_is_better": True,
         "dtype": "f32",
-        "data": "synthetic: random-init N(0,0.02) weights rounded to BF16 for the decoder matrices, "
+        "data": f"synthetic: random-init N(0,0.02) weights rounded to {label} for the decoder matrices, "
                 f"N(0,0.01) biases, seed 1; {PROMPT} uniform random prompt tokens",
         "config": {
-            "workload": "BASELINE config 2's model and context with BF16 decoder matrices (FP32 "
-                        "compute, FP32 biases, norms, embeddings and LM head), stream-ordered kernels",
+            "workload": f"BASELINE config 2's model and context with {label} decoder matrices (FP32 "
+                        "compute, FP32 biases, norms, embeddings and LM head), resident kernel",
             "batch": 1, "context": f"{PROMPT + 1}..{PROMPT + K}", "layers": 24, "hidden": 896,
-            "vocab": VOCAB, "decoder_weights": "bf16",
+            "vocab": VOCAB, "decoder_weights": dtype,
         },
         "trials": {"count": trials, "order": "interleaved rotations, forwards then backwards",
-                   "bf16_ms": {k: round(v, 3) for k, v in w16.items()},
-                   "f32_stream_ms": {k: round(v, 3) for k, v in w32.items()}},
-        "step_hbm": {"achieved_gbs": round(total / (w16["median"] * 1e-3) / 1e9, 1),
+                   f"{dtype}_ms": {k: round(v, 3) for k, v in wh.items()},
+                   "f32_ms": {k: round(v, 3) for k, v in w32.items()}},
+        "step_hbm": {"achieved_gbs": round(total / (wh["median"] * 1e-3) / 1e9, 1),
                      "peak_gbs": HBM_PEAK_GBS, "bytes_per_token": round(total / K)},
-        "f32_stream_tokens_per_s": round(K / (w32["median"] * 1e-3), 2),
-        "roofline": roofline_hbm(name, avg_us, avg_bytes),
-        "kernels_us": {n: round(v[1], 2) for n, v in prof.items()},
+        "f32_tokens_per_s": round(K / (w32["median"] * 1e-3), 2),
+        "roofline": roof,
         "cpu_baseline": None,
-        "path": "stream-ordered kernels (BF16 decoder matrices)",
+        "path": f"resident megakernel, {grid} workgroups ({label} decoder matrices)",
     }
+
+
+def run_bf16(K, W, no_cpu, trials):
+    return run_half("bf16", K, W, no_cpu, trials)
+
+
+def run_f16(K, W, no_cpu, trials):
+    return run_half("f16", K, W, no_cpu, trials)
 
 
 def batch_lengths():
@@ -578,7 +579,8 @@ def copy_probe(mib: int):
     log(f"copy probe: 3 x {mib} MiB device-to-device")
 
 
-DEFAULTS = {"decode": (64, 8), "long": (32, 4), "batch16": (32, 4), "prefill": (20, 3), "bf16": (64, 8)}
+DEFAULTS = {"decode": (64, 8), "long": (32, 4), "batch16": (32, 4), "prefill": (20, 3), "bf16": (64, 8),
+            "f16": (64, 8)}
 
 
 def main():
@@ -602,7 +604,7 @@ def main():
     if K <= 0:
         sys.exit("--steps must be positive")
     run = {"decode": run_decode, "long": run_long, "batch16": run_batch16,
-           "prefill": run_prefill, "bf16": run_bf16}[args.workload]
+           "prefill": run_prefill, "bf16": run_bf16, "f16": run_f16}[args.workload]
     out = run(K, W, args.no_cpu, max(1, args.trials))
     if args.copy_probe:
         copy_probe(args.copy_probe)

@@ -68,18 +68,22 @@ typedef struct qd_config {
   float rope_theta;      /* 1e6 */
   int32_t device;        /* HIP device ordinal */
   uint32_t decoder_dtype; /* qd_dtype of the decoder layers' matrices (wqkv, wo,
-                           * gate, up, down): QD_DTYPE_F32 (0) or QD_DTYPE_BF16,
-                           * with biases, norms, embeddings and the LM head kept in
-                           * FP32 (the reference's BF16-decoder + FP32-tail mode,
-                           * examples/qwen/README.md:291-300). A BF16 engine runs
-                           * the stream-ordered kernels, reading each matrix at
-                           * half the bytes and computing in FP32; it has no
-                           * resident kernel or batched step (QD_ERROR_NOT_SUPPORTED),
+                           * gate, up, down): QD_DTYPE_F32 (0), QD_DTYPE_BF16 or
+                           * QD_DTYPE_F16, with biases, norms, embeddings and the
+                           * LM head kept in FP32 (the reference's FP16- and
+                           * BF16-decoder + FP32-tail modes,
+                           * examples/qwen/README.md:291-300). The matrices are
+                           * rounded to nearest even when loaded; every kernel
+                           * reads them at half the bytes, widens each value
+                           * exactly and computes in FP32 in the FP32 order, so
+                           * such an engine equals an FP32 engine loaded with the
+                           * rounded weights bit for bit. It runs the resident
+                           * kernel; it has no batched step (QD_ERROR_NOT_SUPPORTED),
                            * and its prefill runs the prompt position by position. */
 } qd_config;
 
 /* Storage types of qd_config.decoder_dtype. */
-typedef enum qd_dtype { QD_DTYPE_F32 = 0, QD_DTYPE_BF16 = 1 } qd_dtype;
+typedef enum qd_dtype { QD_DTYPE_F32 = 0, QD_DTYPE_BF16 = 1, QD_DTYPE_F16 = 2 } qd_dtype;
 
 /* Distributions for qd_load_synthetic (0.02, 0.01, 1.0). */
 typedef struct qd_synthetic_init {

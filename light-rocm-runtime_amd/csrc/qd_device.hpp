@@ -39,6 +39,9 @@ __host__ __device__ inline int attn_chunks(int length, int parts = kAttnMaxChunk
 
 enum Mode : uint32_t { kModeStep = 0, kModeGenerate = 1 };
 
+// Storage of the decoder layers' matrices (the values of qd_dtype).
+enum WeightStorage : int { kWeightsF32 = 0, kWeightsBf16 = 1, kWeightsF16 = 2 };
+
 // Device-resident state of one sequence slot. The step kernels read
 // `position` and `token`; the argmax finaliser writes the sampled token and
 // advances the position (the reference's embedding_feedback,

@@ -273,6 +273,24 @@ __device__ __forceinline__ float4 ld_weight(const Bf16x4 *p) {
   return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
                      __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
 }
+// FP16 weights: four consecutive IEEE half values, 8 bytes, widened exactly
+// to FP32 (every half is an FP32 value).
+struct F16 {
+  uint16_t bits;
+};
+struct alignas(8) F16x4 {
+  uint32_t lo, hi;  // elements (0, 1) and (2, 3), low half first
+};
+__device__ __forceinline__ float half_lo(uint32_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v & 0xFFFFu)));
+}
+__device__ __forceinline__ float half_hi(uint32_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v >> 16)));
+}
+__device__ __forceinline__ float4 ld_weight(const F16x4 *p) {
+  const gu32x2 v = __builtin_nontemporal_load((global_u32x2 *)p);
+  return make_float4(half_lo(v.x), half_hi(v.x), half_lo(v.y), half_hi(v.y));
+}
 // The four-element slot type of a weight row of W.
 template <typename W>
 struct WSlot;
@@ -284,6 +302,54 @@ template <>
 struct WSlot<Bf16> {
   using type = Bf16x4;
 };
+template <>
+struct WSlot<F16> {
+  using type = F16x4;
+};
+
+// A weight slot as the resident kernel keeps it in registers and LDS: the
+// stored bits (16 bytes of FP32, 8 bytes of BF16 or FP16), widened to the
+// FP32 float4 only where it is multiplied.
+template <typename W>
+struct WReg;
+template <>
+struct WReg<float> {
+  using type = float4;
+  __device__ static float4 widen(float4 r) { return r; }
+  __device__ static float4 zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+};
+template <>
+struct WReg<Bf16> {
+  using type = uint2;
+  __device__ static float4 widen(uint2 r) {
+    return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xFFFF0000u),
+                       __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xFFFF0000u));
+  }
+  __device__ static uint2 zero() { return make_uint2(0u, 0u); }
+};
+template <>
+struct WReg<F16> {
+  using type = uint2;
+  __device__ static float4 widen(uint2 r) {
+    return make_float4(half_lo(r.x), half_hi(r.x), half_lo(r.y), half_hi(r.y));
+  }
+  __device__ static uint2 zero() { return make_uint2(0u, 0u); }
+};
+// Pins v in registers at this point: the compiler may not move the
+// computation that produced it (a widening) into the instructions that use
+// it later (where it would become mixed-precision FMAs on the critical path).
+__device__ __forceinline__ float4 pin(float4 v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+  return v;
+}
+// Non-temporal load of one stored slot (no widening).
+__device__ __forceinline__ float4 ld_slot(const float4 *p) { return ld_weight(p); }
+template <typename S>
+__device__ __forceinline__ uint2 ld_slot(const S *p) {
+  static_assert(sizeof(S) == 8, "a 16-bit slot is 8 bytes");
+  const gu32x2 v = __builtin_nontemporal_load((global_u32x2 *)p);
+  return make_uint2(v.x, v.y);
+}
 
 // ---- RMSNorm ------------------------------------------------------------------
 

@@ -112,6 +112,16 @@ float from_bf16(uint16_t h) {
   return f;
 }
 
+// FP32 -> IEEE FP16, rounded to nearest even (values beyond the largest
+// half round to infinity); a NaN becomes the canonical quiet NaN 0x7E00,
+// which widens to 0x7FC00000.
+uint16_t to_f16(float f) {
+  if (f != f) return 0x7E00u;
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+float from_f16(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+
 }  // namespace
 
 struct qd_engine {
@@ -215,24 +225,30 @@ struct qd_engine {
           "hipMemcpyAsync H2D");
   }
 
-  // The decoder matrices (wqkv, wo, wg, wu, wd) hold BF16 on an engine
-  // created with QD_DTYPE_BF16 decoder weights, else FP32. LayerPtrs keeps
-  // their addresses as float pointers either way; element offsets into them
-  // go through mat_at.
-  bool bf16 = false;
-  size_t mat_elem() const { return bf16 ? 2 : 4; }
+  // The decoder matrices (wqkv, wo, wg, wu, wd) hold BF16 or FP16 on an
+  // engine created with QD_DTYPE_BF16 / QD_DTYPE_F16 decoder weights, else
+  // FP32. LayerPtrs keeps their addresses as float pointers either way;
+  // element offsets into them go through mat_at.
+  int wdtype = qd::kWeightsF32;
+  bool narrow() const { return wdtype != qd::kWeightsF32; }
+  size_t mat_elem() const { return narrow() ? 2 : 4; }
+  uint16_t to_narrow(float f) const { return wdtype == qd::kWeightsF16 ? to_f16(f) : to_bf16(f); }
+  float from_narrow(uint16_t h) const { return wdtype == qd::kWeightsF16 ? from_f16(h) : from_bf16(h); }
+  const char *dtype_name() const {
+    return wdtype == qd::kWeightsF16 ? "FP16" : wdtype == qd::kWeightsBf16 ? "BF16" : "FP32";
+  }
   char *mat_at(const float *base, size_t off) const {
     return reinterpret_cast<char *>(const_cast<float *>(base)) + off * mat_elem();
   }
   // n FP32 values into a decoder matrix from element `off` (rounded to BF16
-  // on a BF16 engine; that copy completes before the call returns).
+  // or FP16 on such an engine; that copy completes before the call returns).
   void upload_mat(const float *base, size_t off, const float *src, size_t n) {
-    if (!bf16) {
+    if (!narrow()) {
       upload(reinterpret_cast<float *>(mat_at(base, off)), src, n);
       return;
     }
     std::vector<uint16_t> h(n);
-    for (size_t i = 0; i < n; ++i) h[i] = to_bf16(src[i]);
+    for (size_t i = 0; i < n; ++i) h[i] = to_narrow(src[i]);
     check(hipMemcpyAsync(mat_at(base, off), h.data(), n * 2, hipMemcpyHostToDevice, stream), "H2D");
     check(hipStreamSynchronize(stream), "hipStreamSynchronize");
   }
@@ -291,7 +307,7 @@ struct qd_engine {
     a.v_cache = kv_slice(v_cache, seq, layer);
     a.part = part;
     a.attn_parts = attn_parts;
-    a.weights_bf16 = bf16 ? 1 : 0;
+    a.weights_dtype = wdtype;
     a.capacity = static_cast<int>(CAP);
     a.nq = static_cast<int>(NQ);
     a.nkv = static_cast<int>(NKV);
@@ -619,6 +635,7 @@ struct qd_engine {
     for (int r = 0; r < 3; ++r) ra.group_cus[r] = plan.group_cus[r];
     ra.xcd_place = plan.xcd_place;
     ra.attn_parts = attn_parts;
+    ra.weights_dtype = wdtype;
     check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
     // Every hand-off slot starts empty (all bits set).
     check(hipMemsetAsync(roles_slots, 0xFF, roles_slot_bytes, stream), "memset");
@@ -761,9 +778,10 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
       fail(QD_ERROR_INVALID_ARGUMENT, "heads %u not a multiple of kv_heads %u", c.heads, c.kv_heads);
     if (!(c.rms_eps > 0.0f) || !(c.rope_theta > 0.0f))
       fail(QD_ERROR_INVALID_ARGUMENT, "rms_eps and rope_theta must be positive");
-    if (c.decoder_dtype != QD_DTYPE_F32 && c.decoder_dtype != QD_DTYPE_BF16)
-      fail(QD_ERROR_INVALID_ARGUMENT, "decoder_dtype %u is neither QD_DTYPE_F32 nor QD_DTYPE_BF16",
-           c.decoder_dtype);
+    if (c.decoder_dtype != QD_DTYPE_F32 && c.decoder_dtype != QD_DTYPE_BF16 &&
+        c.decoder_dtype != QD_DTYPE_F16)
+      fail(QD_ERROR_INVALID_ARGUMENT,
+           "decoder_dtype %u is none of QD_DTYPE_F32, QD_DTYPE_BF16 and QD_DTYPE_F16", c.decoder_dtype);
     if (!qd::shape_supported(static_cast<int>(c.hidden), static_cast<int>(c.intermediate),
                              static_cast<int>(c.heads), static_cast<int>(c.kv_heads),
                              static_cast<int>(c.head_dim)))
@@ -789,7 +807,9 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     e->L = c.layers;
     e->CAP = c.capacity;
     e->B = c.max_batch;
-    e->bf16 = c.decoder_dtype == QD_DTYPE_BF16;
+    e->wdtype = c.decoder_dtype == QD_DTYPE_BF16 ? qd::kWeightsBf16
+                : c.decoder_dtype == QD_DTYPE_F16  ? qd::kWeightsF16
+                                                   : qd::kWeightsF32;
     e->set_device();
     check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
     check(hipEventCreate(&e->ev_begin), "hipEventCreate");
@@ -866,11 +886,9 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     }
     const char *env = std::getenv("QD_RESIDENT");
     qd::RolePlan plan{};
-    if (e->bf16) {
-      e->resident_off_reason = "BF16 decoder weights run on the stream-ordered kernels";
-    } else if (env && std::strcmp(env, "0") == 0) {
+    if (env && std::strcmp(env, "0") == 0) {
       e->resident_off_reason = "QD_RESIDENT=0";
-    } else if (cus < 64 || cus > qd::kMaxRoleGrid || qd::roles_max_grid(c.device) < cus) {
+    } else if (cus < 64 || cus > qd::kMaxRoleGrid || qd::roles_max_grid(c.device, e->wdtype) < cus) {
       e->resident_off_reason = "device cannot co-schedule one role workgroup per CU";
     } else if (!qd::plan_roles(cus, int(e->H), int(e->I), int(e->NQ), int(e->NKV), 1, &plan)) {
       e->resident_off_reason = "no role plan for this model shape";
@@ -969,11 +987,11 @@ qd_status qd_load_synthetic(qd_engine *e, uint64_t seed, const qd_synthetic_init
           slot ^= 1;
         }
       };
-      // A decoder matrix from element `first`: FP32, or rounded to BF16 in
-      // the staging buffer itself (element i's two bytes land at or below
-      // where its float was read) on a BF16 engine.
+      // A decoder matrix from element `first`: FP32, or rounded to BF16 or
+      // FP16 in the staging buffer itself (element i's two bytes land at or
+      // below where its float was read) on such an engine.
       auto emit_mat = [&](const float *base, size_t first, size_t n, uint64_t stream_id, float stddev) {
-        if (!e->bf16) {
+        if (!e->narrow()) {
           emit(reinterpret_cast<float *>(e->mat_at(base, first)), n, stream_id, stddev, false);
           return;
         }
@@ -982,7 +1000,7 @@ qd_status qd_load_synthetic(qd_engine *e, uint64_t seed, const qd_synthetic_init
           if (pending[slot]) check(hipEventSynchronize(done[slot]), "stage sync");
           fill_normal(stage[slot], m, off, seed, stream_id, stddev);
           uint16_t *h = reinterpret_cast<uint16_t *>(stage[slot]);
-          for (size_t i = 0; i < m; ++i) h[i] = to_bf16(stage[slot][i]);
+          for (size_t i = 0; i < m; ++i) h[i] = e->to_narrow(stage[slot][i]);
           check(hipMemcpyAsync(e->mat_at(base, first + off), h, m * 2, hipMemcpyHostToDevice, e->stream),
                 "H2D");
           check(hipEventRecord(done[slot], e->stream), "hipEventRecord");
@@ -1074,9 +1092,10 @@ qd_status qd_load_bundle(qd_engine *e, const char *directory) {
     e->upload(e->final_norm, t.final_norm_weight.data(), e->H);
     if (e->lm_head != e->embed) e->upload(e->lm_head, t.lm_head_weight.data(), e->V * e->H);
     // No loaded NaN keeps its payload (see launch_canonical_nan).
-    // (BF16 matrices were canonicalised by their rounding; their bytes are
-    // not FP32 words, so only the FP32 tensors of such an engine are swept.)
-    if (!e->bf16) {
+    // (BF16 and FP16 matrices were canonicalised by their rounding; their
+    // bytes are not FP32 words, so only the FP32 tensors of such an engine
+    // are swept.)
+    if (!e->narrow()) {
       check(qd::launch_canonical_nan(e->stream, e->weights, e->weights_floats), "canonical NaN");
     } else {
       for (const qd::LayerPtrs &p : e->layers) {
@@ -1128,12 +1147,12 @@ qd_status qd_read_weight(qd_engine *e, uint32_t layer, uint32_t kind, float *out
     }
     if (!src) fail(QD_ERROR_INVALID_ARGUMENT, "unknown tensor layer %u kind %u", layer, kind);
     if (count != n) fail(QD_ERROR_INVALID_ARGUMENT, "tensor has %zu elements, caller asked %zu", n, count);
-    if (mat && e->bf16) {
+    if (mat && e->narrow()) {
       // Widened to FP32 exactly, as the kernels read them.
       std::vector<uint16_t> h(n);
       check(hipMemcpyAsync(h.data(), src, n * 2, hipMemcpyDeviceToHost, e->stream), "D2H");
       e->sync();
-      for (size_t i = 0; i < n; ++i) out[i] = from_bf16(h[i]);
+      for (size_t i = 0; i < n; ++i) out[i] = e->from_narrow(h[i]);
       return;
     }
     check(hipMemcpyAsync(out, src, n * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
@@ -1431,8 +1450,8 @@ void check_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t 
 // on the last position, which advances the slot to pos0 + n. m (nullable)
 // times every launch.
 void run_prefill(qd_engine *e, uint32_t seq, const uint32_t *tokens, uint32_t n, EventMarker *m) {
-  if (e->bf16) {
-    // BF16 decoder weights: the prompt runs position by position through the
+  if (e->narrow()) {
+    // BF16 or FP16 decoder weights: the prompt runs position by position through the
     // stream-ordered step kernels (the prompt GEMMs read FP32 matrices),
     // writing every position's K/V row; then the tail on the last position.
     for (uint32_t i = 0; i < n; ++i) {
@@ -1477,7 +1496,7 @@ void check_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, const ui
                  uint32_t steps) {
   if (!e || !seq_ids || !tokens) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
   e->check_loaded();
-  if (e->bf16) fail(QD_ERROR_NOT_SUPPORTED, "batched decode needs FP32 decoder weights");
+  if (e->narrow()) fail(QD_ERROR_NOT_SUPPORTED, "batched decode needs FP32 decoder weights");
   if (n_seq == 0 || n_seq > e->B) fail(QD_ERROR_INVALID_ARGUMENT, "n_seq %u out of range", n_seq);
   std::vector<bool> seen(e->B, false);
   for (uint32_t i = 0; i < n_seq; ++i) {
@@ -1553,7 +1572,7 @@ qd_status qd_step_batch_noalloc(qd_engine *e, uint32_t n_seq, const uint32_t *se
   return guard([&] {
     if (!e || !seq_ids || !tokens) fail(QD_ERROR_INVALID_ARGUMENT, "null argument");
     e->check_loaded();
-    if (e->bf16) fail(QD_ERROR_NOT_SUPPORTED, "batched decode needs FP32 decoder weights");
+    if (e->narrow()) fail(QD_ERROR_NOT_SUPPORTED, "batched decode needs FP32 decoder weights");
     if (n_seq == 0 || n_seq > uint32_t(qd::kBatchRows))
       fail(QD_ERROR_INVALID_ARGUMENT,
            "qd_step_batch_noalloc takes 1..%d sequences (its static workspace holds one group), got %u",

@@ -556,7 +556,7 @@ hipError_t launch_embed(hipStream_t s, const float *emb, const SeqState *st,
 
 namespace {
 
-// One layer's launches with the decoder matrices read as W (float or Bf16).
+// One layer's launches with the decoder matrices read as W (float, Bf16 or F16).
 template <typename W>
 hipError_t launch_layer_as(hipStream_t s, const LayerLaunch &p, Marker *m) {
   const W *wqkv = reinterpret_cast<const W *>(p.w.wqkv);
@@ -613,7 +613,12 @@ hipError_t launch_layer_as(hipStream_t s, const LayerLaunch &p, Marker *m) {
 }  // namespace
 
 hipError_t launch_layer(hipStream_t s, const LayerLaunch &p, Marker *m) {
-  return p.weights_bf16 ? launch_layer_as<Bf16>(s, p, m) : launch_layer_as<float>(s, p, m);
+  switch (p.weights_dtype) {
+    case kWeightsF32: return launch_layer_as<float>(s, p, m);
+    case kWeightsBf16: return launch_layer_as<Bf16>(s, p, m);
+    case kWeightsF16: return launch_layer_as<F16>(s, p, m);
+  }
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_tail(hipStream_t s, const TailLaunch &p, Marker *m) {

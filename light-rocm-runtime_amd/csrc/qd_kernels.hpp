@@ -24,7 +24,7 @@ struct LayerLaunch {
   float *part;     // split-KV partials [16][heads][66]
   int capacity;  // KV positions of the slot; kernels skip positions beyond
   int attn_parts;  // chunk geometry: attn_chunks(length, attn_parts, kAttnGrain)
-  int weights_bf16;  // nonzero: w's decoder matrices (wqkv, wo, wg, wu, wd) hold BF16
+  int weights_dtype;  // storage of w's decoder matrices (wqkv, wo, wg, wu, wd): kWeights*
   int nq;
   int nkv;
   float eps;

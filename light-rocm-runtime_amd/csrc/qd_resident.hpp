@@ -80,6 +80,7 @@ struct ResidentArgs {
   int group_cus[3];             // RolePlan::group_cus
   int attn_parts;               // chunk geometry: attn_chunks(length, attn_parts, kAttnGrain)
   int xcd_place;                // RolePlan::xcd_place
+  int weights_dtype;            // kWeights*: storage of the layers' matrices (picks the instance)
 };
 
 // Argmax partial tags: epoch << kTagSeqBits | (token * (5 * layers + 1) + stage + 1).
@@ -112,7 +113,8 @@ int device_cu_count(int device);
 bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int max_length,
                 RolePlan *plan);
 hipError_t launch_roles(hipStream_t s, const ResidentArgs &args, int grid);
-// Largest co-resident grid of the role kernel on `device` (0 if the query fails).
-int roles_max_grid(int device);
+// Largest co-resident grid of the role kernel for decoder matrices stored as
+// `weights_dtype` (kWeights*) on `device` (0 if the query fails).
+int roles_max_grid(int device, int weights_dtype);
 
 }  // namespace qd

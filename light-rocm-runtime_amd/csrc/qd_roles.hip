@@ -523,49 +523,120 @@ struct Clock {
 // k < kW*S sit in register slot k / kW of their wave; the next Lcap units in
 // LDS (unit k - kW*S, in slot-layout order); any further unit is loaded from
 // global memory when computed (only if the plan over-fills a CU).
-template <int H, int S, int Lcap>
+//
+// Registers and LDS always hold FP32, so the arithmetic of a layer is the
+// same code whatever the stored type W. FP32 weights are loaded as they
+// are (LDS by DMA). BF16 / FP16 weights are widened while prefetching: the
+// register units' slots arrive raw and are widened by settle(), which a
+// role calls before it waits for its input; the LDS units pass through a
+// wave's registers (load, widen, LDS store), so their HBM bytes are halved
+// and nothing is widened inside a layer's dot products.
+template <int H, int S, int LdsUnits, typename W>
 struct PairRole {
+  // Units held in LDS: what the region holds, at most what the eight unit
+  // sums of a wave (compute) can carry.
+  static constexpr int Lcap = LdsUnits < (8 - S) * kW ? LdsUnits : (8 - S) * kW;
+  using WT = WReg<W>;
+  using R = typename WT::type;
+  using Slot = typename WSlot<W>::type;
+  static constexpr bool kNarrow = sizeof(R) == 8;
   static constexpr int NJ = PairSlots<H>::NJ;
   static constexpr int K4 = PairSlots<H>::K4;
-  static constexpr int UnitF4 = NJ * kWave;
+  static constexpr int UnitBytes = NJ * 1024;  // FP32 slots, slot-layout order
   float4 wv[S][NJ];
-  float4 *units = nullptr;
+  R raw[kNarrow ? S : 1][NJ];  // narrow register units as loaded, until settle()
+  unsigned char *units = nullptr;
   int n = 0;
+
+  // Slot c of a row pair's run of 2 K4 slots (zero past it).
+  __device__ static R load_slot(const Slot *a4, const Slot *b4, int c, int lane) {
+    const int f = c * kWave + lane;
+    if (c * kWave + kWave <= K4) return ld_slot(a4 + f);
+    if (c * kWave >= K4) return f < 2 * K4 ? ld_slot(b4 + (f - K4)) : WT::zero();
+    return ld_slot(f < K4 ? a4 + f : b4 + (f - K4));
+  }
 
   template <typename Rows>
   __device__ void prefetch_regs(Rows rows) {
-    const int w = wave_u();
+    const int w = wave_u(), lane = lane_id();
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       const int k = w + kW * j;
       if (k < n) {
-        const float *ra, *rb;
+        const W *ra, *rb;
         rows(k, ra, rb);
-        load_pair_weights<H>(ra, rb, wv[j]);
+        const Slot *a4 = reinterpret_cast<const Slot *>(ra);
+        const Slot *b4 = reinterpret_cast<const Slot *>(rb);
+#pragma unroll
+        for (int c = 0; c < NJ; ++c) {
+          if constexpr (kNarrow)
+            raw[j][c] = load_slot(a4, b4, c, lane);
+          else
+            wv[j][c] = load_slot(a4, b4, c, lane);
+        }
         pace();
       } else {
         // An empty slot is still redefined, so its previous contents are
         // not kept live across the code between two prefetches.
 #pragma unroll
-        for (int c = 0; c < NJ; ++c) wv[j][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int c = 0; c < NJ; ++c) {
+          if constexpr (kNarrow)
+            raw[j][c] = WT::zero();
+          else
+            wv[j][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
       }
+    }
+  }
+  // Narrow register units: widen the prefetched slots (waits for them).
+  __device__ void settle() {
+    if constexpr (kNarrow) {
+#pragma unroll
+      for (int j = 0; j < S; ++j)
+#pragma unroll
+        for (int c = 0; c < NJ; ++c) wv[j][c] = pin(WT::widen(raw[j][c]));
     }
   }
   template <typename Rows>
   __device__ void prefetch_lds(Rows rows) {
     const int lane = lane_id();
-    for (int k = kW * S + wave_u(); k < n && k - kW * S < Lcap; k += kW) {
-      const float *ra, *rb;
-      rows(k, ra, rb);
-      const float4 *a4 = reinterpret_cast<const float4 *>(ra);
-      const float4 *b4 = reinterpret_cast<const float4 *>(rb);
-      float4 *dst = units + (k - kW * S) * UnitF4;
+    if constexpr (!kNarrow) {
+      for (int k = kW * S + wave_u(); k < n && k - kW * S < Lcap; k += kW) {
+        const W *ra, *rb;
+        rows(k, ra, rb);
+        const Slot *a4 = reinterpret_cast<const Slot *>(ra);
+        const Slot *b4 = reinterpret_cast<const Slot *>(rb);
+        unsigned char *dst = units + (k - kW * S) * UnitBytes;
 #pragma unroll
-      for (int c = 0; c < NJ; ++c) {
-        const int f = c * kWave + lane;
-        const float4 *src = f < K4 ? a4 + f : (f < 2 * K4 ? b4 + (f - K4) : a4);
-        dma16<kPolicyNt>(src, dst + c * kWave);
-        pace();
+        for (int c = 0; c < NJ; ++c) {
+          const int f = c * kWave + lane;
+          const Slot *src = f < K4 ? a4 + f : (f < 2 * K4 ? b4 + (f - K4) : a4);
+          dma16<kPolicyNt>(src, dst + c * 1024);
+          pace();
+        }
+      }
+    } else {
+      // Two units in flight: unit k's slots are widened and stored while
+      // unit k + kW's loads are outstanding.
+      R cur[NJ], nxt[NJ];
+      int k = kW * S + wave_u();
+      auto fetch = [&](int kk, R (&buf)[NJ]) {
+        const W *ra, *rb;
+        rows(kk, ra, rb);
+        const Slot *a4 = reinterpret_cast<const Slot *>(ra);
+        const Slot *b4 = reinterpret_cast<const Slot *>(rb);
+#pragma unroll
+        for (int c = 0; c < NJ; ++c) buf[c] = load_slot(a4, b4, c, lane);
+      };
+      auto live = [&](int kk) { return kk < n && kk - kW * S < Lcap; };
+      if (live(k)) fetch(k, cur);
+      for (; live(k); k += kW) {
+        if (live(k + kW)) fetch(k + kW, nxt);
+        float4 *dst = reinterpret_cast<float4 *>(units + (k - kW * S) * UnitBytes);
+#pragma unroll
+        for (int c = 0; c < NJ; ++c) dst[c * kWave + lane] = WT::widen(cur[c]);
+#pragma unroll
+        for (int c = 0; c < NJ; ++c) cur[c] = nxt[c];
       }
     }
   }
@@ -593,7 +664,7 @@ struct PairRole {
     for (int i = 0; i < kLdsPerWave; ++i) {
       const int k = kW * S + w + kW * i;
       if (k < n && k - kW * S < Lcap) {
-        const float4 *src = units + (k - kW * S) * UnitF4;
+        const float4 *src = reinterpret_cast<const float4 *>(units + (k - kW * S) * UnitBytes);
         float4 wl[NJ];
 #pragma unroll
         for (int c = 0; c < NJ; ++c) wl[c] = src[c * kWave + lane];
@@ -625,8 +696,12 @@ struct PairRole {
 // slice sums in LDS; wave w then finishes rows w, w + 8, ... (per lane
 // combine_slices over the waves' sums, then wave_sum: dot_row_sliced's
 // order). Registers are indexed with the slice width as a template constant.
-template <int I>
+template <int I, typename W>
 struct DownRole {
+  using WT = WReg<W>;
+  using R = typename WT::type;
+  using Slot = typename WSlot<W>::type;
+  static constexpr bool kNarrow = sizeof(R) == 8;
   static constexpr int NJ = RowSlots<I>::NJ;
   static constexpr int kNsLo = NJ / kRowSlices, kNsHi = (NJ + kRowSlices - 1) / kRowSlices;
   // Weight float4s per lane held in registers (a wider budget for the
@@ -650,7 +725,11 @@ struct DownRole {
     while (n > 0 && lds_rows(n) * kWave * 16 + n * kRowSlices * kWave * 4 > kRegionBytes) --n;
     return n;
   }
+  // Registers and LDS hold FP32 whatever W is (PairRole's scheme): narrow
+  // register rows arrive in raw and are widened by settle(); narrow LDS
+  // rows pass through the wave's registers and are widened on the way.
   float4 wr[kRegF4];
+  R raw[kNarrow ? kRegF4 : 1];
   float4 *lw = nullptr;   // this wave's LDS rows: ((r - nr) * ns + s) * 64 + lane
   int n = 0, c0 = 0, ns = 0, nr = 0;
 
@@ -674,9 +753,13 @@ struct DownRole {
 #pragma unroll
     for (int r = 0; r < Nr; ++r) {
 #pragma unroll
-      for (int s = 0; s < Ns; ++s)
-        wr[r * Ns + s] = r < n ? ld_weight(reinterpret_cast<const float4 *>(row(r)) + (c0 + s) * kWave + lane)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int s = 0; s < Ns; ++s) {
+        const Slot *src = reinterpret_cast<const Slot *>(row(r)) + (c0 + s) * kWave + lane;
+        if constexpr (kNarrow)
+          raw[r * Ns + s] = r < n ? ld_slot(src) : WT::zero();
+        else
+          wr[r * Ns + s] = r < n ? ld_slot(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
       pace();
     }
   }
@@ -684,15 +767,43 @@ struct DownRole {
   __device__ void prefetch_regs(Row row) {
     if (ns == kNsHi) prefetch_regs_ns<kNsHi>(row); else prefetch_regs_ns<kNsLo>(row);
   }
+  // Narrow register rows: widen the prefetched slots (waits for them).
+  __device__ void settle() {
+    if constexpr (kNarrow) {
+#pragma unroll
+      for (int i = 0; i < kRegF4; ++i) wr[i] = pin(WT::widen(raw[i]));
+    }
+  }
   template <typename Row>
   __device__ void prefetch_lds(Row row) {
     const int lane = lane_id();
-    for (int r = nr; r < n; ++r)
-      for (int s = 0; s < ns; ++s) {
-        dma16<kPolicyNt>(reinterpret_cast<const float4 *>(row(r)) + (c0 + s) * kWave + lane,
-                         lw + ((r - nr) * ns + s) * kWave);
-        pace();
+    if constexpr (!kNarrow) {
+      for (int r = nr; r < n; ++r)
+        for (int s = 0; s < ns; ++s) {
+          dma16<kPolicyNt>(reinterpret_cast<const Slot *>(row(r)) + (c0 + s) * kWave + lane,
+                           lw + ((r - nr) * ns + s) * kWave);
+          pace();
+        }
+    } else {
+      // A row's slots (at most kNsHi) in flight while the previous row's
+      // are widened and stored.
+      R cur[kNsHi], nxt[kNsHi];
+      auto fetch = [&](int r, R (&buf)[kNsHi]) {
+        const Slot *src = reinterpret_cast<const Slot *>(row(r)) + c0 * kWave + lane;
+#pragma unroll
+        for (int s = 0; s < kNsHi; ++s)
+          if (s < ns) buf[s] = ld_slot(src + s * kWave);
+      };
+      if (nr < n) fetch(nr, cur);
+      for (int r = nr; r < n; ++r) {
+        if (r + 1 < n) fetch(r + 1, nxt);
+#pragma unroll
+        for (int s = 0; s < kNsHi; ++s)
+          if (s < ns) lw[((r - nr) * ns + s) * kWave + lane] = WT::widen(cur[s]);
+#pragma unroll
+        for (int s = 0; s < kNsHi; ++s) cur[s] = nxt[s];
       }
+    }
   }
   // Per-lane slice sums of every row with this wave's activation slice xa:
   // row r's lands in part[(r * kW + wave) * 64 + lane]. The register rows
@@ -747,7 +858,7 @@ __device__ __forceinline__ int split_begin(int total, int parts, int r) {
   return static_cast<int>((static_cast<int64_t>(total) * r) / parts);
 }
 
-template <int H, int I, int NQ, int NKV>
+template <int H, int I, int NQ, int NKV, typename W = float>
 struct Shape {
   static constexpr int QD = NQ * kHeadDim;
   static constexpr int KVD = NKV * kHeadDim;
@@ -755,7 +866,7 @@ struct Shape {
   static constexpr int QkvRows = QD + 2 * KVD;
   static constexpr int QkvUnits = QkvRows / 2;
   static constexpr int OUnits = H / 2;
-  static constexpr int UnitBytes = PairSlots<H>::NJ * kWave * 16;
+  static constexpr int UnitBytes = PairSlots<H>::NJ * 1024;
   static constexpr int RowBytes = RowSlots<I>::NJ * kWave * 16;
   // QKV region: units, biases (whole float4 DMA rows), cos|sin row.
   static constexpr int BiasF4 = (QkvRows / 4 + kWave - 1) / kWave * kWave;
@@ -766,7 +877,7 @@ struct Shape {
   // (its G query heads) of every row, so its units are row pairs of QDG
   // columns, and its region holds units and its group's records.
   static constexpr int QDG = G * kHeadDim;
-  static constexpr int OUnitBytes = PairSlots<QDG>::NJ * kWave * 16;
+  static constexpr int OUnitBytes = PairSlots<QDG>::NJ * 1024;
   static constexpr int PartFloatsG = G * kAttnMaxChunks * kRoleRecStride;
   static constexpr int LO = (kRegionBytes - PartFloatsG * 4) / OUnitBytes;
   static constexpr int LG = kRegionBytes / UnitBytes;
@@ -798,9 +909,9 @@ __device__ __forceinline__ int attn_v_slot(int j, int d) { return j * kHeadDim +
 // token state, and the pieces every role shares (the per-token loop, the LM
 // head and the argmax). Each role runs its own loop (run_*), so the register
 // slots of one role are never live in another role's code.
-template <int H, int I, int NQ, int NKV, bool kProfile>
+template <int H, int I, int NQ, int NKV, bool kProfile, typename W>
 struct Roles {
-  using Sh = Shape<H, I, NQ, NKV>;
+  using Sh = Shape<H, I, NQ, NKV, W>;
   static constexpr int QD = Sh::QD, KVD = Sh::KVD, GROUP = Sh::G;
   static constexpr int NJ = PairSlots<H>::NJ;
 
@@ -1160,9 +1271,9 @@ struct Roles {
     const int g = rank / gq, rr = rank % gq;
     constexpr int GU = (GROUP + 2) * kRotary;
     const int j0 = split_begin(GU, gq, rr);
-    PairRole<H, kSlotsQ, Sh::LQ> rq;
+    PairRole<H, kSlotsQ, Sh::LQ, W> rq;
     rq.n = split_begin(GU, gq, rr + 1) - j0;
-    rq.units = reinterpret_cast<float4 *>(region);
+    rq.units = region;
     if (!fits(rq.n, rq.capacity())) return;
     // Packed head of the group's local head lh (0..G-1 query, G: K, G+1: V).
     auto head_of = [&](int lh) { return lh < GROUP ? GROUP * g + lh : (lh == GROUP ? NQ + g : NQ + NKV + g); };
@@ -1170,8 +1281,8 @@ struct Roles {
     float4 *q_bias = reinterpret_cast<float4 *>(region + Sh::LQ * Sh::UnitBytes);
     float4 *q_cs = q_bias + Sh::BiasF4;
     auto rows = [&](int l) {
-      const float *base = layer(l).wqkv;
-      return [=](int k, const float *&ra, const float *&rb) {
+      const W *base = reinterpret_cast<const W *>(layer(l).wqkv);
+      return [=](int k, const W *&ra, const W *&rb) {
         const int u = unit_of(j0 + k);
         const int row = (u / kRotary) * kHeadDim + u % kRotary;
         ra = base + static_cast<size_t>(row) * H;
@@ -1217,6 +1328,7 @@ struct Roles {
       if (om.q >= 0) clear_quad(s_qkv(l, t + 1), om);
       float4 gv[NJ];
       load_pair_gain<H>(lw.attn_norm, gv);
+      rq.settle();
       if (!layer_input(t, l, 0, H / 4, cm.vec)) return false;
       clock.lap(2 * kRoleQkv);
       float4 xv[NJ];
@@ -1497,9 +1609,9 @@ struct Roles {
     const int gn = a.group_cus[2];
     const int g = rank / gn, rr = rank % gn;
     const int u0 = split_begin(Sh::OUnits, gn, rr);
-    PairRole<QDG, kSlotsO, Sh::LO> ro;
+    PairRole<QDG, kSlotsO, Sh::LO, W> ro;
     ro.n = split_begin(Sh::OUnits, gn, rr + 1) - u0;
-    ro.units = reinterpret_cast<float4 *>(region);
+    ro.units = region;
     if (!fits(ro.n, ro.capacity())) return;
     // The group's partial records in LDS: record (head 7g + j, c) at
     // (j * kAttnMaxChunks + c) * kRoleRecStride. The merge reads chunks
@@ -1508,8 +1620,8 @@ struct Roles {
     float *parts = reinterpret_cast<float *>(region + Sh::LO * Sh::OUnitBytes);
     for (int i = threadIdx.x; i < Sh::PartFloatsG; i += kT) parts[i] = 0.f;
     auto rows = [&](int l) {
-      const float *base = layer(l).wo + g * QDG;
-      return [=](int k, const float *&ra, const float *&rb) {
+      const W *base = reinterpret_cast<const W *>(layer(l).wo) + g * QDG;
+      return [=](int k, const W *&ra, const W *&rb) {
         ra = base + static_cast<size_t>(2 * (u0 + k)) * QD;
         rb = ra + QD;
       };
@@ -1526,6 +1638,7 @@ struct Roles {
       // input, in the float4s covering them (row r at cm.vec[r - 4 f4]).
       const int f4 = (2 * u0) / 4, e4 = (2 * (u0 + ro.n) + 3) / 4;
       const int roff = 2 * u0 - 4 * f4;
+      ro.settle();
       if (g == 0 && !layer_input(t, l, f4, e4 - f4, cm.vec)) return false;
       // The partial records of the group's heads over C chunks; one pass
       // covers sixteen chunks.
@@ -1616,14 +1729,14 @@ struct Roles {
     // Whole float4s of the activation per CU, so no float4 has two writers.
     static_assert(I % 4 == 0, "activation in float4s");
     const int u0 = 4 * split_begin(I / 4, nrole, rank);
-    PairRole<H, kSlotsG, Sh::LG> rg;
+    PairRole<H, kSlotsG, Sh::LG, W> rg;
     rg.n = 4 * split_begin(I / 4, nrole, rank + 1) - u0;
-    rg.units = reinterpret_cast<float4 *>(region);
+    rg.units = region;
     if (!fits(rg.n, rg.capacity())) return;
     auto rows = [&](int l) {
       const LayerPtrs lp = layer(l);
-      const float *g = lp.wg, *u = lp.wu;
-      return [=](int k, const float *&ra, const float *&rb) {
+      const W *g = reinterpret_cast<const W *>(lp.wg), *u = reinterpret_cast<const W *>(lp.wu);
+      return [=](int k, const W *&ra, const W *&rb) {
         ra = g + static_cast<size_t>(u0 + k) * H;
         rb = u + static_cast<size_t>(u0 + k) * H;
       };
@@ -1638,6 +1751,7 @@ struct Roles {
       float *stage = cm.top;  // unit u0 + k at stage[k + (u0 & 3)]
       float4 gv[NJ];
       load_pair_gain<H>(layer(l).mlp_norm, gv);
+      rg.settle();
       if (!gather_h1(t, l, 0, H / 4, cm.vec)) return false;
       clock.lap(2 * kRoleGate);
       float4 xv[NJ];
@@ -1666,12 +1780,12 @@ struct Roles {
   // ---- down + residual ------------------------------------------------------
   __device__ void run_down() {
     const int u0 = split_begin(H, nrole, rank);
-    DownRole<I> rd;
+    DownRole<I, W> rd;
     const int n = split_begin(H, nrole, rank + 1) - u0;
-    if (!fits(n, DownRole<I>::capacity())) return;
+    if (!fits(n, DownRole<I, W>::capacity())) return;
     rd.init(n, reinterpret_cast<float4 *>(region));
     auto row = [&](int l) {
-      const float *base = layer(l).wd;
+      const W *base = reinterpret_cast<const W *>(layer(l).wd);
       return [=](int k) { return base + static_cast<size_t>(u0 + k) * I; };
     };
     auto pre_lds = [&](int l, int) { rd.prefetch_lds(row(l)); };
@@ -1679,31 +1793,32 @@ struct Roles {
     // This CU's output segment: float4s [seg4, seg4 + 4) of the layer
     // output, rows u0 + k at element k, padded with zeros; thread q < pub4
     // publishes float4 q.
-    static_assert(DownRole<I>::kMaxRows <= kHidSegment, "a down CU's rows fit its segment");
+    static_assert(DownRole<I, W>::kMaxRows <= kHidSegment, "a down CU's rows fit its segment");
     const int seg4 = (kHidSegment / 4) * rank, pub4 = (n + 3) / 4;
     const bool pub = static_cast<int>(threadIdx.x) < pub4;
     const int hb4 = u0 / 4;                       // float4s of h1 covering [u0, u0 + n)
     const int hn4 = (u0 + n + 3) / 4 - hb4;
     // Per-lane slice sums [row][wave][lane], after this CU's LDS rows.
-    float *part = reinterpret_cast<float *>(region) + DownRole<I>::lds_rows(n) * kWave * 4;
+    float *part = reinterpret_cast<float *>(region) + DownRole<I, W>::lds_rows(n) * kWave * 4;
     float *stage = cm.top;  // row u0 + k at stage[k]
     loop(kRoleDown, true, [&](uint32_t t, int l, int position) {
       const Slots out = s_hid(l, t);
       if (pub) s_hid(l, t + 1).clear4(seg4 + threadIdx.x);
+      rd.settle();
       if (!gather_h1(t, l, hb4, hn4, cm.vec)) return false;
       // This wave's slice of the activation, straight into registers.
-      float4 xa[DownRole<I>::kNsHi];
+      float4 xa[DownRole<I, W>::kNsHi];
       bool ok = true;
       {
         const Slots src = s_act(l, t);
         uint32_t pending = (1u << rd.ns) - 1u;
         for (uint32_t spin = 0; ok; ++spin) {
-          Quad got[DownRole<I>::kNsHi];
+          Quad got[DownRole<I, W>::kNsHi];
 #pragma unroll
-          for (int s = 0; s < DownRole<I>::kNsHi; ++s)
+          for (int s = 0; s < DownRole<I, W>::kNsHi; ++s)
             if ((pending >> s) & 1u) got[s] = __builtin_bit_cast(Quad, src.get4((rd.c0 + s) * kWave + lane));
 #pragma unroll
-          for (int s = 0; s < DownRole<I>::kNsHi; ++s) {
+          for (int s = 0; s < DownRole<I, W>::kNsHi; ++s) {
             const Quad &g = got[s];
             if (((pending >> s) & 1u) && g.w[0] != kSlotEmpty && g.w[1] != kSlotEmpty &&
                 g.w[2] != kSlotEmpty && g.w[3] != kSlotEmpty) {
@@ -1728,7 +1843,7 @@ struct Roles {
       // Wave w finishes rows w and w + kW (at most kMaxRows = 2 kW rows): the
       // slice sums of both rows are read at once and reduced together
       // (wave_sum_multi: row w's sum in lane 0, row w + kW's in lane 1).
-      static_assert(DownRole<I>::kMaxRows <= 2 * kW, "two rows per wave");
+      static_assert(DownRole<I, W>::kMaxRows <= 2 * kW, "two rows per wave");
       if (wv < n) {
         const int k1 = min(wv + kW, n - 1);
         float p0[kRowSlices], p1[kRowSlices];
@@ -1759,7 +1874,7 @@ struct Roles {
 
 // Each role's loop is its own (non-inlined) function so the register
 // allocator sizes each role separately instead of one body holding all five.
-template <int H, int I, int NQ, int NKV, bool kProfile, int kRole>
+template <int H, int I, int NQ, int NKV, bool kProfile, typename W, int kRole>
 __device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank, int nrole) {
   // The launch arguments, copied with scalar loads from the kernel's
   // argument segment (whose address the kernel passes: a callee has no
@@ -1782,7 +1897,7 @@ __device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank
 #pragma unroll
     for (size_t i = 0; i < sizeof(ResidentArgs) / 4; ++i) dst[i] = src[i];
   }
-  Roles<H, I, NQ, NKV, kProfile> r(a, roles_lds, __builtin_amdgcn_readfirstlane(rank),
+  Roles<H, I, NQ, NKV, kProfile, W> r(a, roles_lds, __builtin_amdgcn_readfirstlane(rank),
                                    __builtin_amdgcn_readfirstlane(nrole));
   if constexpr (kRole == kRoleQkv) r.run_qkv();
   if constexpr (kRole == kRoleAttn) r.run_attn();
@@ -1816,7 +1931,7 @@ __device__ __forceinline__ uint32_t xcc_id() {
   return v & 0xFu;
 }
 
-template <int H, int I, int NQ, int NKV, bool kProfile>
+template <int H, int I, int NQ, int NKV, bool kProfile, typename W>
 __global__ __launch_bounds__(kT, 1) void roles_kernel(ResidentArgs a) {
   const void *kernarg = (const void *)__builtin_amdgcn_kernarg_segment_ptr();
   // A workgroup placed for an XCD it does not run on stops (its waiting
@@ -1832,27 +1947,36 @@ __global__ __launch_bounds__(kT, 1) void roles_kernel(ResidentArgs a) {
   const int rank = b - rbeg, nrole = a.role_end[role] - rbeg;
   switch (role) {
     case kRoleQkv:
-      run_role<H, I, NQ, NKV, kProfile, kRoleQkv>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleQkv>(kernarg, rank, nrole);
       break;
     case kRoleAttn:
-      run_role<H, I, NQ, NKV, kProfile, kRoleAttn>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleAttn>(kernarg, rank, nrole);
       break;
     case kRoleO:
-      run_role<H, I, NQ, NKV, kProfile, kRoleO>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleO>(kernarg, rank, nrole);
       break;
     case kRoleGate:
-      run_role<H, I, NQ, NKV, kProfile, kRoleGate>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleGate>(kernarg, rank, nrole);
       break;
     default:
-      run_role<H, I, NQ, NKV, kProfile, kRoleDown>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleDown>(kernarg, rank, nrole);
       break;
   }
 }
 
 using Qwen = Shape<896, 4864, 14, 2>;
-const void *roles_fn(bool profile) {
-  return profile ? reinterpret_cast<const void *>(&roles_kernel<896, 4864, 14, 2, true>)
-                 : reinterpret_cast<const void *>(&roles_kernel<896, 4864, 14, 2, false>);
+// The kernel instance for the decoder matrices' storage (kWeights*).
+template <typename W>
+const void *roles_fn_as(bool profile) {
+  return profile ? reinterpret_cast<const void *>(&roles_kernel<896, 4864, 14, 2, true, W>)
+                 : reinterpret_cast<const void *>(&roles_kernel<896, 4864, 14, 2, false, W>);
+}
+const void *roles_fn(bool profile, int weights_dtype) {
+  switch (weights_dtype) {
+    case kWeightsBf16: return roles_fn_as<Bf16>(profile);
+    case kWeightsF16: return roles_fn_as<F16>(profile);
+    default: return roles_fn_as<float>(profile);
+  }
 }
 
 }  // namespace
@@ -1865,7 +1989,7 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
   // O: each of the KV groups covers every row pair (Roles::run_o).
   const int units[4] = {Qwen::QkvUnits, kv_heads * Qwen::OUnits, inter, hidden};
   const int cap[4] = {Qwen::LQ + kW * kSlotsQ, Qwen::LO + kW * kSlotsO, Qwen::LG + kW * kSlotsG,
-                      DownRole<4864>::capacity()};
+                      DownRole<4864, float>::capacity()};
   const double bytes[4] = {double(units[0]) * Qwen::UnitBytes, double(units[1]) * Qwen::OUnitBytes,
                            double(units[2]) * Qwen::UnitBytes, double(units[3]) * Qwen::RowBytes};
   const double total = bytes[0] + bytes[1] + bytes[2] + bytes[3];
@@ -1948,7 +2072,10 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
 
 hipError_t launch_roles(hipStream_t s, const ResidentArgs &args, int grid) {
   void *params[] = {const_cast<ResidentArgs *>(&args)};
-  return hipLaunchCooperativeKernel(roles_fn(args.stage_ticks || args.trace), dim3(grid), dim3(kT),
+  if (args.weights_dtype != kWeightsF32 && args.weights_dtype != kWeightsBf16 &&
+      args.weights_dtype != kWeightsF16)
+    return hipErrorInvalidValue;
+  return hipLaunchCooperativeKernel(roles_fn(args.stage_ticks || args.trace, args.weights_dtype), dim3(grid), dim3(kT),
                                     params, 0, s);
 }
 
@@ -1959,13 +2086,19 @@ int device_cu_count(int device) {
   return cus;
 }
 
-int roles_max_grid(int device) {
+int roles_max_grid(int device, int weights_dtype) {
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, roles_fn(true), kT, 0) != hipSuccess)
-    return 0;
-  return cus * per_cu;
+  // Every instance of the storage type must fit (the profiled one included).
+  int lo = 1 << 30;
+  for (bool profile : {false, true}) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, roles_fn(profile, weights_dtype), kT, 0) !=
+        hipSuccess)
+      return 0;
+    lo = std::min(lo, per_cu);
+  }
+  return cus * lo;
 }
 
 }  // namespace qd

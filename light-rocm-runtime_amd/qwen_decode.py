@@ -21,7 +21,7 @@ SUCCESS, INVALID_ARGUMENT, NOT_INITIALIZED, ALREADY_INITIALIZED, NOT_SUPPORTED, 
 STOP_NONE, STOP_MAXIMUM_TOKENS, STOP_EOS_TOKEN = range(3)
 NO_EOS = 0xFFFFFFFF
 EMBED, FINAL_NORM, LM_HEAD = 0x100, 0x101, 0x102
-DTYPE_F32, DTYPE_BF16 = 0, 1
+DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 
 
 class QdError(RuntimeError):
@@ -187,10 +187,10 @@ class EngineConfig:
     rms_eps: float = 1e-6
     rope_theta: float = 1e6
     device: int = 0
-    decoder_dtype: str = "f32"  # "f32" or "bf16": storage of the decoder layers' matrices
+    decoder_dtype: str = "f32"  # "f32", "bf16" or "f16": storage of the decoder layers' matrices
 
     def c(self) -> Config:
-        dtypes = {"f32": DTYPE_F32, "bf16": DTYPE_BF16}
+        dtypes = {"f32": DTYPE_F32, "bf16": DTYPE_BF16, "f16": DTYPE_F16}
         if self.decoder_dtype not in dtypes:
             raise ValueError(f"decoder_dtype must be one of {sorted(dtypes)}")
         return Config(self.hidden, self.heads, self.kv_heads, self.head_dim, self.intermediate,

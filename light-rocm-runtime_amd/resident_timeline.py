@@ -65,8 +65,10 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=16, help="tokens in the traced launch")
     ap.add_argument("--trace-token", type=int, default=8, help="which token's timeline to record")
     ap.add_argument("--save", help="write the raw [workgroup, layer, stage] array here (.npy)")
+    ap.add_argument("--dtype", default="f32", choices=("f32", "bf16", "f16"),
+                    help="storage of the decoder layers' matrices")
     args = ap.parse_args()
-    eng = qd.Engine(capacity=args.context + args.tokens + 64, max_batch=1)
+    eng = qd.Engine(capacity=args.context + args.tokens + 64, max_batch=1, decoder_dtype=args.dtype)
     try:
         if eng.resident_grid() == 0:
             print("resident path unavailable on this device", file=sys.stderr)
@@ -76,7 +78,7 @@ def main() -> int:
         tr = eng.trace_resident(0, 4242, args.tokens, args.trace_token)
         if args.save:
             np.save(args.save, tr)
-        print(f"context {args.context}, token {args.trace_token} of {args.tokens}")
+        print(f"context {args.context}, token {args.trace_token} of {args.tokens}, {args.dtype} decoder matrices")
         for line in summarize(tr, eng.config.layers):
             print(line)
     finally:
