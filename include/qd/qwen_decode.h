@@ -246,8 +246,8 @@ QD_API qd_status qd_layer_decode(qd_engine *engine, uint32_t seq,
  * of benchmarks/triton_mini_decoder_layer.cpp:394-422. Synchronous. */
 QD_API qd_status qd_tail(qd_engine *engine, uint32_t seq, float *logits_out,
                          uint32_t *greedy_out, float *top_logit);
-/* The slot's logits of its last qd_step / qd_tail / qd_prefill (`count`
- * must equal vocab). Replaces ModelTail::copy_logits
+/* The slot's logits of its last qd_step / qd_tail / qd_prefill /
+ * qd_step_batch / qd_step_batch_noalloc (`count` must equal vocab). Replaces ModelTail::copy_logits
  * (examples/triton/mini_decoder_layer.hpp:866-871). */
 QD_API qd_status qd_read_logits(qd_engine *engine, uint32_t seq, float *out,
                                 size_t count);
@@ -272,7 +272,10 @@ QD_API qd_status qd_prefill(qd_engine *engine, uint32_t seq,
                             float *top_logit);
 
 /* One decode step for n_seq independent sequences at their own positions.
- * logits [n_seq][vocab] and greedy [n_seq] (both nullable). */
+ * logits [n_seq][vocab] and greedy [n_seq] (both nullable); each sequence's
+ * logits also stay on the device in its slot's row, for qd_read_logits.
+ * The reference has no batched step (examples/qwen/README.md:431-432): its
+ * semantics per sequence are qd_step's. */
 QD_API qd_status qd_step_batch(qd_engine *engine, uint32_t n_seq,
                                const uint32_t *seq_ids, const uint32_t *tokens,
                                float *logits, uint32_t *greedy);
@@ -282,11 +285,13 @@ QD_API qd_status qd_step_batch(qd_engine *engine, uint32_t n_seq,
  * later. Its scratch (activation rows, attention records, split-K partials,
  * arrival counters, LM-head partials: 2.25 MiB) is a static device array of
  * the library, one per GPU, whose address the engine looks up when it is
- * created. Results equal qd_step_batch's bit for bit. Calls that overlap on
- * one GPU (two engines, or two host threads) share that array and race.
- * More than 16 sequences: QD_ERROR_INVALID_ARGUMENT. No counterpart in the
- * reference; it is for callers that cannot allocate (code under graph
- * capture, allocation-free serving loops). */
+ * created. Results equal qd_step_batch's bit for bit. Calls on one GPU (two
+ * engines, or two host threads) share that array: the library serialises
+ * them per GPU with a host lock, so they cannot interleave on the device.
+ * The call synchronises its stream before it returns (it is not capturable
+ * into a HIP graph). More than 16 sequences: QD_ERROR_INVALID_ARGUMENT. No
+ * counterpart in the reference; it is for callers that cannot allocate
+ * (allocation-free serving loops, harnesses that forbid hipMalloc). */
 QD_API qd_status qd_step_batch_noalloc(qd_engine *engine, uint32_t n_seq,
                                        const uint32_t *seq_ids,
                                        const uint32_t *tokens, float *logits,

@@ -613,7 +613,7 @@ __global__ __launch_bounds__(kBlock) void batch_lmhead_kernel(BatchLaunch p, Bat
   const int t = threadIdx.x;
   const int seq = tile_seq(t);
   const float inv = rsqrtf(ss[seq] / static_cast<float>(kH) + p.eps);
-  float *out = seq < p.rows ? tl.logits + static_cast<size_t>(seq) * tl.vocab : nullptr;
+  float *out = seq < p.rows ? tl.logits + static_cast<size_t>(p.slot[seq]) * tl.vocab : nullptr;
   float best = -INFINITY;
   uint32_t best_i = UINT32_MAX;
   for (int it = 0; tile < tiles; tile += gridDim.x, ++it) {
@@ -791,6 +791,11 @@ void *batch_scratch(int device, hipError_t *err) {
     g_scratch_ptr[device] = p;
   }
   return g_scratch_ptr[device];
+}
+
+std::mutex &batch_scratch_lock(int device) {
+  static std::mutex locks[kMaxScratchDevices];
+  return locks[device >= 0 && device < kMaxScratchDevices ? device : 0];
 }
 
 hipError_t launch_batch_clear_counters(hipStream_t s, uint32_t *counters) {

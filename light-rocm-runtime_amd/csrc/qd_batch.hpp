@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
 #include "qd_device.hpp"
 #include "qd_kernels.hpp"
@@ -52,7 +53,7 @@ constexpr int kBatchCounters = 1024;
 struct BatchTail {
   const float *final_norm;
   const float *head;     // [vocab, 896]
-  float *logits;         // [kBatchRows][vocab], row = batch row
+  float *logits;         // [max_batch][vocab]: batch row b writes the row of its slot, slot[b]
   float *part_val;       // [kBatchRows][kBatchLmParts]
   uint32_t *part_idx;
   uint32_t *out_token;   // [kBatchRows] greedy token of each row
@@ -87,6 +88,9 @@ BatchWorkspace carve_batch_workspace(void *base, int nq);
 // while that device is current. nullptr (and *err set) on failure.
 constexpr size_t kBatchScratchBytes = size_t(9) << 18;  // 2.25 MiB
 void *batch_scratch(int device, hipError_t *err);
+// Host lock of a device's static batch workspace: a step that uses the
+// workspace holds it from its first launch until its stream is synchronised.
+std::mutex &batch_scratch_lock(int device);
 // Zeroes a workspace's arrival counters with a fill kernel (a step expects
 // them zero; a step that stopped early can leave them set).
 hipError_t launch_batch_clear_counters(hipStream_t s, uint32_t *counters);

@@ -416,13 +416,14 @@ struct qd_engine {
     return b;
   }
 
-  // Tail arguments of the group whose first batch row is `first`: logits go
-  // to rows first.. of the logits buffer, greedy results to bt_token/bt_top.
+  // Tail arguments of the group whose first batch row is `first`: each
+  // row's logits go to its slot's row of the logits buffer (where
+  // qd_read_logits finds them), greedy results to bt_token/bt_top.
   qd::BatchTail batch_tail(size_t first) const {
     qd::BatchTail t{};
     t.final_norm = final_norm;
     t.head = lm_head;
-    t.logits = logits + first * V;
+    t.logits = logits;
     t.part_val = bt_val;
     t.part_idx = bt_idx;
     t.out_token = bt_token + first;
@@ -915,6 +916,7 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
       e->batch_scratch = qd::batch_scratch(c.device, &err);
       if (!e->batch_scratch) e->batch_scratch_error = hipGetErrorString(err);
     }
+
     e->sync();
     *out = e.release();
   });
@@ -1556,9 +1558,10 @@ qd_status qd_step_batch(qd_engine *e, uint32_t n_seq, const uint32_t *seq_ids, c
     check(hipMemcpyAsync(e->h_bt_out + e->B, e->bt_top, n_seq * 4, hipMemcpyDeviceToHost, e->stream),
           "D2H");
     if (logits)
-      check(hipMemcpyAsync(logits, e->logits, size_t(n_seq) * e->V * 4, hipMemcpyDeviceToHost,
-                           e->stream),
-            "D2H");
+      for (uint32_t i = 0; i < n_seq; ++i)
+        check(hipMemcpyAsync(logits + size_t(i) * e->V, e->logits + size_t(seq_ids[i]) * e->V, e->V * 4,
+                             hipMemcpyDeviceToHost, e->stream),
+              "D2H");
     e->sync();
     for (uint32_t i = 0; i < n_seq; ++i) {
       e->positions[seq_ids[i]] += 1;
@@ -1589,6 +1592,8 @@ qd_status qd_step_batch_noalloc(qd_engine *e, uint32_t n_seq, const uint32_t *se
     if (!e->batch_scratch)
       fail(QD_ERROR_NOT_SUPPORTED, "static batch workspace unavailable: %s", e->batch_scratch_error.c_str());
     e->set_device();
+    // One step at a time per GPU on the shared workspace.
+    std::lock_guard<std::mutex> lock(qd::batch_scratch_lock(e->cfg.device));
     // Every buffer but the step's inputs and outputs (weights, KV cache,
     // slot states, the logits rows) lives in the static workspace.
     const qd::BatchWorkspace w = qd::carve_batch_workspace(e->batch_scratch, int(e->NQ));
@@ -1635,8 +1640,10 @@ qd_status qd_step_batch_noalloc(qd_engine *e, uint32_t n_seq, const uint32_t *se
     if (greedy)
       check(hipMemcpyAsync(greedy, w.out_token, n_seq * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
     if (logits)
-      check(hipMemcpyAsync(logits, e->logits, size_t(n_seq) * e->V * 4, hipMemcpyDeviceToHost, e->stream),
-            "D2H");
+      for (uint32_t i = 0; i < n_seq; ++i)
+        check(hipMemcpyAsync(logits + size_t(i) * e->V, e->logits + size_t(seq_ids[i]) * e->V, e->V * 4,
+                             hipMemcpyDeviceToHost, e->stream),
+              "D2H");
     e->sync();
     for (uint32_t i = 0; i < n_seq; ++i) e->positions[seq_ids[i]] += 1;
   });

@@ -61,7 +61,19 @@ constexpr int kLdsBytes = 160 * 1024 - 512;
 constexpr int kAttnCap = 256;     // positions of an attention window staged in LDS
 
 // Register slots per wave: row-pair units of the K=H roles, rows of DOWN.
-constexpr int kSlotsQ = 2, kSlotsO = 4, kSlotsG = 2;
+#ifndef QD_SLOTS_Q
+#define QD_SLOTS_Q 2
+#endif
+#ifndef QD_SLOTS_O
+#define QD_SLOTS_O 4
+#endif
+#ifndef QD_SLOTS_G
+#define QD_SLOTS_G 2
+#endif
+#ifndef QD_DOWN_REG_F4
+#define QD_DOWN_REG_F4 18
+#endif
+constexpr int kSlotsQ = QD_SLOTS_Q, kSlotsO = QD_SLOTS_O, kSlotsG = QD_SLOTS_G;
 
 // Wave index as a wave-uniform (scalar) value: unit indices, slot branches
 // and row addresses derived from it stay in SGPRs.
@@ -707,7 +719,7 @@ struct DownRole {
   // Weight float4s per lane held in registers (a wider budget for the
   // wide slices made the compiler keep the array in scratch).
   __host__ __device__ static constexpr int reg_f4(int) { return kRegF4; }
-  static constexpr int kRegF4 = 18;
+  static constexpr int kRegF4 = QD_DOWN_REG_F4;
   static constexpr int kMaxRows = 16;
   static_assert(kRowSlices == kW && kNsLo >= 1, "one slice per wave");
   // LDS 1 KiB slot-rows of the CU's n rows (what the registers do not hold).

@@ -6,7 +6,9 @@ skinny M=16 GEMMs on the FP32 matrix cores. Parity:
   * each batched step of every sequence against the batch-1 step of the same
     sequence from the same cache state (the batch-1 path is pinned against
     the oracle in test_gpu_decode.py);
-  * the two shortest sequences directly against the CPU oracle;
+  * the two shortest sequences directly against the CPU oracle, and all 16
+    (up to context 2,048) against the oracle decoding over the engine's own
+    K/V rows;
   * KV-cache slot indexing: the step writes exactly row L of each slot's
     cache, rows below L stay bit-identical, and row L matches the oracle's.
 Bars as in test_gpu_decode.py: logits max|d|/max|ref| <= 1e-4, tokens equal
@@ -122,6 +124,60 @@ def test_batch16_first_step_matches_oracle_and_single_steps(batch16):
             k, v = eng.read_kv(s, 5, lengths[s], 1)
             assert rel_err(batch_kv[s][0], k[0]) <= HIDDEN_RTOL, s
             assert rel_err(batch_kv[s][1], v[0]) <= HIDDEN_RTOL, s
+
+
+def test_batch16_every_sequence_matches_oracle_on_engine_kv(batch16):
+    """One batched step of all 16 sequences, each against the CPU oracle
+    decoding the same token at the same position over the engine's own K/V
+    rows [0, L) (read back through qd_read_kv and written into the oracle's
+    cache), so the longest contexts (up to 2,048) are checked directly, not
+    only through the batch-1 path. The batched logits also stay on the
+    device in each slot's row (qd_read_logits)."""
+    eng, lengths, prompts, firsts = batch16
+    slots = list(range(ROWS))
+    for s in slots:
+        eng.kv_reset(s, lengths[s])
+    say("batch step over 16 ragged sequences")
+    greedy, logits = eng.step_batch(slots, firsts)
+    for s in slots:
+        assert np.array_equal(eng.read_logits(s), logits[s]), s
+    model = qo.Model(SHAPE)
+    model.fill_synthetic(SEED)
+    try:
+        for s in sorted(slots, key=lambda i: -lengths[i]):
+            say(f"oracle over the engine's K/V: slot {s}, context {lengths[s]}")
+            cache = qo.Cache(model, lengths[s] + 4)
+            for layer in range(SHAPE.layers):
+                k, v = eng.read_kv(s, layer, 0, lengths[s])
+                cache.layer(layer, False)[: lengths[s]] = k
+                cache.layer(layer, True)[: lengths[s]] = v
+            rtok, _, rlog = cache.decode_step(firsts[s], lengths[s])
+            check_logits(int(greedy[s]), logits[s], rtok, rlog, f"batch slot {s} (context {lengths[s]}) vs oracle")
+            k, v = eng.read_kv(s, 11, lengths[s], 1)
+            assert rel_err(k[0], cache.layer(11, False)[lengths[s]]) <= HIDDEN_RTOL, s
+            assert rel_err(v[0], cache.layer(11, True)[lengths[s]]) <= HIDDEN_RTOL, s
+            cache.close()
+    finally:
+        model.close()
+
+
+def test_batch_step_leaves_other_slots_logits(batch16):
+    """qd_read_logits returns each slot's logits of its last step: a batched
+    step over other slots leaves a slot's qd_tail logits in place."""
+    eng, lengths, _, firsts = batch16
+    say("qd_tail on slot 0, then a batched step of slots 1..15")
+    eng.kv_reset(0, lengths[0])
+    eng.embed_hidden(0, firsts[0])
+    eng.layer_decode(0, 0, SHAPE.layers, lengths[0] + 1)
+    tok0, _, tail_logits = eng.tail(0)
+    assert np.array_equal(eng.read_logits(0), tail_logits)
+    others = list(range(1, ROWS))
+    for s in others:
+        eng.kv_reset(s, lengths[s])
+    _, logits = eng.step_batch(others, [firsts[s] for s in others])
+    assert np.array_equal(eng.read_logits(0), tail_logits)
+    for i, s in enumerate(others):
+        assert np.array_equal(eng.read_logits(s), logits[i]), s
 
 
 def test_batch16_greedy_steps_track_single_steps(batch16):

@@ -2,7 +2,10 @@
 static device workspace, against qd_step_batch (same kernels, engine-owned
 workspace): tokens, logits and K/V rows bit for bit, on two calls in a row,
 the second with fewer sequences (the workspace keeps the first call's
-contents)."""
+contents). After the first call, further calls change neither the device's
+free memory (hipMemGetInfo) nor the engine's own allocations."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -17,6 +20,15 @@ VOCAB = 4096
 
 def say(msg):
     print(f"[gpu-case] {msg}", flush=True)
+
+
+def free_device_bytes():
+    """hipMemGetInfo's free bytes of the current device (the HIP runtime the
+    engine library already loaded)."""
+    hip = C.CDLL("libamdhip64.so")
+    free, total = C.c_size_t(), C.c_size_t()
+    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return int(free.value)
 
 
 def test_noalloc_batch_step_equals_batch_step():
@@ -40,9 +52,12 @@ def test_noalloc_batch_step_equals_batch_step():
                 k1, v1 = eng.read_kv(i, layer, len(p), 1)
                 k2, v2 = eng.read_kv(GROUP + i, layer, len(p), 1)
                 assert np.array_equal(k1, k2) and np.array_equal(v1, v2), (i, layer)
-        # A smaller second call, scrambled slots, greedy tokens fed back.
+        # A smaller second call, scrambled slots, greedy tokens fed back; it
+        # allocates nothing on the device.
         sel = np.array([3, 0, 11, 7, 14], np.uint32)
+        free0, own0 = free_device_bytes(), eng.device_bytes()
         g3, l3 = eng.step_batch_noalloc(sel, g1[sel])
+        assert free_device_bytes() == free0 and eng.device_bytes() == own0
         g4, l4 = eng.step_batch(sel + GROUP, g2[sel])
         assert np.array_equal(g3, g4) and np.array_equal(l3, l4)
         for j, i in enumerate(sel.tolist()):
