@@ -217,7 +217,7 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token):
     first, _, _ = eng.prefill(0, prompt, want_logits=False)
     grid = eng.resident_grid()
 
-    # Two decode paths over the same K tokens, interleaved over trials:
+    # Decode paths over the same K tokens, interleaved over trials:
     # "resident" (qd_generate_resident: one launch, argmax fed back on the
     # device) and "step" (qd_step per token with the logits copied to the
     # host: the reference executor surface's per-token contract).
@@ -233,14 +233,36 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token):
             out.append(tok)
         return out, None
 
-    paths = {"resident": resident, "step": step}
+    # "graph": the same per-token contract with the step's launches replayed
+    # from the slot's captured HIP graph (qd_step_graph).
+    def graph():
+        out, tok = [], first
+        for _ in range(K):
+            tok, _, _ = eng.step_graph(0, tok, want_logits=True)
+            out.append(tok)
+        return out, None
+
+    # "resident_step": the same per-token contract (one call per token, its
+    # logits copied to the host) served by the resident kernel: one
+    # cooperative launch per token (qd_generate_resident, max_tokens 1).
+    def resident_step():
+        out, tok = [], first
+        for _ in range(K):
+            toks, _, _ = eng.generate(0, tok, 1, want_logits=True)
+            tok = int(toks[0])
+            out.append(tok)
+        return out, None
+
+    paths = {"resident": resident, "step": step, "graph": graph, "resident_step": resident_step}
     if W:
         log(f"warmup {W} tokens per path")
         eng.generate(0, first, W)
-        eng.kv_reset(0, prompt_len)
-        tok = first
-        for _ in range(W):
-            tok, _, _ = eng.step(0, tok, want_logits=True)
+        one = lambda seq, tok, want_logits: eng.generate(seq, tok, 1, want_logits=want_logits)[0]
+        for fn in (eng.step, eng.step_graph, one):
+            eng.kv_reset(0, prompt_len)
+            tok = first
+            for _ in range(W):
+                tok = int(fn(0, tok, want_logits=True)[0])
     samples = {name: {"wall_ms": [], "device_us": []} for name in paths}
     tokens = {}
     log(f"timed: {trials} interleaved trials x {K} tokens per path")
@@ -256,10 +278,13 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token):
                 samples[name]["device_us"].append(dev_us)
             tokens.setdefault(name, toks)
             assert toks == tokens[name], f"{name}: trial {t} produced other tokens"
-    # The two paths run the same arithmetic: the same greedy chain.
-    assert tokens["resident"] == tokens["step"], "resident and step paths disagree"
+    # The paths run the same arithmetic: the same greedy chain.
+    assert tokens["resident"] == tokens["step"] == tokens["graph"] == tokens["resident_step"], \
+        "resident, step, graph and per-token resident paths disagree"
     res_wall = spread(samples["resident"]["wall_ms"])
     step_wall = spread(samples["step"]["wall_ms"])
+    graph_wall = spread(samples["graph"]["wall_ms"])
+    rstep_wall = spread(samples["resident_step"]["wall_ms"])
     total_bytes = sum(step_bytes(prompt_len + 1 + i) for i in range(K))
     tok_s = K / (res_wall["median"] * 1e-3)
 
@@ -310,18 +335,32 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token):
         },
         "trials": {"count": trials, "order": "interleaved rotations, forwards then backwards",
                    "resident_ms": {k: round(v, 3) for k, v in res_wall.items()},
-                   "step_ms": {k: round(v, 3) for k, v in step_wall.items()}},
+                   "step_ms": {k: round(v, 3) for k, v in step_wall.items()},
+                   "graph_ms": {k: round(v, 3) for k, v in graph_wall.items()},
+                   "resident_step_ms": {k: round(v, 3) for k, v in rstep_wall.items()}},
         "step_hbm": {"achieved_gbs": round(total_bytes / (res_wall["median"] * 1e-3) / 1e9, 1),
                      "peak_gbs": HBM_PEAK_GBS, "bytes_per_token": round(total_bytes / K)},
         "device_tokens_per_s": round(K / (roof["avg_us"] * 1e-6), 2) if grid else None,
         "roofline": roof,
         "hbm_measured": {"read_gbs": round(read_gbs, 1), "copy_gbs": round(copy_gbs, 1),
                          "probe": "qd_probe_hbm: best of 5 passes over 2 GiB"},
+        # The per-token contract (one call per token, its 607,744-byte
+        # logits row copied to the host) on each of the engine's paths; the
+        # headline figure is the fastest, the resident kernel launched once
+        # per token.
         "executor_surface": {
-            "path": "qd_step per token: stream-ordered kernels + 607,744-byte logits copy to the host",
-            "tokens_per_s": round(K / (step_wall["median"] * 1e-3), 2),
-            "ms_per_token": round(step_wall["median"] / K, 4),
-            "dominant_kernel": roofline_hbm(dname, davg_us, davg_bytes),
+            "path": "qd_generate_resident with max_tokens 1 per token: one cooperative launch of the "
+                    "resident kernel + the logits copy to the host",
+            "tokens_per_s": round(K / (rstep_wall["median"] * 1e-3), 2),
+            "ms_per_token": round(rstep_wall["median"] / K, 4),
+            "step": {"path": "qd_step per token: stream-ordered kernels + the logits copy",
+                     "tokens_per_s": round(K / (step_wall["median"] * 1e-3), 2),
+                     "ms_per_token": round(step_wall["median"] / K, 4),
+                     "dominant_kernel": roofline_hbm(dname, davg_us, davg_bytes)},
+            "graph": {"path": "qd_step_graph per token: qd_step's kernels replayed from the slot's "
+                              "captured HIP graph + the logits copy",
+                      "tokens_per_s": round(K / (graph_wall["median"] * 1e-3), 2),
+                      "ms_per_token": round(graph_wall["median"] / K, 4)},
         },
         "cpu_baseline": cpu,
         "path": f"resident megakernel, {grid} workgroups" if grid else "stream-ordered kernels",

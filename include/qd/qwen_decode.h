@@ -262,6 +262,18 @@ QD_API qd_status qd_step(qd_engine *engine, uint32_t seq, uint32_t token_in,
                          float *logits_out, uint32_t *greedy_out,
                          float *top_logit);
 
+/* qd_step through a HIP graph: the slot's launch sequence (embedding, every
+ * layer, LM head, argmax: 147 kernels at 24 layers) is captured on the
+ * slot's first call and replayed by one hipGraphLaunch per token after that;
+ * the kernels read the position and token from the slot's device state, so
+ * one graph serves every step. Same arguments, semantics and results (bit
+ * for bit) as qd_step. Replaces the reference's HIP-Graph step
+ * (benchmarks/qwen_hip_graph.hpp:27-199, timed beside the resident path in
+ * docs/stateful-graph.md:636-650). */
+QD_API qd_status qd_step_graph(qd_engine *engine, uint32_t seq, uint32_t token_in,
+                               float *logits_out, uint32_t *greedy_out,
+                               float *top_logit);
+
 /* Prefill of n tokens from the slot's position; advances it by n. Writes the
  * last position's logits (nullable) and greedy token. Semantically n
  * sequential qd_step calls (the reference's prompt stack,

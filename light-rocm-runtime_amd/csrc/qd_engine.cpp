@@ -33,7 +33,7 @@
 
 namespace {
 
-constexpr uint32_t kAbiVersion = 3;
+constexpr uint32_t kAbiVersion = 4;
 constexpr int kLmHeadParts = 1024;  // LM-head workgroups = top-1 partials
 
 thread_local std::string g_error;
@@ -155,7 +155,7 @@ struct qd_engine {
   float *roles_slots = nullptr;             // hand-off slots
   size_t roles_slot_bytes = 0;
   uint32_t epoch = 0;                       // last launch epoch (1..4095)
-  uint32_t *resident_error = nullptr;       // [1]
+  uint32_t *resident_error = nullptr;       // [1 + kXcds]
   uint32_t spin_limit = qd::kResidentSpinLimit;
   int roles_grid = 0;                       // 0: resident path unavailable
   // Attention chunk geometry of both paths, attn_chunks(length, attn_parts, kAttnGrain):
@@ -187,17 +187,24 @@ struct qd_engine {
 
   qd::SeqState *h_states = nullptr;  // pinned [max_batch]
   uint32_t *h_tokens = nullptr;      // pinned [capacity]
+  uint32_t *h_error = nullptr;       // pinned [1]: a resident launch's error word
   std::vector<uint32_t> positions;   // host mirror of each slot's position
   bool loaded = false;
   qd_timing timing{};
+  // Per slot: qd_step's launch sequence captured as a HIP graph (nullptr
+  // until the slot's first qd_step_graph).
+  std::vector<hipGraphExec_t> step_graphs;
 
   // Teardown cannot report errors; a device fault was already reported by
   // the call that observed it.
   ~qd_engine() {
     if (stream) (void)hipStreamSynchronize(stream);
+    for (hipGraphExec_t g : step_graphs)
+      if (g) (void)hipGraphExecDestroy(g);
     for (void *p : allocs) (void)hipFree(p);
     if (h_states) (void)hipHostFree(h_states);
     if (h_tokens) (void)hipHostFree(h_tokens);
+    if (h_error) (void)hipHostFree(h_error);
     if (h_bt_out) (void)hipHostFree(h_bt_out);
     if (ev_begin) (void)hipEventDestroy(ev_begin);
     if (ev_end) (void)hipEventDestroy(ev_end);
@@ -344,6 +351,32 @@ struct qd_engine {
       check(qd::launch_layer(stream, layer_args(seq, l), m), "layer launch");
     check(qd::launch_tail(stream, tail_args(seq, out_logits, hist, out_tokens), m),
           "tail launch");
+  }
+  // The slot's qd_step launch sequence as an instantiated HIP graph,
+  // captured on first use. Every kernel of it reads the position and the
+  // token from the slot's device state and takes only fixed buffers and a
+  // fixed grid as arguments (the attention split is the engine's, fixed at
+  // creation), so one capture serves every later step of the slot. The
+  // graph holds kernel nodes only (no memset or copy nodes).
+  hipGraphExec_t step_graph(uint32_t seq) {
+    if (step_graphs.empty()) step_graphs.assign(B, nullptr);
+    if (step_graphs[seq]) return step_graphs[seq];
+    check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    hipGraph_t graph = nullptr;
+    try {
+      enqueue_step(seq, logits + seq * V, 0, nullptr);
+    } catch (...) {
+      (void)hipStreamEndCapture(stream, &graph);
+      if (graph) (void)hipGraphDestroy(graph);
+      throw;
+    }
+    check(hipStreamEndCapture(stream, &graph), "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    check(err, "hipGraphInstantiate");
+    step_graphs[seq] = exec;
+    return exec;
   }
 
   // Algorithmic bytes of one launch of `kernel` when the step attends over
@@ -599,8 +632,6 @@ struct qd_engine {
                              uint64_t *stage_ticks, uint64_t *trace = nullptr,
                              uint32_t trace_token = 0) {
     epoch = epoch % 4095u + 1u;
-    if (epoch == 1u)
-      check(hipMemsetAsync(top_pairs, 0, 4 * size_t(roles_grid) * 8, stream), "memset");
     qd::ResidentArgs ra{};
     ra.layer_ptrs = layer_ptrs_dev;
     ra.embed = embed;
@@ -637,26 +668,35 @@ struct qd_engine {
     ra.xcd_place = plan.xcd_place;
     ra.attn_parts = attn_parts;
     ra.weights_dtype = wdtype;
-    check(hipMemsetAsync(resident_error, 0, 4, stream), "memset");
-    // Every hand-off slot starts empty (all bits set).
-    check(hipMemsetAsync(roles_slots, 0xFF, roles_slot_bytes, stream), "memset");
+    // Error word and tickets zero, token 0's hand-off slots empty (all bits
+    // set), the tag arena zero when the epoch counter wrapped.
+    check(qd::launch_roles_prepare(stream, resident_error, roles_slots, roles_slot_bytes / (8 * L),
+                                   int(L), epoch == 1u ? top_pairs : nullptr, 4 * roles_grid),
+          "resident prepare");
     return qd::launch_roles(stream, ra, roles_grid);
   }
 
   // After a resident launch has completed (stream synchronised): turns the
   // kernel's error word into a status.
   void check_resident_error() {
-    uint32_t err = 0;
-    check(hipMemcpyAsync(&err, resident_error, 4, hipMemcpyDeviceToHost, stream), "D2H");
+    enqueue_resident_error();
     sync();
+    resident_status(*h_error);
+  }
+  // The error word's copy to h_error, stream ordered after the launch.
+  void enqueue_resident_error() {
+    check(hipMemcpyAsync(h_error, resident_error, 4, hipMemcpyDeviceToHost, stream), "D2H");
+  }
+  // Fails with the status that a nonzero error word names.
+  void resident_status(uint32_t err) {
     if (err & qd::kResidentPlanOverfill)
       fail(QD_ERROR_RUNTIME,
            "resident role plan gives a CU more weight units than it holds on chip (error word 0x%x)",
            err);
     if (err & qd::kResidentPlacement)
       fail(QD_ERROR_RUNTIME,
-           "resident kernel: a workgroup ran on another XCD than workgroup b %% %d, which the "
-           "role placement assumes (error word 0x%x)",
+           "resident kernel: an XCD received more than grid / %d workgroups, which the role "
+           "placement assumes (error word 0x%x)",
            qd::kXcds, err);
     if (err & qd::kResidentWaitGaveUp)
       fail(QD_ERROR_DEVICE_FAULT,
@@ -869,6 +909,8 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     check(hipHostMalloc(reinterpret_cast<void **>(&e->h_tokens), e->CAP * sizeof(uint32_t),
                         hipHostMallocDefault),
           "hipHostMalloc");
+    check(hipHostMalloc(reinterpret_cast<void **>(&e->h_error), sizeof(uint32_t), hipHostMallocDefault),
+          "hipHostMalloc");
     e->positions.assign(e->B, 0);
     e->build_rope_tables(c.rope_theta);
 
@@ -910,7 +952,7 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
                             qd::roles_slot_floats(int(e->H), int(e->I), int(e->NQ), int(e->NKV));
       e->roles_slots = e->alloc<float>(e->roles_slot_bytes / 4);
     }
-    e->resident_error = e->alloc<uint32_t>(1);
+    e->resident_error = e->alloc<uint32_t>(1 + qd::kXcds);
     {
       hipError_t err = hipSuccess;
       e->batch_scratch = qd::batch_scratch(c.device, &err);
@@ -1346,8 +1388,12 @@ qd_status qd_read_logits(qd_engine *e, uint32_t seq, float *out, size_t count) {
   });
 }
 
-qd_status qd_step(qd_engine *e, uint32_t seq, uint32_t token, float *logits_out, uint32_t *greedy,
-                  float *top_logit) {
+namespace {
+// qd_step and qd_step_graph: the slot's state is written (a copy from
+// pinned host memory), the step runs as launches or as the slot's graph,
+// then the state and (optionally) the logits come back.
+qd_status step_common(qd_engine *e, uint32_t seq, uint32_t token, float *logits_out, uint32_t *greedy,
+                      float *top_logit, bool graph) {
   return guard([&] {
     if (!e) fail(QD_ERROR_INVALID_ARGUMENT, "null engine");
     e->check_seq(seq);
@@ -1356,9 +1402,13 @@ qd_status qd_step(qd_engine *e, uint32_t seq, uint32_t token, float *logits_out,
     if (e->positions[seq] >= e->CAP)
       fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full (capacity %zu)", seq, e->CAP);
     e->set_device();
-    e->push_state(seq, token, qd::kModeStep, UINT32_MAX, 0);
     float *dev_logits = e->logits + seq * e->V;
-    e->enqueue_step(seq, dev_logits, 0, nullptr);
+    hipGraphExec_t g = graph ? e->step_graph(seq) : nullptr;
+    e->push_state(seq, token, qd::kModeStep, UINT32_MAX, 0);
+    if (g)
+      check(hipGraphLaunch(g, e->stream), "hipGraphLaunch");
+    else
+      e->enqueue_step(seq, dev_logits, 0, nullptr);
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState),
                          hipMemcpyDeviceToHost, e->stream), "D2H");
     if (logits_out)
@@ -1368,6 +1418,17 @@ qd_status qd_step(qd_engine *e, uint32_t seq, uint32_t token, float *logits_out,
     if (greedy) *greedy = e->h_states[seq].token;
     if (top_logit) *top_logit = e->h_states[seq].top_logit;
   });
+}
+}  // namespace
+
+qd_status qd_step(qd_engine *e, uint32_t seq, uint32_t token, float *logits_out, uint32_t *greedy,
+                  float *top_logit) {
+  return step_common(e, seq, token, logits_out, greedy, top_logit, false);
+}
+
+qd_status qd_step_graph(qd_engine *e, uint32_t seq, uint32_t token, float *logits_out, uint32_t *greedy,
+                        float *top_logit) {
+  return step_common(e, seq, token, logits_out, greedy, top_logit, true);
 }
 
 namespace {
@@ -1677,11 +1738,12 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
       hist = e->history;
       use_hist = 1;
     }
-    e->push_state(seq, first_token, qd::kModeGenerate, eos, max_tokens);
     qd::RolePlan plan{};
     bool resident = e->resident_fits(max_tokens) && e->resident_plan(e->positions[seq] + max_tokens, &plan);
     check(hipEventRecord(e->ev_begin, e->stream), "hipEventRecord");
     if (resident) {
+      // The kernel takes its start from the launch arguments and writes the
+      // slot's whole state when it ends.
       const hipError_t err =
           e->launch_resident(plan, seq, first_token, max_tokens, eos, hist, use_hist, nullptr);
       if (err != hipSuccess) {
@@ -1689,19 +1751,30 @@ qd_status qd_generate_resident(qd_engine *e, uint32_t seq, uint32_t first_token,
         resident = false;
       }
     }
-    if (!resident)
+    if (!resident) {
+      e->push_state(seq, first_token, qd::kModeGenerate, eos, max_tokens);
       for (uint32_t t = 0; t < max_tokens; ++t) e->enqueue_step(seq, hist, use_hist, e->tokens_dev);
+    }
     check(hipEventRecord(e->ev_end, e->stream), "hipEventRecord");
+    // One synchronisation for the state, the error word and the tokens (all
+    // max_tokens words); a one-token generation's logits row comes along.
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState), hipMemcpyDeviceToHost,
                          e->stream), "D2H");
+    if (resident) e->enqueue_resident_error();
+    check(hipMemcpyAsync(e->h_tokens, e->tokens_dev, size_t(max_tokens) * 4, hipMemcpyDeviceToHost,
+                         e->stream), "D2H");
+    const bool row_now = all_logits && max_tokens == 1;
+    if (row_now)
+      check(hipMemcpyAsync(all_logits, e->history, e->V * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
     e->sync();
-    if (resident) e->check_resident_error();
+    if (resident) e->resident_status(*e->h_error);
     const qd::SeqState &s = e->h_states[seq];
-    const uint32_t n = s.generated;
-    check(hipMemcpyAsync(out_tokens, e->tokens_dev, size_t(n) * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
-    if (all_logits && n)
+    const uint32_t n = std::min(s.generated, max_tokens);
+    std::memcpy(out_tokens, e->h_tokens, size_t(n) * 4);
+    if (all_logits && n && !row_now) {
       check(hipMemcpyAsync(all_logits, e->history, size_t(n) * e->V * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
-    e->sync();
+      e->sync();
+    }
     float ms = 0.f;
     check(hipEventElapsedTime(&ms, e->ev_begin, e->ev_end), "hipEventElapsedTime");
     e->timing.total_us = ms * 1000.0;

@@ -29,7 +29,11 @@ struct RolePlan {
   int group_cus[3];     // QKV, attention and O CUs per KV group (each role has nkv times as many)
   int xcd_place;        // 1: KV group g's QKV, attention and O CUs all run on XCD g
 };
-// XCDs of the device; workgroup b of a launch runs on XCD b % kXcds.
+// XCDs of the device. The dispatcher deals a launch's workgroups to the
+// XCDs round-robin, but the XCD it starts from is not fixed (after HIP graph
+// replays on a stream, workgroup 0 of the next launch has run on another XCD
+// than 0), so the resident kernel takes each workgroup's placement position
+// from the XCD it runs on.
 constexpr int kXcds = 8;
 
 // Bits of the kernel's error word (zero at launch). A CU that raises one
@@ -37,7 +41,7 @@ constexpr int kXcds = 8;
 // every workgroup exits.
 constexpr uint32_t kResidentWaitGaveUp = 1u;    // a hand-off poll exhausted its spin limit
 constexpr uint32_t kResidentPlanOverfill = 2u;  // the host plan gave a CU more units than it holds
-constexpr uint32_t kResidentPlacement = 4u;     // a workgroup ran on another XCD than the plan placed it on
+constexpr uint32_t kResidentPlacement = 4u;     // an XCD received more workgroups than grid / kXcds
 // Polls before a hand-off wait gives up (several milliseconds; a healthy
 // hand-off takes a few microseconds).
 constexpr uint32_t kResidentSpinLimit = 1u << 21;
@@ -58,7 +62,8 @@ struct ResidentArgs {
   float *logits;                // [vocab] or [max_tokens][vocab]
   uint32_t *out_tokens;         // [max_tokens]
   SeqState *st;
-  uint32_t *error;              // zero at launch; kResident* bits
+  uint32_t *error;              // [1 + kXcds], zero at launch: kResident* bits, then each
+                                //   XCD's count of workgroups that have taken a position
   uint64_t *stage_ticks;        // nullptr, or [kResidentStages] 100 MHz ticks
   uint64_t *trace;              // nullptr, or [grid][layers + 1][kResidentStages]
                                 //   100 MHz timestamps of token trace_token
@@ -113,6 +118,12 @@ int device_cu_count(int device);
 bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int max_length,
                 RolePlan *plan);
 hipError_t launch_roles(hipStream_t s, const ResidentArgs &args, int grid);
+// Prepares a resident launch in one dispatch: error[0 .. kXcds] zero, the
+// parity-0 block ([slot_floats] floats at slots + 2 * l * slot_floats) of
+// each of `layers` layers all kSlotEmpty, and, when top is not null, its
+// top_pairs (value, tag) pairs zero.
+hipError_t launch_roles_prepare(hipStream_t s, uint32_t *error, float *slots, size_t slot_floats,
+                               int layers, void *top, int top_pairs);
 // Largest co-resident grid of the role kernel for decoder matrices stored as
 // `weights_dtype` (kWeights*) on `device` (0 if the query fails).
 int roles_max_grid(int device, int weights_dtype);

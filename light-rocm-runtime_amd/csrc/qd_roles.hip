@@ -504,9 +504,9 @@ struct Clock {
   // Timeline of the traced token: row[l][stage] for this CU's role stages,
   // its sub-phases in the last three stage slots, and the LM head / argmax
   // stages.
-  __device__ void flush_trace(uint64_t *trace, int layers, int role) const {
+  __device__ void flush_trace(uint64_t *trace, int wg, int layers, int role) const {
     if (!kProfile || !trace || threadIdx.x != 0) return;
-    uint64_t *row = trace + static_cast<size_t>(blockIdx.x) * (layers + 1) * kResidentStages;
+    uint64_t *row = trace + static_cast<size_t>(wg) * (layers + 1) * kResidentStages;
     for (int l = 0; l < layers && l < kMaxTraceLayers; ++l) {
       const uint64_t *st = lds->stamps + kStampsPerLayer * l;
       row[l * kResidentStages + 2 * role] = st[0];
@@ -930,19 +930,20 @@ struct Roles {
   const ResidentArgs &a;
   Common &cm;
   unsigned char *region;
-  int rank, nrole, lane, wv, grid;
+  int rank, nrole, wg, lane, wv, grid;  // wg: placement position (the trace row)
   uint32_t per_token;
   TagVec ttop;
   Clock<kProfile> clock;
   uint32_t token, generated = 0, stop_reason = 0;
   float top = 0.f;
 
-  __device__ Roles(const ResidentArgs &args, unsigned char *lds, int rank_, int nrole_)
+  __device__ Roles(const ResidentArgs &args, unsigned char *lds, int rank_, int nrole_, int wg_)
       : a(args),
         cm(*reinterpret_cast<Common *>(lds)),
         region(lds + kRegionOffset),
         rank(rank_),
         nrole(nrole_),
+        wg(wg_),
         lane(lane_id()),
         wv(wave_u()),
         grid(gridDim.x),
@@ -1105,7 +1106,7 @@ struct Roles {
       if (defer_first) pre_lds(0, position + 1);
       pre_regs(0);  // register share of layer 0 for the next token
       if (!argmax(t)) return;
-      if (traced) clock.flush_trace(a.trace, a.layers, role);
+      if (traced) clock.flush_trace(a.trace, wg, a.layers, role);
       generated = t + 1;
       if (blockIdx.x == 0 && threadIdx.x == 0)
         *(__attribute__((address_space(1))) uint32_t *)(a.out_tokens + t) = token;
@@ -1887,7 +1888,7 @@ struct Roles {
 // Each role's loop is its own (non-inlined) function so the register
 // allocator sizes each role separately instead of one body holding all five.
 template <int H, int I, int NQ, int NKV, bool kProfile, typename W, int kRole>
-__device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank, int nrole) {
+__device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank, int nrole, int wg) {
   // The launch arguments, copied with scalar loads from the kernel's
   // argument segment (whose address the kernel passes: a callee has no
   // kernarg segment pointer of its own, and the address of the kernel's
@@ -1910,7 +1911,8 @@ __device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank
     for (size_t i = 0; i < sizeof(ResidentArgs) / 4; ++i) dst[i] = src[i];
   }
   Roles<H, I, NQ, NKV, kProfile, W> r(a, roles_lds, __builtin_amdgcn_readfirstlane(rank),
-                                   __builtin_amdgcn_readfirstlane(nrole));
+                                   __builtin_amdgcn_readfirstlane(nrole),
+                                   __builtin_amdgcn_readfirstlane(wg));
   if constexpr (kRole == kRoleQkv) r.run_qkv();
   if constexpr (kRole == kRoleAttn) r.run_attn();
   if constexpr (kRole == kRoleO) r.run_o();
@@ -1946,32 +1948,45 @@ __device__ __forceinline__ uint32_t xcc_id() {
 template <int H, int I, int NQ, int NKV, bool kProfile, typename W>
 __global__ __launch_bounds__(kT, 1) void roles_kernel(ResidentArgs a) {
   const void *kernarg = (const void *)__builtin_amdgcn_kernarg_segment_ptr();
-  // A workgroup placed for an XCD it does not run on stops (its waiting
-  // peers give up): the intra-XCD hand-offs rely on the placement.
-  if (a.xcd_place && xcc_id() != blockIdx.x % kXcds) {
-    if (threadIdx.x == 0) atomicOr(a.error, kResidentPlacement);
-    return;
+  // With XCD placement a workgroup's position is i * kXcds + x, x the XCD it
+  // runs on and i its arrival order there (a ticket from a.error[1 + x]),
+  // whatever XCD the dispatcher started the launch from. An XCD dealt more
+  // than grid / kXcds workgroups stops the extra ones (their waiting peers
+  // give up): the intra-XCD hand-offs rely on the placement.
+  int wg = blockIdx.x;
+  if (a.xcd_place) {
+    uint32_t *ticket = reinterpret_cast<uint32_t *>(roles_lds);
+    const uint32_t x = xcc_id();
+    if (threadIdx.x == 0) *ticket = x < kXcds ? atomicAdd(a.error + 1 + x, 1u) : ~0u;
+    __syncthreads();
+    const uint32_t i = *ticket;
+    __syncthreads();  // every wave has read the ticket before the LDS is reused
+    if (i >= gridDim.x / kXcds) {
+      if (threadIdx.x == 0) atomicOr(a.error, kResidentPlacement);
+      return;
+    }
+    wg = static_cast<int>(i * kXcds + x);
   }
-  const int b = placement(a, blockIdx.x);
+  const int b = placement(a, wg);
   int role = 0;
   while (role < kRoleCount - 1 && b >= a.role_end[role]) ++role;
   const int rbeg = role ? a.role_end[role - 1] : 0;
   const int rank = b - rbeg, nrole = a.role_end[role] - rbeg;
   switch (role) {
     case kRoleQkv:
-      run_role<H, I, NQ, NKV, kProfile, W, kRoleQkv>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleQkv>(kernarg, rank, nrole, wg);
       break;
     case kRoleAttn:
-      run_role<H, I, NQ, NKV, kProfile, W, kRoleAttn>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleAttn>(kernarg, rank, nrole, wg);
       break;
     case kRoleO:
-      run_role<H, I, NQ, NKV, kProfile, W, kRoleO>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleO>(kernarg, rank, nrole, wg);
       break;
     case kRoleGate:
-      run_role<H, I, NQ, NKV, kProfile, W, kRoleGate>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleGate>(kernarg, rank, nrole, wg);
       break;
     default:
-      run_role<H, I, NQ, NKV, kProfile, W, kRoleDown>(kernarg, rank, nrole);
+      run_role<H, I, NQ, NKV, kProfile, W, kRoleDown>(kernarg, rank, nrole, wg);
       break;
   }
 }
@@ -1989,6 +2004,23 @@ const void *roles_fn(bool profile, int weights_dtype) {
     case kWeightsF16: return roles_fn_as<F16>(profile);
     default: return roles_fn_as<float>(profile);
   }
+}
+
+// What a resident launch expects at its start, in one dispatch: the error
+// word and the XCD tickets zero, and parity 0's block of every layer's
+// hand-off slots empty (token 0's). Parity 1's blocks need no clearing:
+// token 0's writers clear their slots there before any CU starts token 1.
+// With `top`, the argmax tag arena is zeroed too.
+__global__ __launch_bounds__(256) void roles_prepare_kernel(uint32_t *error, uint4 *slots,
+                                                            uint32_t block_u4, uint2 *top,
+                                                            uint32_t top_pairs) {
+  const uint32_t t = threadIdx.x + blockIdx.x * blockDim.x, n = gridDim.x * blockDim.x;
+  if (blockIdx.y == 0) {
+    if (t < 1 + kXcds) error[t] = 0u;
+    for (uint32_t i = t; i < top_pairs; i += n) top[i] = make_uint2(0u, 0u);
+  }
+  uint4 *blk = slots + size_t(blockIdx.y) * 2 * block_u4;
+  for (uint32_t i = t; i < block_u4; i += n) blk[i] = make_uint4(kSlotEmpty, kSlotEmpty, kSlotEmpty, kSlotEmpty);
 }
 
 }  // namespace
@@ -2089,6 +2121,19 @@ hipError_t launch_roles(hipStream_t s, const ResidentArgs &args, int grid) {
     return hipErrorInvalidValue;
   return hipLaunchCooperativeKernel(roles_fn(args.stage_ticks || args.trace, args.weights_dtype), dim3(grid), dim3(kT),
                                     params, 0, s);
+}
+
+hipError_t launch_roles_prepare(hipStream_t s, uint32_t *error, float *slots, size_t slot_floats,
+                               int layers, void *top, int top_pairs) {
+  if (slot_floats % 4 != 0 || reinterpret_cast<uintptr_t>(slots) % 16 != 0 || layers < 1 ||
+      layers > 65535)
+    return hipErrorInvalidValue;
+  const uint32_t block_u4 = static_cast<uint32_t>(slot_floats / 4);
+  const dim3 grid((block_u4 + 4 * 256 - 1) / (4 * 256), static_cast<uint32_t>(layers));
+  hipLaunchKernelGGL(roles_prepare_kernel, grid, dim3(256), 0, s, error,
+                     reinterpret_cast<uint4 *>(slots), block_u4, static_cast<uint2 *>(top),
+                     top ? static_cast<uint32_t>(top_pairs) : 0u);
+  return hipGetLastError();
 }
 
 int device_cu_count(int device) {

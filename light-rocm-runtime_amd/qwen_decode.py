@@ -91,6 +91,7 @@ _SIGNATURES = {
     "qd_tail": (C.c_int, [_E, C.c_uint32, _F, _U, _F]),
     "qd_read_logits": (C.c_int, [_E, C.c_uint32, _F, C.c_size_t]),
     "qd_step": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F, _U, _F]),
+    "qd_step_graph": (C.c_int, [_E, C.c_uint32, C.c_uint32, _F, _U, _F]),
     "qd_prefill": (C.c_int, [_E, C.c_uint32, _U, C.c_uint32, _F, _U, _F]),
     "qd_step_batch": (C.c_int, [_E, C.c_uint32, _U, _U, _F, _U]),
     "qd_step_batch_noalloc": (C.c_int, [_E, C.c_uint32, _U, _U, _F, _U]),
@@ -309,6 +310,14 @@ class Engine:
         tok = C.c_uint32()
         top = C.c_float()
         _check(lib().qd_step(self.handle, seq, token, _f(logits), C.byref(tok), C.byref(top)))
+        return int(tok.value), float(top.value), logits
+
+    def step_graph(self, seq: int, token: int, want_logits: bool = True):
+        """qd_step replayed from the slot's captured HIP graph."""
+        logits = np.empty(self.config.vocab, np.float32) if want_logits else None
+        tok = C.c_uint32()
+        top = C.c_float()
+        _check(lib().qd_step_graph(self.handle, seq, token, _f(logits), C.byref(tok), C.byref(top)))
         return int(tok.value), float(top.value), logits
 
     def prefill(self, seq: int, tokens, want_logits: bool = True):

@@ -5,7 +5,8 @@ role, when its input arrived, its three sub-phase stamps and when it
 published its outputs. Each figure is the median over layers 4..19 of the
 role's per-CU median, in microseconds from the layer's first QKV input. Also
 printed: the layer period and the LM head's input-to-done time, overall and
-per XCD (workgroup b runs on XCD b % 8).
+per XCD (trace row w is the workgroup placed at position w, which runs on
+XCD w % 8).
 
     python3 light-rocm-runtime_amd/resident_timeline.py --context 512
     python3 light-rocm-runtime_amd/resident_timeline.py --context 4096 --save trace.npy

@@ -32,7 +32,7 @@ def test_status_strings_match_lr_status_values():
     expected = ["success", "invalid argument", "not initialized", "already initialized",
                 "not supported", "runtime error", "device fault"]
     assert [qd.status_string(i) for i in range(7)] == expected
-    assert qd.lib().qd_abi_version() == 3
+    assert qd.lib().qd_abi_version() == 4
 
 
 def test_device_count_is_callable():

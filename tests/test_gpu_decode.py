@@ -305,6 +305,45 @@ def test_resident_multi_window_beyond_4096_matches_stream_and_oracle(full, strea
     long_context_generation(full, stream_full, 4090, 40, 777, "resident 4091..4130 (two windows)")
 
 
+def test_resident_step_and_graph_agree(full):
+    """The reference's three-way cross-check of one greedy chain
+    (benchmarks/qwen_stateful_graph.cpp:1619-1746): the resident megakernel
+    (qd_generate_resident), the per-token launches (qd_step) and the same
+    launches replayed from a captured HIP graph (qd_step_graph, one graph
+    per slot, benchmarks/qwen_hip_graph.hpp:27-199) give the same tokens,
+    logits, decode state and K/V rows, bit for bit. Every graph replay is
+    checked against the eager step that ran just before it, with the
+    program's own eager work and host synchronisations in between."""
+    eng, _ = full
+    prompt = qo.fill_tokens(11, 1, PROMPT_STREAM + 9, FULL.vocab)
+    steps = 8
+    say("resident vs qd_step vs qd_step_graph, 8 greedy tokens")
+    firsts = []
+    for slot in (0, 1, 2):
+        eng.kv_reset(slot, 0)
+        t, _, _ = eng.prefill(slot, prompt, want_logits=False)
+        firsts.append(t)
+    assert firsts[0] == firsts[1] == firsts[2]
+    rtoks, _, rlogits = eng.generate(0, firsts[0], steps, want_logits=True)
+    fs = fg = firsts[0]
+    for i in range(steps):
+        ts, tops, ls = eng.step(1, fs)
+        tg, topg, lg = eng.step_graph(2, fg)
+        assert ts == tg == int(rtoks[i]) and tops == topg, i
+        assert np.array_equal(ls, lg) and np.array_equal(ls, rlogits[i]), i
+        assert eng.decode_state(1).token_position == eng.decode_state(2).token_position == len(prompt) + i + 1
+        fs, fg = ts, tg
+    assert_kv_equal(eng, eng, 0, 1, len(prompt), steps, "resident vs step KV")
+    assert_kv_equal(eng, eng, 1, 2, len(prompt), steps, "step vs graph KV")
+    assert np.array_equal(eng.read_logits(2), rlogits[-1])
+    # A resident launch right after graph replays on the same stream: the
+    # dispatcher may start it from another XCD than 0, and the kernel's
+    # placement follows the XCD each workgroup runs on.
+    eng.kv_reset(0, len(prompt))
+    rtoks2, _, rlogits2 = eng.generate(0, firsts[0], steps, want_logits=True)
+    assert np.array_equal(rtoks2, rtoks) and np.array_equal(rlogits2, rlogits)
+
+
 def test_layer_by_layer_decode_equals_step(full):
     """The reference driver's per-token loop through the C ABI
     (benchmarks/triton_mini_decoder_layer.cpp:1051-1068): the embedding row
