@@ -16,8 +16,15 @@ Workloads (synthetic random-init weights):
            tail, on the resident kernel, timed against the FP32 default line's
            engine (interleaved).
   f16      the same with IEEE FP16 decoder matrices.
+  layer    config 1: one decoder layer's decode step at KV context 128
+           (weights seed 0), cycling over 8 synthetic layers (8 x 59.6 MB,
+           more than the 256 MB last-level cache) so every step streams its
+           weights from HBM. One "step" = one token through the 8 layers on
+           the resident kernel (small-vocabulary tail); value = layer steps/s.
+           qd_layer_decode (one layer per call, stream kernels, context
+           exactly 128) is timed beside it.
 
-  python bench.py [--workload decode|long|batch16|prefill|bf16|f16] [--steps K]
+  python bench.py [--workload decode|long|batch16|prefill|bf16|f16|layer] [--steps K]
                   [--warmup W] [--trials T] [--gpus 1] [--no-cpu]
 """
 import argparse
@@ -530,6 +537,133 @@ def run_batch16(K, W, no_cpu, trials):
     }
 
 
+# one decoder layer, one decode step at KV context 128.
+LAYER_COPIES = 8          # layers cycled per token: 8 x 59.6 MB > the 256 MB MALL
+LAYER_CONTEXT = 128
+LAYER_SEED = 0
+LAYER_VOCAB = 1024        # the resident launch's tail over a small vocabulary
+# Algorithmic bytes of one layer step attending over L positions: the
+# layer's FP32 weights, biases and norms + its K/V reads (1,024 L).
+LAYER_WEIGHT_BYTES = 59_649_536
+
+
+def layer_step_bytes(length: int) -> int:
+    return LAYER_WEIGHT_BYTES + 1024 * length
+
+
+def cpu_layer_baseline(budget_s=10.0, max_steps=20000):
+    """The CPU oracle's single layer step (FP32, OpenMP) at position 128,
+    cycling over LAYER_COPIES layers of the seed-0 model as the GPU line does
+    (so the weights stream from DRAM rather than sit in the host's caches),
+    as many steps as fit the budget."""
+    import qwen_oracle as qo
+
+    model = qo.Model(qo.ModelShape(layers=LAYER_COPIES, vocab=LAYER_VOCAB))
+    model.fill_synthetic(LAYER_SEED)
+    cache = qo.Cache(model, LAYER_CONTEXT + 2)
+    for layer in range(LAYER_COPIES):
+        cache.layer(layer, False)[:LAYER_CONTEXT] = 0.01
+        cache.layer(layer, True)[:LAYER_CONTEXT] = 0.01
+    hidden = np.full(896, 0.01, np.float32)
+    for layer in range(LAYER_COPIES):  # warm threads
+        cache.layer_step(layer, hidden, LAYER_CONTEXT)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        cache.layer_step(steps % LAYER_COPIES, hidden, LAYER_CONTEXT)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or steps >= max_steps:
+            break
+    model.close()
+    return steps, el, qo.threads()
+
+
+def run_layer(K, W, no_cpu, trials):
+    log(f"engine create: {LAYER_COPIES} synthetic layers (seed {LAYER_SEED}), vocab {LAYER_VOCAB}")
+    eng = qd.Engine(layers=LAYER_COPIES, vocab=LAYER_VOCAB, capacity=LAYER_CONTEXT + max(K, W) + 8,
+                    max_batch=1)
+    eng.load_synthetic(LAYER_SEED)
+    grid = eng.resident_grid()
+    first = 1
+
+    # "resident": K tokens in one launch, each through the 8 layers
+    # (contexts 129 .. 128 + K), timed by HIP events on the engine stream.
+    def resident():
+        eng.kv_reset(0, LAYER_CONTEXT)
+        toks, reason, _ = eng.generate(0, first, K)
+        assert len(toks) == K, (len(toks), reason)
+        return eng.last_timing().total_us
+
+    # "layer": qd_layer_decode, one layer per call at context exactly 128
+    # (the query at position 128), cycling over the layers.
+    def layer_calls():
+        eng.sync()
+        t0 = time.perf_counter()
+        for i in range(K * LAYER_COPIES):
+            eng.layer_decode(0, i % LAYER_COPIES, 1, LAYER_CONTEXT + 1)
+        eng.sync()
+        return (time.perf_counter() - t0) * 1e6
+
+    if W:
+        log(f"warmup {W} tokens per path")
+        eng.kv_reset(0, LAYER_CONTEXT)
+        eng.generate(0, first, W)
+        for i in range(W * LAYER_COPIES):
+            eng.layer_decode(0, i % LAYER_COPIES, 1, LAYER_CONTEXT + 1)
+    samples = {"resident": [], "layer": []}
+    paths = {"resident": resident, "layer": layer_calls}
+    log(f"timed: {trials} interleaved trials x {K} tokens x {LAYER_COPIES} layers per path")
+    for t in range(trials):
+        for name in trial_orders(list(paths))[t % 4]:
+            samples[name].append(paths[name]())
+    eng.close()
+    steps = K * LAYER_COPIES
+    res_us = spread(samples["resident"])
+    lay_us = spread(samples["layer"])
+    res_step_us = res_us["median"] / steps
+    lay_step_us = lay_us["median"] / steps
+    # Bytes of the resident launch's layer steps (the small tail excluded:
+    # the figure is a floor on what the layers alone achieve).
+    res_bytes = LAYER_COPIES * sum(layer_step_bytes(LAYER_CONTEXT + 1 + i) for i in range(K))
+    roof = roofline_hbm("roles_kernel", res_us["median"], float(res_bytes))
+    roof["per"] = f"one launch: {K} tokens x {LAYER_COPIES} layer steps"
+    lay_gbs = layer_step_bytes(LAYER_CONTEXT + 1) / (lay_step_us * 1e-6) / 1e9
+    cpu = None
+    if not no_cpu:
+        n, el, cores = cpu_layer_baseline()
+        cpu = {"value": round(n / el, 2), "unit": "layer-steps/s", "cores": cores, "kind": "port",
+               "sample": f"{n} single-layer steps at position 128 cycling over {LAYER_COPIES} layers "
+                         f"(synthetic cached KV), oracle/libqwen_oracle.so FP32 OpenMP"}
+    return {
+        "metric": "single decoder layer decode steps/s (Qwen2 layer shape FP32, KV context 128) "
+                  "+ % HBM roofline",
+        "value": round(1e6 / res_step_us, 1),
+        "unit": "layer-steps/s",
+        "ms_per_step": round(res_us["median"] / K / 1e3, 4),
+        "higher_is_better": True,
+        "dtype": "f32",
+        "data": f"synthetic: random-init N(0,0.02) weights / N(0,0.01) biases, seed {LAYER_SEED}; "
+                f"{LAYER_COPIES} distinct layers; zero K/V context",
+        "config": {
+            "workload": "BASELINE config 1: one Qwen2 decoder layer (hidden 896, 14/2 heads, "
+                        "intermediate 4864) decode step at KV context 128, batch 1, cycling over "
+                        f"{LAYER_COPIES} weight copies",
+            "batch": 1, "context": f"{LAYER_CONTEXT + 1}..{LAYER_CONTEXT + K}", "layers": LAYER_COPIES,
+            "hidden": 896, "vocab": LAYER_VOCAB,
+        },
+        "us_per_layer_step": round(res_step_us, 3),
+        "trials": {"count": trials, "resident_us": {k: round(v, 2) for k, v in res_us.items()},
+                   "layer_decode_us": {k: round(v, 2) for k, v in lay_us.items()}},
+        "roofline": roof,
+        "layer_decode": {"path": "qd_layer_decode per layer: stream-ordered kernels, context 128",
+                         "us_per_layer_step": round(lay_step_us, 3),
+                         "achieved_gbs": round(lay_gbs, 1),
+                         "frac": round(lay_gbs / HBM_PEAK_GBS, 4)},
+        "cpu_baseline": cpu,
+        "path": f"resident megakernel, {grid} workgroups" if grid else "stream-ordered kernels",
+    }
+
+
 def run_prefill(K, W, no_cpu, trials):
     prompt = stream_tokens(PROMPT, PREFILL_SEED, PROMPT_STREAM, VOCAB)
     log("engine create + synthetic weights (seed 4)")
@@ -619,7 +753,7 @@ def copy_probe(mib: int):
 
 
 DEFAULTS = {"decode": (64, 8), "long": (32, 4), "batch16": (32, 4), "prefill": (20, 3), "bf16": (64, 8),
-            "f16": (64, 8)}
+            "f16": (64, 8), "layer": (16, 4)}
 
 
 def main():
@@ -643,7 +777,7 @@ def main():
     if K <= 0:
         sys.exit("--steps must be positive")
     run = {"decode": run_decode, "long": run_long, "batch16": run_batch16,
-           "prefill": run_prefill, "bf16": run_bf16, "f16": run_f16}[args.workload]
+           "prefill": run_prefill, "bf16": run_bf16, "f16": run_f16, "layer": run_layer}[args.workload]
     out = run(K, W, args.no_cpu, max(1, args.trials))
     if args.copy_probe:
         copy_probe(args.copy_probe)

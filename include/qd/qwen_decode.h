@@ -55,8 +55,8 @@ typedef enum qd_stop_reason {
  * persistent path hard-codes (benchmarks/qwen_stateful_graph.cpp:379,818). */
 typedef struct qd_config {
   uint32_t hidden;       /* 896 */
-  uint32_t heads;        /* 14 query heads */
-  uint32_t kv_heads;     /* 2; heads / kv_heads at most 8 */
+  uint32_t heads;        /* 14 query heads (the only supported value) */
+  uint32_t kv_heads;     /* 2 (the only supported value with 14 heads) */
   uint32_t head_dim;     /* 64 (the only supported value) */
   uint32_t intermediate; /* 4864 */
   uint32_t vocab;        /* 151936 */

@@ -827,8 +827,8 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
                              static_cast<int>(c.heads), static_cast<int>(c.kv_heads),
                              static_cast<int>(c.head_dim)))
       fail(QD_ERROR_NOT_SUPPORTED,
-           "unsupported shape: kernels are built for hidden 896, intermediate 4864, "
-           "head_dim 64, heads*head_dim == hidden");
+           "unsupported shape: kernels are built for hidden 896, intermediate 4864 and "
+           "14 query heads over 2 KV heads of head_dim 64");
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
       fail(QD_ERROR_NOT_SUPPORTED, "no HIP device visible");

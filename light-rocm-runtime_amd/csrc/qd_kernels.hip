@@ -528,9 +528,10 @@ const char *kernel_name(int id) {
 
 bool shape_supported(int hidden, int intermediate, int heads, int kv_heads,
                      int head_dim) {
-  return hidden == 896 && intermediate == 4864 && head_dim == kHeadDim &&
-         kv_heads > 0 && heads % kv_heads == 0 && heads / kv_heads <= kAttnMaxGroup &&
-         heads * head_dim == 896;
+  // The Qwen2.5-0.5B layer, the one shape whose parity the kernels are
+  // tested at: 14 query heads over 2 KV heads of 64.
+  return hidden == 896 && intermediate == 4864 && head_dim == kHeadDim && heads == 14 &&
+         kv_heads == 2;
 }
 
 namespace {
@@ -588,14 +589,9 @@ hipError_t launch_layer_as(hipStream_t s, const LayerLaunch &p, Marker *m) {
   {
     Scope scope(m, kKOproj);
     const dim3 grid((H / 2 + kWavesPerBlock - 1) / kWavesPerBlock);
-    // The KV-group counts of QD / 64 query heads (shape_supported).
-    switch (p.nkv) {
-      case 1: oproj_residual_kernel<H, QD, 1, W><<<grid, kBlock, 0, s>>>(p.attn, wo, p.st, p.hidden); break;
-      case 2: oproj_residual_kernel<H, QD, 2, W><<<grid, kBlock, 0, s>>>(p.attn, wo, p.st, p.hidden); break;
-      case 7: oproj_residual_kernel<H, QD, 7, W><<<grid, kBlock, 0, s>>>(p.attn, wo, p.st, p.hidden); break;
-      case 14: oproj_residual_kernel<H, QD, 14, W><<<grid, kBlock, 0, s>>>(p.attn, wo, p.st, p.hidden); break;
-      default: return hipErrorInvalidValue;
-    }
+    // Two KV groups (shape_supported).
+    if (p.nkv != 2) return hipErrorInvalidValue;
+    oproj_residual_kernel<H, QD, 2, W><<<grid, kBlock, 0, s>>>(p.attn, wo, p.st, p.hidden);
   }
   {
     Scope scope(m, kKGateUp);

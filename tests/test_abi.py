@@ -46,6 +46,11 @@ def test_engine_create_validates_before_touching_a_device():
     with pytest.raises(qd.QdError) as e:
         qd.Engine(hidden=1024, heads=16)
     assert e.value.status == qd.NOT_SUPPORTED
+    # Only the tested attention shape, 14 query heads over 2 KV heads.
+    for kv_heads in (7, 14):
+        with pytest.raises(qd.QdError) as e:
+            qd.Engine(kv_heads=kv_heads)
+        assert e.value.status == qd.NOT_SUPPORTED, kv_heads
     with pytest.raises(qd.QdError) as e:
         qd.Engine(capacity=0)
     assert e.value.status == qd.INVALID_ARGUMENT

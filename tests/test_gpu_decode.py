@@ -52,7 +52,7 @@ def check_logits(gpu_tok, gpu_logits, ref_tok, ref_logits, what):
 # ---- shared full-size model ------------------------------------------------------
 
 FULL = qo.QWEN25_05B
-CAPACITY = 4200
+CAPACITY = 5200
 
 
 @pytest.fixture(scope="module")
@@ -300,9 +300,16 @@ def test_resident_config3_context_4096_matches_stream_and_oracle(full, stream_fu
 
 def test_resident_multi_window_beyond_4096_matches_stream_and_oracle(full, stream_full):
     """Across context 4096 (4091..4130; 464-position chunks, 9 per KV head,
-    on a 256-CU MI355X), each chunk walked in LDS windows of at most 256
-    positions."""
+    on a 256-CU MI355X), each chunk walked in two windows: 256 positions in
+    LDS, then the rest in the waves' registers."""
     long_context_generation(full, stream_full, 4090, 40, 777, "resident 4091..4130 (two windows)")
+
+
+def test_resident_third_window_beyond_4608_matches_stream_and_oracle(full, stream_full):
+    """Above context 4608 (5101..5130; 576-position chunks on a 256-CU
+    MI355X) a chunk needs a third window: after the LDS window and the
+    register window, the last positions are loaded into LDS again."""
+    long_context_generation(full, stream_full, 5100, 30, 999, "resident 5101..5130 (three windows)")
 
 
 def test_resident_step_and_graph_agree(full):
@@ -420,36 +427,52 @@ def test_batch_step_matches_oracle_per_sequence(full):
         check_logits(int(greedy[slot]), logits[slot], rtok, rlog, f"batch seq {slot}")
 
 
-def test_prefill_512_config5_matches_oracle(full):
-    """BASELINE config 5 prompt: 512 positions through the MFMA prompt path
-    (dense GEMMs + causal attention), then decode steps reusing its cache."""
-    eng, model = full
-    prompt = qo.fill_tokens(512, 4, PROMPT_STREAM, FULL.vocab)
-    say("prefill 512 (config 5) vs oracle")
-    eng.kv_reset(0, 0)
-    cache = qo.Cache(model, 530)
-    tok, _, logits = eng.prefill(0, prompt)
-    rtok, _, rlogits = cache.prefill(prompt)
-    check_logits(tok, logits, rtok, rlogits, "prefill 512")
-    assert eng.decode_state(0).token_position == 512
-    for layer in (0, 11, 23):
-        gk, gv = eng.read_kv(0, layer, 0, 512)
-        assert rel_err(gk, cache.layer(layer, False)[:512]) <= HIDDEN_RTOL, layer
-        assert rel_err(gv, cache.layer(layer, True)[:512]) <= HIDDEN_RTOL, layer
-    feed = rtok
-    for i in range(3):
-        tok, _, logits = eng.step(0, feed)
-        rtok, _, rlogits = cache.decode_step(feed, 512 + i)
-        check_logits(tok, logits, rtok, rlogits, f"decode after prefill {i}")
-        feed = rtok
-    # Config 2's decode range (context 516..523) on the resident kernel,
-    # directly against the oracle teacher-forced on the engine's tokens.
-    say("resident generation at context 516..523 vs oracle")
-    toks, _, gen_logits = eng.generate(0, feed, 8, want_logits=True)
-    for i, t in enumerate(toks.tolist()):
-        rtok, _, rlogits = cache.decode_step(feed, 515 + i)
-        check_logits(t, gen_logits[i], rtok, rlogits, f"resident after prefill {i}")
-        feed = t
+def test_prefill_512_config5_matches_oracle():
+    """BASELINE config 5 on its own model (weights seed 4): the 512-token
+    prompt through the MFMA prompt path (dense GEMMs + causal attention),
+    then 128 greedy decode steps reusing its cache: 3 qd_step calls, the rest
+    one resident generation, each against the oracle teacher-forced on the
+    engine's tokens."""
+    say("config 5: seed-4 model, engine + oracle")
+    eng = qd.Engine(layers=FULL.layers, vocab=FULL.vocab, capacity=512 + 128 + 8, max_batch=1)
+    eng.load_synthetic(4)
+    model = qo.Model(FULL)
+    model.fill_synthetic(4)
+    try:
+        prompt = qo.fill_tokens(512, 4, PROMPT_STREAM, FULL.vocab)
+        say("prefill 512 (config 5) vs oracle")
+        eng.kv_reset(0, 0)
+        cache = qo.Cache(model, 530 + 128)
+        tok, _, logits = eng.prefill(0, prompt)
+        rtok, _, rlogits = cache.prefill(prompt)
+        check_logits(tok, logits, rtok, rlogits, "prefill 512")
+        assert eng.decode_state(0).token_position == 512
+        for layer in (0, 11, 23):
+            gk, gv = eng.read_kv(0, layer, 0, 512)
+            assert rel_err(gk, cache.layer(layer, False)[:512]) <= HIDDEN_RTOL, layer
+            assert rel_err(gv, cache.layer(layer, True)[:512]) <= HIDDEN_RTOL, layer
+        feed = tok
+        for i in range(3):
+            tok, _, logits = eng.step(0, feed)
+            rtok, _, rlogits = cache.decode_step(feed, 512 + i)
+            check_logits(tok, logits, rtok, rlogits, f"decode after prefill {i}")
+            feed = tok
+        say("resident generation of the other 125 steps (context 516..640) vs oracle")
+        toks, reason, gen_logits = eng.generate(0, feed, 125, want_logits=True)
+        assert reason == qd.STOP_MAXIMUM_TOKENS and len(toks) == 125
+        errs = []
+        for i, t in enumerate(toks.tolist()):
+            rtok, _, rlogits = cache.decode_step(feed, 515 + i)
+            errs.append(check_logits(t, gen_logits[i], rtok, rlogits, f"resident after prefill {i}"))
+            feed = t
+        gk, gv = eng.read_kv(0, 23, 639, 1)
+        assert rel_err(gk[0], cache.layer(23, False)[639]) <= HIDDEN_RTOL
+        assert rel_err(gv[0], cache.layer(23, True)[639]) <= HIDDEN_RTOL
+        say(f"config 5: max logits rel err {max(errs):.3e}")
+        cache.close()
+    finally:
+        eng.close()
+        model.close()
 
 
 def test_profile_prefill_matches_prefill(full):
