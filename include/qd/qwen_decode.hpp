@@ -119,6 +119,15 @@ class Engine {
                   top_logit));
     return greedy;
   }
+  // The same step replayed from the slot's captured HIP graph (qd_step_graph).
+  uint32_t step_graph(uint32_t seq, uint32_t token, std::vector<float> *logits = nullptr,
+                      float *top_logit = nullptr) {
+    if (logits) logits->resize(config().vocab);
+    uint32_t greedy = 0;
+    check(qd_step_graph(get(), seq, token, logits ? logits->data() : nullptr, &greedy,
+                        top_logit));
+    return greedy;
+  }
 
   uint32_t prefill(uint32_t seq, const std::vector<uint32_t> &tokens,
                    std::vector<float> *last_logits = nullptr,
