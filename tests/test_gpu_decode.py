@@ -290,6 +290,34 @@ def test_resident_config2_context_512_matches_stream_and_oracle(full, stream_ful
     long_context_generation(full, stream_full, 512, 16, 31337, "config 2 resident 513..528")
 
 
+def test_config2_bench_chain_matches_oracle(full):
+    """BASELINE config 2 exactly as bench.py runs it: the seed-1 model, the
+    512-token prompt of the bench's stream prefilled on the MFMA path, then
+    one resident launch of 64 greedy tokens (context 513..576). Every step's
+    logits and token against the oracle teacher-forced on the engine's
+    tokens."""
+    eng, model = full
+    prompt = qo.fill_tokens(512, 1, PROMPT_STREAM, FULL.vocab)
+    say("config 2 bench chain: prefill 512 + 64 resident tokens vs oracle")
+    eng.kv_reset(3, 0)
+    first, _, _ = eng.prefill(3, prompt, want_logits=False)
+    toks, reason, logits = eng.generate(3, first, 64, want_logits=True)
+    assert reason == qd.STOP_MAXIMUM_TOKENS and len(toks) == 64
+    cache = qo.Cache(model, 512 + 64 + 8)
+    rtok, _, rlog = cache.prefill(prompt)
+    assert rtok == first or margin(rlog) <= MARGIN
+    feed, errs = first, []
+    for i, t in enumerate(toks.tolist()):
+        rtok, _, rlog = cache.decode_step(feed, 512 + i)
+        errs.append(check_logits(t, logits[i], rtok, rlog, f"config 2 step {i}"))
+        feed = t
+    gk, gv = eng.read_kv(3, 23, 512, 64)
+    assert rel_err(gk, cache.layer(23, False)[512:576]) <= HIDDEN_RTOL
+    assert rel_err(gv, cache.layer(23, True)[512:576]) <= HIDDEN_RTOL
+    cache.close()
+    say(f"config 2 bench chain: max logits rel err {max(errs):.3e}")
+
+
 def test_resident_config3_context_4096_matches_stream_and_oracle(full, stream_full):
     """BASELINE config 3 as the bench runs it: the resident kernel at context
     4065..4096 (on a 256-CU MI355X, 464-position chunks, 9 per KV head, each

@@ -55,6 +55,19 @@ def test_rng_tokens_uniform_in_range():
     assert counts.min() > 0.9 * 200000 / 16
 
 
+def test_bench_prompt_stream_is_the_oracles():
+    """bench.py draws its prompts with its own copy of the token generator;
+    the GPU tests that replay a bench workload draw them from the oracle."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "bench_mod", os.path.join(os.path.dirname(__file__), "..", "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    for n, seed, stream in ((512, 1, 0x300000), (64, 3, 0x410005), (512, 4, 0x300000)):
+        assert np.array_equal(bench.stream_tokens(n, seed, stream, 151936),
+                              qo.fill_tokens(n, seed, stream, 151936)), (n, seed, stream)
+
+
 def test_synthetic_fill_distributions():
     shape = qo.ModelShape(hidden=128, heads=2, kv_heads=1, head_dim=64, intermediate=256, vocab=300, layers=2)
     m = qo.Model(shape)
