@@ -309,7 +309,7 @@ __global__ __launch_bounds__(kBlock) void gemm_reduce_rows_kernel(const float *_
 }
 
 // ---- causal GQA flash attention ---------------------------------------------------
-// Workgroup = (query head h, block of 16 prompt rows); its four waves take
+// One query block = (query head h, 16 prompt rows); a workgroup's four waves take
 // the key blocks (32 positions) round-robin, each keeping an online softmax
 // and an output accumulator for the 16 queries, merged in LDS at the end.
 // Per key block a wave computes S = Q . K^T (two 16 x 16 tiles over 64
@@ -346,12 +346,12 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-__global__ __launch_bounds__(kBlock) void attention_prefill_kernel(
-    const float *__restrict__ qkv, int rows, int pos0, int nq, int nkv,
+// Query block qb of head h (the causal extent of a block grows with qb).
+__device__ __forceinline__ void attention_prefill_block(
+    PrefillAttnLds &sh, int qb, const float *__restrict__ qkv, int rows, int pos0, int nq, int nkv,
     const float *__restrict__ k_cache, const float *__restrict__ v_cache, float *__restrict__ out) {
-  __shared__ PrefillAttnLds sh;
   const int h = blockIdx.y;
-  const int r0 = blockIdx.x * kQBlock;
+  const int r0 = qb * kQBlock;
   const int g = h / (nq / nkv);
   const int qd = nq * kHeadDim, kvd = nkv * kHeadDim;
   const int ld = qd + 2 * kvd;
@@ -500,6 +500,22 @@ __global__ __launch_bounds__(kBlock) void attention_prefill_kernel(
   }
 }
 
+// Workgroup (pair p, head h) takes query blocks p and nqb - 1 - p: the pair's
+// key blocks add up to about the same count for every p, so the launch is
+// one balanced round of workgroups instead of a long causal tail.
+__global__ __launch_bounds__(kBlock) void attention_prefill_kernel(
+    const float *__restrict__ qkv, int rows, int pos0, int nq, int nkv,
+    const float *__restrict__ k_cache, const float *__restrict__ v_cache, float *__restrict__ out) {
+  __shared__ PrefillAttnLds sh;
+  const int nqb = (rows + kQBlock - 1) / kQBlock;
+  const int p = blockIdx.x;
+  attention_prefill_block(sh, p, qkv, rows, pos0, nq, nkv, k_cache, v_cache, out);
+  const int q = nqb - 1 - p;
+  if (q <= p) return;
+  __syncthreads();  // the first block's merge has read the LDS
+  attention_prefill_block(sh, q, qkv, rows, pos0, nq, nkv, k_cache, v_cache, out);
+}
+
 }  // namespace
 
 hipError_t launch_gemm_nt(hipStream_t s, const float *A, int lda, const float *W, int ldw,
@@ -549,7 +565,8 @@ hipError_t launch_rope_kv_rows(hipStream_t s, float *qkv, int rows, int pos0, in
 hipError_t launch_attention_prefill(hipStream_t s, const float *qkv, int rows, int pos0, int nq,
                                     int nkv, const float *k_cache, const float *v_cache,
                                     float *out) {
-  const dim3 grid((rows + kQBlock - 1) / kQBlock, nq);
+  const int nqb = (rows + kQBlock - 1) / kQBlock;
+  const dim3 grid((nqb + 1) / 2, nq);
   attention_prefill_kernel<<<grid, kBlock, 0, s>>>(qkv, rows, pos0, nq, nkv, k_cache, v_cache, out);
   return hipGetLastError();
 }
