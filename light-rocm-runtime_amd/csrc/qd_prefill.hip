@@ -417,14 +417,21 @@ __device__ __forceinline__ void attention_prefill_block(
       vs[row][4 * lr + 3] = vv.w;
     }
     if (kb + kWavesPerBlock < kblocks) load_block(kb + kWavesPerBlock);
-    // S tiles: keys k0 + 16 tt + lr.
-    f4v s[2];
+    // S tiles: keys k0 + 16 tt + lr. Every B operand is read from LDS before
+    // the first MFMA (one wait instead of one per step), and the two tiles'
+    // chains run interleaved; each chain keeps its order over st.
+    float kop[2][kHeadDim / 4];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      s[tt] = f4v{0.f, 0.f, 0.f, 0.f};
+    for (int st = 0; st < kHeadDim / 4; ++st) {
+      kop[0][st] = ks[lr][4 * st + lg];
+      kop[1][st] = ks[16 + lr][4 * st + lg];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f4v s[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int st = 0; st < kHeadDim / 4; ++st)
-        s[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], ks[16 * tt + lr][4 * st + lg], s[tt], 0, 0, 0);
+    for (int st = 0; st < kHeadDim / 4; ++st) {
+      s[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], kop[0][st], s[0], 0, 0, 0);
+      s[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], kop[1][st], s[1], 0, 0, 0);
     }
     // Online softmax per query row (row = lg * 4 + r, spread over the 16
     // lanes of DPP row lg and the two tiles).
@@ -455,14 +462,21 @@ __device__ __forceinline__ void attention_prefill_block(
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[dt][r] *= corr[r];
-    // O += P . V: A = P[row lr][key 4 st + lg], B = V[key 4 st + lg][dim 16 dt + lr].
+    // O += P . V: A = P[row lr][key 4 st + lg], B = V[key 4 st + lg][dim 16 dt + lr],
+    // the operands read from LDS first as for S.
+    float pa[kKBlock / 4], vb[kKBlock / 4][4];
 #pragma unroll
     for (int st = 0; st < kKBlock / 4; ++st) {
-      const float pa = ps[lr][4 * st + lg];
+      pa[st] = ps[lr][4 * st + lg];
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) vb[st][dt] = vs[4 * st + lg][16 * dt + lr];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < kKBlock / 4; ++st)
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vs[4 * st + lg][16 * dt + lr], o[dt], 0, 0, 0);
-    }
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[st], vb[st][dt], o[dt], 0, 0, 0);
   }
   // Merge the four waves' partials.
 #pragma unroll
