@@ -22,10 +22,26 @@ def say(msg):
     print(f"[gpu-case] {msg}", flush=True)
 
 
+def engine_hip_runtime():
+    """The HIP runtime library the engine library runs on, by the path mapped
+    into this process. torch, when an earlier test imported it, maps a HIP
+    runtime of its own under the same name, and that copy does not see the
+    engine's device state; so the copy is picked by path, not by name."""
+    qd.lib()
+    paths = []
+    with open("/proc/self/maps") as f:
+        for line in f:
+            parts = line.split()
+            if len(parts) >= 6 and "libamdhip64" in parts[5] and parts[5] not in paths:
+                paths.append(parts[5])
+    mine = [p for p in paths if "/torch/" not in p]
+    return C.CDLL(mine[0] if mine else "libamdhip64.so")
+
+
 def free_device_bytes():
-    """hipMemGetInfo's free bytes of the current device (the HIP runtime the
-    engine library already loaded)."""
-    hip = C.CDLL("libamdhip64.so")
+    """hipMemGetInfo's free bytes of the current device, through the engine's
+    HIP runtime."""
+    hip = engine_hip_runtime()
     free, total = C.c_size_t(), C.c_size_t()
     assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
     return int(free.value)
