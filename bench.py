@@ -227,8 +227,10 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token, w
 
     # Decode paths over the same K tokens, interleaved over trials:
     # "resident" (qd_generate_resident: one launch, argmax fed back on the
-    # device) and "step" (qd_step per token with the logits copied to the
-    # host: the reference executor surface's per-token contract).
+    # device) and the per-token contract of the reference's executor surface
+    # (one call per token, its logits copied to the host): "step" (qd_step,
+    # one resident-kernel launch per token) and "graph" (qd_step_graph, the
+    # stream kernels replayed from the slot's captured HIP graph).
     def resident():
         toks, reason, _ = eng.generate(0, first, K)
         assert len(toks) == K, (len(toks), reason)
@@ -241,8 +243,6 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token, w
             out.append(tok)
         return out, None
 
-    # "graph": the same per-token contract with the step's launches replayed
-    # from the slot's captured HIP graph (qd_step_graph).
     def graph():
         out, tok = [], first
         for _ in range(K):
@@ -250,25 +250,13 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token, w
             out.append(tok)
         return out, None
 
-    # "resident_step": the same per-token contract (one call per token, its
-    # logits copied to the host) served by the resident kernel: one
-    # cooperative launch per token (qd_generate_resident, max_tokens 1).
-    def resident_step():
-        out, tok = [], first
-        for _ in range(K):
-            toks, _, _ = eng.generate(0, tok, 1, want_logits=True)
-            tok = int(toks[0])
-            out.append(tok)
-        return out, None
-
-    paths = {"resident": resident, "step": step, "graph": graph, "resident_step": resident_step}
+    paths = {"resident": resident, "step": step, "graph": graph}
     if not with_graph:
         del paths["graph"]
     if W:
         log(f"warmup {W} tokens per path")
         eng.generate(0, first, W)
-        one = lambda seq, tok, want_logits: eng.generate(seq, tok, 1, want_logits=want_logits)[0]
-        for fn in (eng.step, eng.step_graph, one) if with_graph else (eng.step, one):
+        for fn in (eng.step, eng.step_graph) if with_graph else (eng.step,):
             eng.kv_reset(0, prompt_len)
             tok = first
             for _ in range(W):
@@ -290,11 +278,10 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token, w
             assert toks == tokens[name], f"{name}: trial {t} produced other tokens"
     # The paths run the same arithmetic: the same greedy chain.
     assert all(tokens[name] == tokens["resident"] for name in paths), \
-        "resident, step, graph and per-token resident paths disagree"
+        "resident, step and graph paths disagree"
     res_wall = spread(samples["resident"]["wall_ms"])
     step_wall = spread(samples["step"]["wall_ms"])
     graph_wall = spread(samples["graph"]["wall_ms"]) if with_graph else None
-    rstep_wall = spread(samples["resident_step"]["wall_ms"])
     total_bytes = sum(step_bytes(prompt_len + 1 + i) for i in range(K))
     tok_s = K / (res_wall["median"] * 1e-3)
 
@@ -346,8 +333,7 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token, w
         "trials": {"count": trials, "order": "interleaved rotations, forwards then backwards",
                    "resident_ms": {k: round(v, 3) for k, v in res_wall.items()},
                    "step_ms": {k: round(v, 3) for k, v in step_wall.items()},
-                   "graph_ms": {k: round(v, 3) for k, v in graph_wall.items()} if graph_wall else None,
-                   "resident_step_ms": {k: round(v, 3) for k, v in rstep_wall.items()}},
+                   "graph_ms": {k: round(v, 3) for k, v in graph_wall.items()} if graph_wall else None},
         "step_hbm": {"achieved_gbs": round(total_bytes / (res_wall["median"] * 1e-3) / 1e9, 1),
                      "peak_gbs": HBM_PEAK_GBS, "bytes_per_token": round(total_bytes / K)},
         "device_tokens_per_s": round(K / (roof["avg_us"] * 1e-6), 2) if grid else None,
@@ -355,22 +341,18 @@ def decode_line(K, W, no_cpu, trials, prompt_len, workload, traffic_per_token, w
         "hbm_measured": {"read_gbs": round(read_gbs, 1), "copy_gbs": round(copy_gbs, 1),
                          "probe": "qd_probe_hbm: best of 5 passes over 2 GiB"},
         # The per-token contract (one call per token, its 607,744-byte
-        # logits row copied to the host) on each of the engine's paths; the
-        # headline figure is the fastest, the resident kernel launched once
-        # per token.
+        # logits row copied to the host): qd_step, and the stream kernels
+        # replayed from a HIP graph beside it.
         "executor_surface": {
-            "path": "qd_generate_resident with max_tokens 1 per token: one cooperative launch of the "
-                    "resident kernel + the logits copy to the host",
-            "tokens_per_s": round(K / (rstep_wall["median"] * 1e-3), 2),
-            "ms_per_token": round(rstep_wall["median"] / K, 4),
-            "step": {"path": "qd_step per token: stream-ordered kernels + the logits copy",
-                     "tokens_per_s": round(K / (step_wall["median"] * 1e-3), 2),
-                     "ms_per_token": round(step_wall["median"] / K, 4),
-                     "dominant_kernel": roofline_hbm(dname, davg_us, davg_bytes)},
-            "graph": {"path": "qd_step_graph per token: qd_step's kernels replayed from the slot's "
-                              "captured HIP graph + the logits copy",
+            "path": "qd_step per token: one cooperative launch of the resident kernel + the logits "
+                    "copy to the host",
+            "tokens_per_s": round(K / (step_wall["median"] * 1e-3), 2),
+            "ms_per_token": round(step_wall["median"] / K, 4),
+            "graph": {"path": "qd_step_graph per token: the stream-ordered step kernels replayed from "
+                              "the slot's captured HIP graph + the logits copy",
                       "tokens_per_s": round(K / (graph_wall["median"] * 1e-3), 2),
-                      "ms_per_token": round(graph_wall["median"] / K, 4)} if graph_wall else None,
+                      "ms_per_token": round(graph_wall["median"] / K, 4),
+                      "dominant_kernel": roofline_hbm(dname, davg_us, davg_bytes)} if graph_wall else None,
         },
         "cpu_baseline": cpu,
         "path": f"resident megakernel, {grid} workgroups" if grid else "stream-ordered kernels",

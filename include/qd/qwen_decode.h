@@ -255,15 +255,18 @@ QD_API qd_status qd_read_logits(qd_engine *engine, uint32_t seq, float *out,
 /* One full decode step of `token_in` at the slot's position: embedding, all
  * layers, final norm, LM head, argmax (lowest index on ties); advances the
  * position by one. logits_out (vocab floats) and top_logit may be NULL.
- * Replaces the per-token loop body of
- * benchmarks/triton_mini_decoder_layer.cpp:1041-1076 (stack + ModelTail::run
- * + copy_logits + host top_logits). */
+ * Runs as one launch of the resident kernel when the engine has one (else,
+ * and with QD_RESIDENT=0, as the stream-ordered kernels); the two compute
+ * the same values bit for bit and leave the same decode state. Replaces the
+ * per-token loop body of benchmarks/triton_mini_decoder_layer.cpp:1041-1076
+ * (stack + ModelTail::run + copy_logits + host top_logits). */
 QD_API qd_status qd_step(qd_engine *engine, uint32_t seq, uint32_t token_in,
                          float *logits_out, uint32_t *greedy_out,
                          float *top_logit);
 
-/* qd_step through a HIP graph: the slot's launch sequence (embedding, every
- * layer, LM head, argmax: 147 kernels at 24 layers) is captured on the
+/* The stream-ordered step through a HIP graph: the slot's launch sequence
+ * (embedding, every layer, LM head, argmax: 147 kernels at 24 layers) is
+ * captured on the
  * slot's first call and replayed by one hipGraphLaunch per token after that;
  * the kernels read the position and token from the slot's device state, so
  * one graph serves every step. Same arguments, semantics and results (bit

@@ -1403,17 +1403,46 @@ qd_status step_common(qd_engine *e, uint32_t seq, uint32_t token, float *logits_
       fail(QD_ERROR_INVALID_ARGUMENT, "sequence %u is full (capacity %zu)", seq, e->CAP);
     e->set_device();
     float *dev_logits = e->logits + seq * e->V;
-    hipGraphExec_t g = graph ? e->step_graph(seq) : nullptr;
-    e->push_state(seq, token, qd::kModeStep, UINT32_MAX, 0);
-    if (g)
-      check(hipGraphLaunch(g, e->stream), "hipGraphLaunch");
-    else
-      e->enqueue_step(seq, dev_logits, 0, nullptr);
+    // qd_step runs the resident kernel for one token when the engine has it
+    // (one cooperative launch instead of the stream kernels' ~150); the graph
+    // replays the stream kernels. Both compute the same values bit for bit.
+    qd::RolePlan plan{};
+    bool resident = !graph && e->resident_fits(1) && e->resident_plan(e->positions[seq] + 1, &plan);
+    if (resident) {
+      const hipError_t err = e->launch_resident(plan, seq, token, 1, UINT32_MAX, dev_logits, 0, nullptr);
+      if (err != hipSuccess) {
+        if (!e->resident_refused(err)) check(err, "resident launch");
+        resident = false;
+      }
+    }
+    if (!resident) {
+      hipGraphExec_t g = graph ? e->step_graph(seq) : nullptr;
+      e->push_state(seq, token, qd::kModeStep, UINT32_MAX, 0);
+      if (g)
+        check(hipGraphLaunch(g, e->stream), "hipGraphLaunch");
+      else
+        e->enqueue_step(seq, dev_logits, 0, nullptr);
+    }
     check(hipMemcpyAsync(&e->h_states[seq], e->states + seq, sizeof(qd::SeqState),
                          hipMemcpyDeviceToHost, e->stream), "D2H");
+    if (resident) e->enqueue_resident_error();
     if (logits_out)
       check(hipMemcpyAsync(logits_out, dev_logits, e->V * 4, hipMemcpyDeviceToHost, e->stream), "D2H");
     e->sync();
+    if (resident) {
+      e->resident_status(*e->h_error);
+      // The slot's state as the stream step leaves it: a step, not a
+      // one-token generation (the kernel wrote position, token and logit).
+      qd::SeqState &h = e->h_states[seq];
+      h.generated = 0;
+      h.max_tokens = 0;
+      h.stop_reason = 0;
+      h.stopped = 0;
+      h.eos = UINT32_MAX;
+      h.mode = qd::kModeStep;
+      check(hipMemcpyAsync(e->states + seq, &h, sizeof(h), hipMemcpyHostToDevice, e->stream),
+            "state upload");
+    }
     e->positions[seq] += 1;
     if (greedy) *greedy = e->h_states[seq].token;
     if (top_logit) *top_logit = e->h_states[seq].top_logit;

@@ -343,12 +343,13 @@ def test_resident_third_window_beyond_4608_matches_stream_and_oracle(full, strea
 def test_resident_step_and_graph_agree(full):
     """The reference's three-way cross-check of one greedy chain
     (benchmarks/qwen_stateful_graph.cpp:1619-1746): the resident megakernel
-    (qd_generate_resident), the per-token launches (qd_step) and the same
-    launches replayed from a captured HIP graph (qd_step_graph, one graph
-    per slot, benchmarks/qwen_hip_graph.hpp:27-199) give the same tokens,
-    logits, decode state and K/V rows, bit for bit. Every graph replay is
-    checked against the eager step that ran just before it, with the
-    program's own eager work and host synchronisations in between."""
+    over several tokens (qd_generate_resident), one resident launch per token
+    (qd_step) and the stream-ordered step kernels replayed from a captured
+    HIP graph (qd_step_graph, one graph per slot,
+    benchmarks/qwen_hip_graph.hpp:27-199) give the same tokens, logits, top
+    logits, positions and K/V rows, bit for bit. Every graph replay is
+    checked against the step that ran just before it, with the program's
+    own work and host synchronisations in between."""
     eng, _ = full
     prompt = qo.fill_tokens(11, 1, PROMPT_STREAM + 9, FULL.vocab)
     steps = 8

@@ -47,11 +47,13 @@ def test_resident_wait_give_up_reports_device_fault(monkeypatch):
         assert err.value.status == qd.DEVICE_FAULT
         assert "gave up" in str(err.value)
         # The position did not move, and the device is healthy: a stream step
-        # from the same state equals the same step on an untouched engine.
+        # (the graph replay of the step kernels) from the same state equals
+        # the step on an untouched engine (the resident kernel's one-token
+        # launch, as qd_step runs it there).
         assert eng.decode_state(0).token_position == len(prompt)
         ref.kv_reset(0, 0)
         ref.prefill(0, prompt, want_logits=False)
-        tok, _, logits = eng.step(0, first)
+        tok, _, logits = eng.step_graph(0, first)
         tok2, _, logits2 = ref.step(0, first)
         assert tok == tok2 and np.array_equal(logits, logits2)
         # And the untouched engine's resident path still completes.
