@@ -368,6 +368,10 @@ def test_resident_step_and_graph_agree(full):
         assert ts == tg == int(rtoks[i]) and tops == topg, i
         assert np.array_equal(ls, lg) and np.array_equal(ls, rlogits[i]), i
         assert eng.decode_state(1).token_position == eng.decode_state(2).token_position == len(prompt) + i + 1
+        # qd_step's one-token resident launch leaves the stream step's state.
+        d1, d2 = eng.decode_state(1), eng.decode_state(2)
+        assert [getattr(d1, f) for f, _ in qd.DecodeState._fields_] == \
+            [getattr(d2, f) for f, _ in qd.DecodeState._fields_], i
         fs, fg = ts, tg
     assert_kv_equal(eng, eng, 0, 1, len(prompt), steps, "resident vs step KV")
     assert_kv_equal(eng, eng, 1, 2, len(prompt), steps, "step vs graph KV")
