@@ -1560,7 +1560,12 @@ struct Roles {
               attn_tile_ops(
                   qa,
                   [&](int i) {
-                    return kfresh ? reinterpret_cast<const float4 *>(ar.kn)[(kHeadDim / 8) * hq + i] : kw2[i];
+                    // The fresh row as a register value (pin): a choice
+                    // between two loads would be folded into one load
+                    // through a generic pointer, keeping kw2 in scratch.
+                    float4 f = reinterpret_cast<const float4 *>(ar.kn)[(kHeadDim / 8) * hq + i];
+                    pin(f);
+                    return kfresh ? f : kw2[i];
                   },
                   [&](int k) { return k >= knew ? vfresh : vw2[k]; }, ps, t0, end, acc);
             }
