@@ -283,12 +283,20 @@ __device__ __forceinline__ void attn_tile_ops(const float4 (&q)[kHeadDim / 4], K
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // V operands in groups of 8, each group read before its MFMAs (one LDS
+  // wait per group rather than one per position).
 #pragma unroll
-  for (int k = 0; k < kAttnTile; ++k) {
-    const float vv = vl(k);
-    const float a = attn_c(pa[k / 4], k % 4);
-    acc.o[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, vv, acc.o[0], 0, 0, 1);
-    acc.o[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, vv, acc.o[1], 0, 0, 2);
+  for (int k0 = 0; k0 < kAttnTile; k0 += 8) {
+    float vv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) vv[j] = vl(k0 + j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float a = attn_c(pa[(k0 + j) / 4], (k0 + j) % 4);
+      acc.o[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, vv[j], acc.o[0], 0, 0, 1);
+      acc.o[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, vv[j], acc.o[1], 0, 0, 2);
+    }
   }
 }
 
