@@ -57,6 +57,13 @@ def summarize(tr: np.ndarray, layers: int) -> list[str]:
     xcd = np.arange(grid) % 8
     lines.append("lm head done by XCD: " + ", ".join(
         f"{np.median(lm[xcd == x, 1] - lm[xcd == x, 0]):.1f}" for x in range(8)))
+    # Argmax: stage 12 is when a CU holds every CU's top-1 partial, stage 13
+    # when it has the token; times from the last CU's LM head end.
+    am = tr[:, layers, 12:14]
+    last = lm[:, 1].max()
+    lines.append("argmax after the last lm head end: " + ", ".join(
+        f"{name} gathered {np.median(am[roles == r, 0]) - last:.2f} done {np.median(am[roles == r, 1]) - last:.2f}"
+        for r, name in enumerate(ROLES) if (roles == r).any()))
     return lines
 
 
