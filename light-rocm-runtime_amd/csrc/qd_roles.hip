@@ -68,7 +68,7 @@ constexpr int kAttnCap = 256;     // positions of an attention window staged in 
 #define QD_SLOTS_O 4
 #endif
 #ifndef QD_SLOTS_G
-#define QD_SLOTS_G 2
+#define QD_SLOTS_G 3
 #endif
 #ifndef QD_DOWN_REG_F4
 #define QD_DOWN_REG_F4 18
@@ -2056,8 +2056,12 @@ bool plan_roles(int grid, int hidden, int inter, int heads, int kv_heads, int ma
   for (int r = 0; r < 4; ++r) floor_weights += need_of(r);
   // One attention CU per (KV head, chunk) unit of the longest context, or
   // as many as the weight roles leave (an attention CU then takes several
-  // units, the later ones staged after its query arrives).
-  int n_attn = std::min(kv_heads * attn_chunks(max_length), grid - floor_weights);
+  // units, the later ones staged after its query arrives). A long context
+  // gets a chunk per window of kAttnCap positions (up to kAttnMaxChunks),
+  // so each chunk's tiles run as one round on the CU's waves.
+  const int chunks = std::max(attn_chunks(max_length),
+                              std::min(kAttnMaxChunks, (max_length + kAttnCap - 1) / kAttnCap));
+  int n_attn = std::min(kv_heads * chunks, grid - floor_weights);
   n_attn -= n_attn % kv_heads;  // whole KV groups
   if (n_attn < kv_heads) return false;
   const int rest = grid - n_attn;
