@@ -348,11 +348,15 @@ struct AttnStage {
 };
 constexpr int kAttnStageFloats = kAttnSlots * kMaxGroup * (2 + kHeadDim);
 
-// The chunk partial of head row h, output dim d: the slots that took a tile
-// (the first min(tiles, kAttnSlots)) folded in slot order (attn_fold). All
-// slots' values are read before the first fold.
+// The chunk partial of head row h, output dim d, over the slots that took a
+// tile (the first min(tiles, kAttnSlots)): M = max_s m_s, w_s = 2^(m_s - M)
+// (zero for a slot without a tile), L = sum_s w_s l_s and A = sum_s w_s a_s,
+// each sum over the rounded products (never contracted) as the pairwise tree
+// ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7)). The slots' weights are
+// independent, so no step waits for the previous slot's fold.
 __device__ __forceinline__ void attn_slot_merge(const AttnStage &st, int tiles, int h, int d, float &M, float &L,
                                                 float &A) {
+  static_assert(kAttnSlots == 8, "three-level tree");
   float sm[kAttnSlots], sl[kAttnSlots], so[kAttnSlots];
 #pragma unroll
   for (int w = 0; w < kAttnSlots; ++w) {
@@ -360,12 +364,19 @@ __device__ __forceinline__ void attn_slot_merge(const AttnStage &st, int tiles, 
     sl[w] = st.l[w * kMaxGroup + h];
     so[w] = st.o[(w * kMaxGroup + h) * kHeadDim + d];
   }
-  M = -INFINITY;
-  L = 0.f;
-  A = 0.f;
+  float mx[kAttnSlots];
 #pragma unroll
-  for (int w = 0; w < kAttnSlots; ++w)
-    if (w < tiles) attn_fold(sm[w], sl[w], so[w], M, L, A);
+  for (int w = 0; w < kAttnSlots; ++w) mx[w] = w < tiles ? sm[w] : -INFINITY;
+  M = fmaxf(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])), fmaxf(fmaxf(mx[4], mx[5]), fmaxf(mx[6], mx[7])));
+  float pl[kAttnSlots], pa[kAttnSlots];
+#pragma unroll
+  for (int w = 0; w < kAttnSlots; ++w) {
+    const float wt = w < tiles ? exp2_fast(sm[w] - M) : 0.f;
+    pl[w] = w < tiles ? __fmul_rn(wt, sl[w]) : 0.f;
+    pa[w] = w < tiles ? __fmul_rn(wt, so[w]) : 0.f;
+  }
+  L = ((pl[0] + pl[1]) + (pl[2] + pl[3])) + ((pl[4] + pl[5]) + (pl[6] + pl[7]));
+  A = ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pa[4] + pa[5]) + (pa[6] + pa[7]));
 }
 
 // Merge of one head's partials for output dim d; part(c, k) returns element
