@@ -175,6 +175,11 @@ __device__ __forceinline__ float attn_c(float4 v, int c) { return c == 0 ? v.x :
 //           dims m (BLGP 1) and 32 + m (BLGP 2).
 constexpr int kAttnTile = 32;
 constexpr int kAttnMaxGroup = 8;
+// A-operand broadcast of the score MFMAs (CBSZ): block 0 of each group of
+// 2^3 blocks (ABID 0) hands its A to the group, i.e. lanes 0-3 to lanes 0-31
+// and lanes 32-35 to lanes 32-63; the A operand (a head's query) is the same
+// in every block of a half.
+constexpr int kAttnCbsz = 3;
 // Probability tile of one wave in LDS: [8 rows][32 positions], rows 36 floats
 // apart (16-byte aligned, the 8 rows' float4 reads on distinct banks).
 constexpr int kAttnTilePsStride = 36;
@@ -203,13 +208,19 @@ struct AttnAcc {
 };
 
 // Query operand of a group of up to 8 heads: q[d4] = float4 d4 of the query
-// of head 4 (l / 32) + l % 4 (zero past the group's `heads`). q4(h, d4)
-// returns float4 d4 of head h's query.
+// of head 4 (l / 32) + l % 4 (zero past the group's `heads`), in lanes 0-3
+// and 32-35 only (the tiles' MFMAs broadcast those lanes' A operand to
+// their half; the other lanes hold zeros). q4(h, d4) returns float4 d4 of
+// head h's query.
 template <typename Q4>
 __device__ __forceinline__ void attn_query(Q4 q4, int heads, float4 (&q)[kHeadDim / 4]) {
   const int row = 4 * (lane_id() >> 5) + (lane_id() & 3);
 #pragma unroll
-  for (int d4 = 0; d4 < kHeadDim / 4; ++d4) q[d4] = row < heads ? q4(row, d4) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int d4 = 0; d4 < kHeadDim / 4; ++d4) q[d4] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if ((lane_id() & 31) < 4 && row < heads) {
+#pragma unroll
+    for (int d4 = 0; d4 < kHeadDim / 4; ++d4) q[d4] = q4(row, d4);
+  }
 }
 
 // One tile of 32 positions [t0, t0 + 32) for every head of a KV group of up
@@ -241,9 +252,9 @@ __device__ __forceinline__ void attn_tile_ops(const float4 (&q)[kHeadDim / 4], K
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const float b = attn_c(kv[i], c);
-      s[2 * (i & 1)] = __builtin_amdgcn_mfma_f32_4x4x1f32(attn_c(q[i], c), b, s[2 * (i & 1)], 0, 0, 1);
-      s[2 * (i & 1) + 1] =
-          __builtin_amdgcn_mfma_f32_4x4x1f32(attn_c(q[kHeadDim / 8 + i], c), b, s[2 * (i & 1) + 1], 0, 0, 2);
+      s[2 * (i & 1)] = __builtin_amdgcn_mfma_f32_4x4x1f32(attn_c(q[i], c), b, s[2 * (i & 1)], kAttnCbsz, 0, 1);
+      s[2 * (i & 1) + 1] = __builtin_amdgcn_mfma_f32_4x4x1f32(attn_c(q[kHeadDim / 8 + i], c), b,
+                                                              s[2 * (i & 1) + 1], kAttnCbsz, 0, 2);
     }
   }
   const attn_f4v sc = (s[0] + s[1]) + (s[2] + s[3]);
