@@ -212,6 +212,10 @@ constexpr int kRegionBytes = kLdsBytes - kRegionOffset;
 // Whole-workgroup gather of `pairs` tagged pairs: map(p, src_pair, dst)
 // names pair p's source pair index and its destination float index (two
 // consecutive floats). Returns false when the wait gave up (error raised).
+// Each wave polls its own items until they are all complete, with no
+// workgroup barrier between its polls; one barrier at the end makes the
+// whole destination visible to every wave. (The same holds for gather4 and
+// gather4_put.)
 template <int kMaxPer, typename Map>
 __device__ bool gather_map(const TagVec &src, int pairs, uint32_t tag, float *dst, Wait wait,
                            uint32_t *flags, Map map) {
@@ -220,6 +224,7 @@ __device__ bool gather_map(const TagVec &src, int pairs, uint32_t tag, float *ds
 #pragma unroll
   for (int k = 0; k < kMaxPer; ++k)
     if (t + k * kT < pairs) pending |= 1u << k;
+  bool ok = true;
   for (uint32_t spin = 0;; ++spin) {
     Pair2 got[kMaxPer];
 #pragma unroll
@@ -244,12 +249,14 @@ __device__ bool gather_map(const TagVec &src, int pairs, uint32_t tag, float *ds
     // Every wave's earlier vector memory operations (its LDS DMA above all)
     // are complete when the gather returns.
     vm_wait();
-    if (block_all(pending == 0, flags)) return true;
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
     if (spin > wait.limit) {
-      if (t == 0) atomicOr(wait.error, kResidentWaitGaveUp);
-      return false;
+      if (lane_id() == 0) atomicOr(wait.error, kResidentWaitGaveUp);
+      ok = false;
+      break;
     }
   }
+  return block_all(ok, flags);
 }
 
 // Contiguous gather: elements [first, first + n) (first and n even) -> dst.
@@ -319,6 +326,7 @@ __device__ bool gather4(const Slots &src, int n4, float4 *dst, Wait wait, uint32
 #pragma unroll
   for (int k = 0; k < kMaxPer; ++k)
     if (t + k * kT < n4) pending |= 1u << k;
+  bool ok = true;
   for (uint32_t spin = 0;; ++spin) {
     Quad got[kMaxPer];
 #pragma unroll
@@ -343,12 +351,14 @@ __device__ bool gather4(const Slots &src, int n4, float4 *dst, Wait wait, uint32
     // Every wave's earlier vector memory operations (its LDS DMA and its
     // slot clears above all) are complete when the gather returns.
     vm_wait();
-    if (block_all(pending == 0, flags)) return true;
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
     if (spin > wait.limit) {
-      if (t == 0) atomicOr(wait.error, kResidentWaitGaveUp);
-      return false;
+      if (lane_id() == 0) atomicOr(wait.error, kResidentWaitGaveUp);
+      ok = false;
+      break;
     }
   }
+  return block_all(ok, flags);
 }
 
 // Contiguous float4s [first4, first4 + n4) of a slot block -> dst[0, n4).
@@ -377,6 +387,7 @@ __device__ bool gather4_put(const Slots &src, int items, Wait wait, uint32_t *fl
     slot[k] = 0;
     if (t + k * kT < items && live(t + k * kT, k, slot[k])) pending |= 1u << k;
   }
+  bool ok = true;
   for (uint32_t spin = 0;; ++spin) {
     Quad got[kMaxPer];
 #pragma unroll
@@ -393,12 +404,14 @@ __device__ bool gather4_put(const Slots &src, int items, Wait wait, uint32_t *fl
       }
     }
     vm_wait();
-    if (block_all(pending == 0, flags)) return true;
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
     if (spin > wait.limit) {
-      if (t == 0) atomicOr(wait.error, kResidentWaitGaveUp);
-      return false;
+      if (lane_id() == 0) atomicOr(wait.error, kResidentWaitGaveUp);
+      ok = false;
+      break;
     }
   }
+  return block_all(ok, flags);
 }
 
 // Publishing a role's outputs. A role CU's outputs are fixed runs of slot
