@@ -113,7 +113,10 @@ __device__ __forceinline__ void pace() {
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0 | (kPaceDepth & 15u) | ((kPaceDepth >> 4) << 14));
 }
 // Whole-workgroup AND (flags: one LDS word per wave). The ballot is taken
-// with the whole wave active, then lane 0 records it.
+// with the whole wave active, then lane 0 records it. Successive calls
+// alternate between two flag sets (Roles::flag_set), so one barrier
+// suffices: a wave writes the set of call k + 2 only after passing call
+// k + 1's barrier, which every wave reaches only after reading call k's.
 __device__ __forceinline__ bool block_all(bool v, uint32_t *flags) {
   const uint32_t wave_all = __builtin_amdgcn_ballot_w64(!v) == 0 ? 1u : 0u;
   if (lane_id() == 0) flags[wave_u()] = wave_all;
@@ -121,7 +124,6 @@ __device__ __forceinline__ bool block_all(bool v, uint32_t *flags) {
   uint32_t all = 1u;
 #pragma unroll
   for (int w = 0; w < kW; ++w) all &= flags[w];
-  lds_barrier();
   return all != 0u;
 }
 
@@ -192,10 +194,9 @@ struct ClockLds {
 struct Common {
   float vec[1024];   // gathered input vector (hidden, h1, residual rows)
   float xn[1024];    // normalised GEMV operand / merged attention
-  float red[kW];
+  uint32_t flags[2][kW];                // block_all, two alternating sets
   float bv[kW];
   uint32_t bi[kW];
-  uint32_t flags[kW];                   // block_all
   float top[2 * kMaxRoleGrid];          // argmax partials (value, index bits); in the
                                         //   layers, a role's outputs staged for their stores
   ClockLds clock;                       // profiling (profiled variant only)
@@ -949,6 +950,13 @@ struct Roles {
   Clock<kProfile> clock;
   uint32_t token, generated = 0, stop_reason = 0;
   float top = 0.f;
+  uint32_t flag_parity = 0;
+  // The block_all flag set of the next workgroup-wide AND (every wave makes
+  // the same sequence of calls).
+  __device__ uint32_t *flag_set() {
+    flag_parity ^= 1u;
+    return cm.flags[flag_parity];
+  }
 
   __device__ Roles(const ResidentArgs &args, unsigned char *lds, int rank_, int nrole_, int wg_)
       : a(args),
@@ -1005,7 +1013,7 @@ struct Roles {
   __device__ bool gather_h1(uint32_t t, int l, int first4, int n4, float *dst) {
     if (!gather4<(NKV * H / 4 + kT - 1) / kT>(slots(l, t, kOffH1, NKV * H), NKV * n4,
                                               reinterpret_cast<float4 *>(dst), wt(),
-                                              cm.flags, [&](int p, int &s4, int &d4) {
+                                              flag_set(), [&](int p, int &s4, int &d4) {
                                                 const int g = p / n4, q = p % n4;
                                                 s4 = g * (H / 4) + first4 + q;
                                                 d4 = g * kH1Stride4 + q;
@@ -1051,7 +1059,7 @@ struct Roles {
     // Item p: float4 q of segment r; rows [b, e) of that float4 land in dst.
     int first[kHidMaxPer], count[kHidMaxPer];
     return gather4_put<kHidMaxPer>(
-        s_hid(l, t), items, wt(), cm.flags,
+        s_hid(l, t), items, wt(), flag_set(),
         [&](int p, int k, int &s4) {
           const int r = r_lo + p / 4, q = p % 4;
           s4 = (kHidSegment / 4) * r + q;
@@ -1232,7 +1240,7 @@ struct Roles {
     const uint32_t par = t & 1u;
     const uint32_t tag_top = tag(t * per_token + 5u * a.layers);
     if (!gather<(kMaxRoleGrid + kT - 1) / kT>(ttop, par * 2 * grid, 2 * grid, tag_top, cm.top,
-                                              wt(), cm.flags))
+                                              wt(), flag_set()))
       return false;
     clock.lap(2 * kRoleCount + 2);
     float best = -INFINITY;
@@ -1500,7 +1508,7 @@ struct Roles {
         constexpr int q4 = GROUP * kHeadDim / 4, r4 = kHeadDim / 4;
         const int n4 = q4 + (has_new ? 2 * r4 : 0);
         if (!gather4<(q4 + 2 * r4 + kT - 1) / kT>(in, n4, reinterpret_cast<float4 *>(ar.qs), wt(),
-                                                  cm.flags, [&](int p, int &s, int &d) {
+                                                  flag_set(), [&](int p, int &s, int &d) {
               if (p < q4) {
                 s = g * q4 + p;
                 d = p;
@@ -1678,7 +1686,7 @@ struct Roles {
       static_assert(kPer <= 8, "partial gather pass");
       const Slots in = s_part(l, t);
       const int n4 = GROUP * C * kRec4;
-      if (!gather4<kPer>(in, n4, reinterpret_cast<float4 *>(parts), wt(), cm.flags, [&](int p, int &s, int &d) {
+      if (!gather4<kPer>(in, n4, reinterpret_cast<float4 *>(parts), wt(), flag_set(), [&](int p, int &s, int &d) {
             const int rec = p / kRec4, k = p % kRec4;
             const int j = rec / C, c = rec % C;
             s = ((g * GROUP + j) * kAttnMaxChunks + c) * kRec4 + k;
@@ -1870,7 +1878,7 @@ struct Roles {
       clock.mark(0);
       if (ok) rd.sums(xa, part);
       clock.mark(1);
-      if (!block_all(ok, cm.flags)) return false;
+      if (!block_all(ok, flag_set())) return false;
       // Wave w finishes rows w and w + kW (at most kMaxRows = 2 kW rows): the
       // slice sums of both rows are read at once and reduced together
       // (wave_sum_multi: row w's sum in lane 0, row w + kW's in lane 1).
