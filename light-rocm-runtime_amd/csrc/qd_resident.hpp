@@ -86,6 +86,8 @@ struct ResidentArgs {
   int attn_parts;               // chunk geometry: attn_chunks(length, attn_parts, kAttnGrain)
   int xcd_place;                // RolePlan::xcd_place
   int weights_dtype;            // kWeights*: storage of the layers' matrices (picks the instance)
+  int attn_long;                // 1: every chunk of every token is longer than one block
+                                //   (attn_single_block false), picking the tiles-only instance
 };
 
 // Argmax partial tags: epoch << kTagSeqBits | (token * (5 * layers + 1) + stage + 1).

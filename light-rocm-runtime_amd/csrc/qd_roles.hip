@@ -1439,6 +1439,10 @@ struct Roles {
     }
   }
 
+  // kLongOnly: every chunk of the launch is longer than one block, so the
+  // one-block (vector ALU) form is left out of this instance (the MFMA
+  // tiles' code then gets the role's registers to itself).
+  template <bool kLongOnly>
   __device__ void run_attn() {
     static_assert(GROUP <= kAttnMaxGroup, "an attention tile takes up to 8 heads per KV group");
     AttnRegion &ar = *reinterpret_cast<AttnRegion *>(region);
@@ -1522,7 +1526,7 @@ struct Roles {
             }))
           return false;
         if (first_unit) clock.lap(2 * kRoleAttn);
-        if (attn_single_block(cl)) {
+        if (!kLongOnly && attn_single_block(cl)) {
           // One block (the window, loaded ahead): wave h takes head h, its
           // query in registers, and stores the head's record (m, l, two pad
           // words, acc[64]) itself: one contiguous 256-byte store of acc and
@@ -1913,6 +1917,9 @@ struct Roles {
 
 // Each role's loop is its own (non-inlined) function so the register
 // allocator sizes each role separately instead of one body holding all five.
+// kRoleAttnLong: the attention role of a launch whose chunks all exceed one
+// block (ResidentArgs::attn_long).
+constexpr int kRoleAttnLong = kRoleCount;
 template <int H, int I, int NQ, int NKV, bool kProfile, typename W, int kRole>
 __device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank, int nrole, int wg) {
   // The launch arguments, copied with scalar loads from the kernel's
@@ -1940,7 +1947,8 @@ __device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank
                                    __builtin_amdgcn_readfirstlane(nrole),
                                    __builtin_amdgcn_readfirstlane(wg));
   if constexpr (kRole == kRoleQkv) r.run_qkv();
-  if constexpr (kRole == kRoleAttn) r.run_attn();
+  if constexpr (kRole == kRoleAttn) r.template run_attn<false>();
+  if constexpr (kRole == kRoleAttnLong) r.template run_attn<true>();
   if constexpr (kRole == kRoleO) r.run_o();
   if constexpr (kRole == kRoleGate) r.run_gate();
   if constexpr (kRole == kRoleDown) r.run_down();
@@ -2003,7 +2011,10 @@ __global__ __launch_bounds__(kT, 1) void roles_kernel(ResidentArgs a) {
       run_role<H, I, NQ, NKV, kProfile, W, kRoleQkv>(kernarg, rank, nrole, wg);
       break;
     case kRoleAttn:
-      run_role<H, I, NQ, NKV, kProfile, W, kRoleAttn>(kernarg, rank, nrole, wg);
+      if (a.attn_long)
+        run_role<H, I, NQ, NKV, kProfile, W, kRoleAttnLong>(kernarg, rank, nrole, wg);
+      else
+        run_role<H, I, NQ, NKV, kProfile, W, kRoleAttn>(kernarg, rank, nrole, wg);
       break;
     case kRoleO:
       run_role<H, I, NQ, NKV, kProfile, W, kRoleO>(kernarg, rank, nrole, wg);
