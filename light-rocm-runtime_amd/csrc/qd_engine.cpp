@@ -667,12 +667,15 @@ struct qd_engine {
     for (int r = 0; r < 3; ++r) ra.group_cus[r] = plan.group_cus[r];
     ra.xcd_place = plan.xcd_place;
     ra.attn_parts = attn_parts;
-    // The first token attends to the fewest positions; a chunk never shrinks
-    // as the context grows.
-    ra.attn_long = qd::attn_chunk_len(static_cast<int>(positions[seq]) + 1, attn_parts, qd::kAttnGrain) >
-                           qd::kAttnPass
-                       ? 1
-                       : 0;
+    // The first token attends to the fewest positions and the last to the
+    // most; a chunk never shrinks as the context grows.
+    {
+      const int first = static_cast<int>(positions[seq]) + 1;
+      const int last = static_cast<int>(std::min<uint64_t>(uint64_t(positions[seq]) + max_tokens, CAP));
+      ra.attn_mode = qd::attn_chunk_len(first, attn_parts, qd::kAttnGrain) > qd::kAttnPass ? 1
+                     : qd::attn_chunk_len(last, attn_parts, qd::kAttnGrain) <= qd::kAttnPass ? 2
+                                                                                             : 0;
+    }
     ra.weights_dtype = wdtype;
     // Error word and tickets zero, token 0's hand-off slots empty (all bits
     // set), the tag arena zero when the epoch counter wrapped.

@@ -86,8 +86,9 @@ struct ResidentArgs {
   int attn_parts;               // chunk geometry: attn_chunks(length, attn_parts, kAttnGrain)
   int xcd_place;                // RolePlan::xcd_place
   int weights_dtype;            // kWeights*: storage of the layers' matrices (picks the instance)
-  int attn_long;                // 1: every chunk of every token is longer than one block
-                                //   (attn_single_block false), picking the tiles-only instance
+  int attn_mode;                // attention role instance: 0 both chunk forms, 1 every chunk
+                                //   of every token longer than one block (tiles only), 2 none
+                                //   (one-block form only)
 };
 
 // Argmax partial tags: epoch << kTagSeqBits | (token * (5 * layers + 1) + stage + 1).

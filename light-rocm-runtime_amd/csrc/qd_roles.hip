@@ -1439,10 +1439,12 @@ struct Roles {
     }
   }
 
-  // kLongOnly: every chunk of the launch is longer than one block, so the
-  // one-block (vector ALU) form is left out of this instance (the MFMA
-  // tiles' code then gets the role's registers to itself).
-  template <bool kLongOnly>
+  // kMode (ResidentArgs::attn_mode): 0, both chunk forms; 1, every chunk of
+  // the launch is longer than one block, so the one-block (vector ALU) form
+  // is left out of the instance; 2, no chunk is, so the MFMA tiles and their
+  // register window are left out. Each instance's code then gets the role's
+  // registers to itself.
+  template <int kMode>
   __device__ void run_attn() {
     static_assert(GROUP <= kAttnMaxGroup, "an attention tile takes up to 8 heads per KV group");
     AttnRegion &ar = *reinterpret_cast<AttnRegion *>(region);
@@ -1463,7 +1465,7 @@ struct Roles {
       const int begin = rr * cl, end = min(length, begin + cl);
       attn_dma(l, g, begin, min(end, begin + kAttnCap), ar);
       const int t0 = begin + kAttnCap + wv * kAttnTile;
-      if (t0 < end) {
+      if (kMode != 2 && t0 < end) {
         const Coherent kc(kv_layer(a.k_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
         const Coherent vc(kv_layer(a.v_cache, l), static_cast<uint32_t>(a.capacity) * KVD * 4u);
         const int pk = min(t0 + (lane & 31), end - 1);
@@ -1526,7 +1528,13 @@ struct Roles {
             }))
           return false;
         if (first_unit) clock.lap(2 * kRoleAttn);
-        if (!kLongOnly && attn_single_block(cl)) {
+        if constexpr (kMode == 2) {
+          if (!attn_single_block(cl)) {  // the host's mode would be wrong
+            if (threadIdx.x == 0) atomicOr(a.error, kResidentPlanOverfill);
+            return false;
+          }
+        }
+        if (kMode == 2 || (kMode == 0 && attn_single_block(cl))) {
           // One block (the window, loaded ahead): wave h takes head h, its
           // query in registers, and stores the head's record (m, l, two pad
           // words, acc[64]) itself: one contiguous 256-byte store of acc and
@@ -1917,9 +1925,9 @@ struct Roles {
 
 // Each role's loop is its own (non-inlined) function so the register
 // allocator sizes each role separately instead of one body holding all five.
-// kRoleAttnLong: the attention role of a launch whose chunks all exceed one
-// block (ResidentArgs::attn_long).
-constexpr int kRoleAttnLong = kRoleCount;
+// kRoleAttnLong / kRoleAttnShort: the attention role of a launch whose
+// chunks all exceed one block / all fit one (ResidentArgs::attn_mode).
+constexpr int kRoleAttnLong = kRoleCount, kRoleAttnShort = kRoleCount + 1;
 template <int H, int I, int NQ, int NKV, bool kProfile, typename W, int kRole>
 __device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank, int nrole, int wg) {
   // The launch arguments, copied with scalar loads from the kernel's
@@ -1947,8 +1955,9 @@ __device__ __attribute__((noinline)) void run_role(const void *kernarg, int rank
                                    __builtin_amdgcn_readfirstlane(nrole),
                                    __builtin_amdgcn_readfirstlane(wg));
   if constexpr (kRole == kRoleQkv) r.run_qkv();
-  if constexpr (kRole == kRoleAttn) r.template run_attn<false>();
-  if constexpr (kRole == kRoleAttnLong) r.template run_attn<true>();
+  if constexpr (kRole == kRoleAttn) r.template run_attn<0>();
+  if constexpr (kRole == kRoleAttnLong) r.template run_attn<1>();
+  if constexpr (kRole == kRoleAttnShort) r.template run_attn<2>();
   if constexpr (kRole == kRoleO) r.run_o();
   if constexpr (kRole == kRoleGate) r.run_gate();
   if constexpr (kRole == kRoleDown) r.run_down();
@@ -2011,8 +2020,10 @@ __global__ __launch_bounds__(kT, 1) void roles_kernel(ResidentArgs a) {
       run_role<H, I, NQ, NKV, kProfile, W, kRoleQkv>(kernarg, rank, nrole, wg);
       break;
     case kRoleAttn:
-      if (a.attn_long)
+      if (a.attn_mode == 1)
         run_role<H, I, NQ, NKV, kProfile, W, kRoleAttnLong>(kernarg, rank, nrole, wg);
+      else if (a.attn_mode == 2)
+        run_role<H, I, NQ, NKV, kProfile, W, kRoleAttnShort>(kernarg, rank, nrole, wg);
       else
         run_role<H, I, NQ, NKV, kProfile, W, kRoleAttn>(kernarg, rank, nrole, wg);
       break;
