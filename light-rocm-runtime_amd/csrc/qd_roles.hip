@@ -62,10 +62,10 @@ constexpr int kAttnCap = 256;     // positions of an attention window staged in 
 
 // Register slots per wave: row-pair units of the K=H roles, rows of DOWN.
 #ifndef QD_SLOTS_Q
-#define QD_SLOTS_Q 2
+#define QD_SLOTS_Q 3
 #endif
 #ifndef QD_SLOTS_O
-#define QD_SLOTS_O 4
+#define QD_SLOTS_O 5
 #endif
 #ifndef QD_SLOTS_G
 #define QD_SLOTS_G 3
