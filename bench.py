@@ -63,10 +63,10 @@ WEIGHT_BYTES = 1_976_131_072
 # the factors a 1 GiB device copy gives in the same profile
 # (profiles/roles_kernel_config2.md).
 # Re-measured when a kernel changes; None where no measurement exists.
-RESIDENT_TRAFFIC_PER_TOKEN = 2_006_754_613
-# The role-split kernel on a 64-token launch of the config-3 workload
-# (context 4065..4128; profiles/roles_kernel_config3.md).
-RESIDENT_TRAFFIC_PER_TOKEN_LONG = 2_114_254_998
+RESIDENT_TRAFFIC_PER_TOKEN = 2_005_670_715
+# The role-split kernel on the bench's own 32-token launch of the config-3
+# workload (context 4065..4096; profiles/roles_kernel_config3.md).
+RESIDENT_TRAFFIC_PER_TOKEN_LONG = 2_102_114_363
 
 
 def step_bytes(length: int) -> int:
