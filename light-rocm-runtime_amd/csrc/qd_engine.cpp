@@ -31,6 +31,16 @@
 #include "qd_resident.hpp"
 #include "qd_rng.hpp"
 
+// Stream-K workgroups per CU of the prompt's QKV and down GEMMs (0:
+// split-K). The O GEMM keeps split-K 2: its 224 workgroups already give
+// every CU one equal share.
+#ifndef QD_PREFILL_SK_QKV
+#define QD_PREFILL_SK_QKV 1
+#endif
+#ifndef QD_PREFILL_SK_DOWN
+#define QD_PREFILL_SK_DOWN 2
+#endif
+
 namespace {
 
 constexpr uint32_t kAbiVersion = 4;
@@ -170,8 +180,23 @@ struct qd_engine {
   static constexpr size_t kPrefillRows = 512;
   float *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_attn = nullptr,
         *pf_act = nullptr, *pf_split = nullptr;
-  // Split-K factors of the narrow GEMMs (QKV, O, down) so they fill the CUs.
+  // Split-K factors of the narrow GEMMs (QKV, O, down) so they fill the CUs,
+  // used when stream-K is off (sk_target 0).
   static constexpr int kSplitQkv = 2, kSplitO = 2, kSplitDown = 4;
+  // Stream-K for the QKV and down GEMMs: up to per_cu workgroups per CU
+  // (QD_PREFILL_SK_QKV / QD_PREFILL_SK_DOWN), each taking at least
+  // kSkMinSlices K slices of 32, so every CU gets an equal share of the
+  // (tile, slice) work; pf_split_floats is the partial workspace that any
+  // prompt chunk of up to kPrefillRows rows needs.
+  static constexpr int kSkMinSlices = 8;
+  int cu_count = 0;
+  size_t pf_split_floats = 0;
+  int sk_groups(int m, int n, int k, int per_cu) const {
+    if (per_cu <= 0 || cu_count <= 0) return 0;
+    const long long total = static_cast<long long>((m + 63) / 64) * ((n + 63) / 64) * (k / 32);
+    return static_cast<int>(
+        std::min<long long>(static_cast<long long>(per_cu) * cu_count, std::max<long long>(1, total / kSkMinSlices)));
+  }
   uint32_t *pf_tokens = nullptr;
   // Batched-step workspace (allocated on the first batched step): rows of
   // up to kBatchRows sequences, attention and split-K partials, arrival
@@ -552,7 +577,16 @@ struct qd_engine {
       pf_attn = alloc<float>(kPrefillRows * QD);
       pf_act = alloc<float>(kPrefillRows * I);
       pf_tokens = alloc<uint32_t>(kPrefillRows);
-      pf_split = alloc<float>(kPrefillRows * std::max({kSplitQkv * QKV, kSplitO * H, kSplitDown * H}));
+      pf_split_floats = kPrefillRows * std::max({kSplitQkv * QKV, kSplitO * H, kSplitDown * H});
+      const int shapes[2][3] = {{int(QKV), int(H), QD_PREFILL_SK_QKV}, {int(H), int(I), QD_PREFILL_SK_DOWN}};
+      for (int rows = 1; rows <= int(kPrefillRows); ++rows)
+        for (const auto &sh : shapes) {
+          const int g = sk_groups(rows, sh[0], sh[1], sh[2]);
+          if (g > 0)
+            pf_split_floats = std::max(pf_split_floats, size_t(qd::gemm_streamk_slots(rows, sh[0], sh[1], g)) *
+                                                            size_t(rows) * size_t(sh[0]));
+        }
+      pf_split = alloc<float>(pf_split_floats);
     }
     check(hipMemcpyAsync(pf_tokens, tokens, size_t(n) * 4, hipMemcpyHostToDevice, stream), "H2D");
     const int h = int(H), in = int(I), qkv = int(QKV), qd = int(QD);
@@ -583,7 +617,8 @@ struct qd_engine {
         rope.k_cache = kc;
         rope.v_cache = vc;
         return qd::launch_gemm_nt(stream, pf_xn, h, w.wqkv, h, pf_qkv, qkv, n, qkv, h, qd::kGemmBias,
-                                  w.bqkv, kSplitQkv, pf_split, &rope);
+                                  w.bqkv, kSplitQkv, pf_split, &rope, sk_groups(n, qkv, h, QD_PREFILL_SK_QKV),
+                                  pf_split_floats);
       });
       span(kPAttn, "attention", [&] {
         return qd::launch_attention_prefill(stream, pf_qkv, n, pos0, nq, nkv, kc, vc, pf_attn);
@@ -610,7 +645,8 @@ struct qd_engine {
         }
         return qd::launch_gemm_nt(stream, pf_act, in, w.wd, in, pf_h, h, n, h, in,
                                   qd::kGemmAccumulate, nullptr, kSplitDown, pf_split,
-                                  l + 1 < L ? &norm : nullptr);
+                                  l + 1 < L ? &norm : nullptr, sk_groups(n, h, in, QD_PREFILL_SK_DOWN),
+                                  pf_split_floats);
       });
     }
   }
@@ -930,6 +966,7 @@ qd_status qd_engine_create(const qd_config *config, qd_engine **out) {
     // lowers the polls a hand-off wait makes before it gives up (tests
     // force the give-up path with it).
     const int cus = qd::device_cu_count(c.device);
+    e->cu_count = std::max(cus, 0);
     {
       qd::RolePlan cap_plan{};
       if (cus >= 64 && cus <= qd::kMaxRoleGrid &&

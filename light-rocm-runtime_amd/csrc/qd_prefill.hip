@@ -74,25 +74,27 @@ __device__ __forceinline__ void gemm_lds_barrier() { asm volatile("s_waitcnt lgk
 // rows of that range and its last 32 wu's (W2), so waves (wr, 0) hold the
 // gate sums and waves (wr, 1) the up sums of the same elements; the up sums
 // cross through LDS and waves (wr, 0) store silu_mul(gate, up).
-__global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict__ A, int lda,
-                                                         const float *__restrict__ W,
-                                                         const float *__restrict__ W2, int ldw,
-                                                         float *__restrict__ C, int ldc, int m,
-                                                         int n, int k, int mode,
-                                                         const float *__restrict__ bias) {
-  __shared__ __attribute__((aligned(16))) float stage_lds[kStages * kStageFloats];
+// Stream-K (sk_groups > 0, a one-dimensional grid of sk_groups workgroups):
+// the (tile, slice) iterations, tile-major, are cut into sk_groups equal
+// contiguous ranges. Workgroup g takes range [g T / G, (g + 1) T / G) and
+// writes one plain partial per tile it touches, to partial slot g -
+// sk_owner(first iteration of the tile) (C + slot * m * ldc); the reduction
+// sums a tile's slots in slot order. Every CU then gets the same number of
+// slices whatever the tile count.
+__host__ __device__ inline int sk_owner(long long it, int groups, long long total) {
+  return static_cast<int>(((it + 1) * groups - 1) / total);
+}
+
+// One tile's product over K slices [s_begin, s_end) into C (plain, bias or
+// accumulate per mode; SwiGLU as described above).
+__device__ __forceinline__ void gemm_tile(float *stage_lds, const float *__restrict__ A, int lda,
+                                          const float *__restrict__ W, const float *__restrict__ W2,
+                                          int ldw, float *__restrict__ C, int ldc, int m, int n, int mode,
+                                          const float *__restrict__ bias, bool add_bias, int tx, int m0,
+                                          int n0, int s_begin, int s_end) {
   const int lane = lane_id();
   const int w = wave_id();
   const int wr = w >> 1, wc = w & 1;
-  const int m0 = blockIdx.y * kTileM, n0 = blockIdx.x * kTileN;
-  const int split = gridDim.z;
-  const int slices_all = k / kTileK;
-  const int s_begin = static_cast<int>(blockIdx.z) * slices_all / split;
-  const int s_end = (static_cast<int>(blockIdx.z) + 1) * slices_all / split;
-  if (split > 1) {
-    C += static_cast<size_t>(blockIdx.z) * m * ldc;
-    mode = kGemmStore;
-  }
   const int slices = s_end - s_begin;
   // DMA of slice s into stage b: instruction i of a tile covers rows
   // 8 i .. 8 i + 7; this wave issues instructions w and w + 4 of the A tile
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict
       const int ra = min(m0 + 8 * i + drow, m - 1);
       const float *wrow;
       if (mode == kGemmSwiGLU) {
-        const int j = blockIdx.x * (kTileN / 2) + 8 * (i & 3) + drow;
+        const int j = tx * (kTileN / 2) + 8 * (i & 3) + drow;
         wrow = (i < 4 ? W : W2) + static_cast<size_t>(j) * ldw;
       } else {
         wrow = W + static_cast<size_t>(min(n0 + 8 * i + drow, n - 1)) * ldw;
@@ -162,7 +164,7 @@ __global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict
     }
     gemm_lds_barrier();
     if (wc == 0) {
-      const int col = blockIdx.x * (kTileN / 2) + (lane & 31);
+      const int col = tx * (kTileN / 2) + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wr * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict
   }
   const int col = n0 + wc * 32 + (lane & 31);
   if (col >= n) return;
-  const float bv = mode == kGemmBias && split == 1 ? bias[col] : 0.f;
+  const float bv = mode == kGemmBias && add_bias ? bias[col] : 0.f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int row = m0 + wr * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
@@ -187,17 +189,68 @@ __global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict
   }
 }
 
-// C[r][c] (op)= sum_z part[z][r][c] (+ bias[c]) for the split-K partials.
+__global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict__ A, int lda,
+                                                         const float *__restrict__ W,
+                                                         const float *__restrict__ W2, int ldw,
+                                                         float *__restrict__ C, int ldc, int m,
+                                                         int n, int k, int mode,
+                                                         const float *__restrict__ bias, int sk_groups) {
+  __shared__ __attribute__((aligned(16))) float stage_lds[kStages * kStageFloats];
+  const int slices_all = k / kTileK;
+  if (sk_groups > 0) {
+    const int tiles_n = (n + kTileN - 1) / kTileN;
+    const long long total = static_cast<long long>((m + kTileM - 1) / kTileM) * tiles_n * slices_all;
+    const int g = blockIdx.x;
+    const long long it1 = (g + 1) * total / sk_groups;
+    for (long long it = g * total / sk_groups; it < it1;) {
+      const int tile = static_cast<int>(it / slices_all);
+      const long long first = static_cast<long long>(tile) * slices_all;
+      const int s_begin = static_cast<int>(it - first);
+      const int s_end = static_cast<int>(min(it1 - first, static_cast<long long>(slices_all)));
+      const int slot = g - sk_owner(first, sk_groups, total);
+      gemm_lds_barrier();  // the previous tile's last stage reads are done
+      gemm_tile(stage_lds, A, lda, W, W2, ldw, C + static_cast<size_t>(slot) * m * ldc, ldc, m, n, kGemmStore,
+                bias, false, tile % tiles_n, (tile / tiles_n) * kTileM, (tile % tiles_n) * kTileN, s_begin,
+                s_end);
+      it = first + slices_all;
+    }
+    return;
+  }
+  const int split = gridDim.z;
+  const int s_begin = static_cast<int>(blockIdx.z) * slices_all / split;
+  const int s_end = (static_cast<int>(blockIdx.z) + 1) * slices_all / split;
+  if (split > 1) {
+    C += static_cast<size_t>(blockIdx.z) * m * ldc;
+    mode = kGemmStore;
+  }
+  gemm_tile(stage_lds, A, lda, W, W2, ldw, C, ldc, m, n, mode, bias, split == 1, blockIdx.x,
+            blockIdx.y * kTileM, blockIdx.x * kTileN, s_begin, s_end);
+}
+
+// Partial slots of a tile's product: split (classic split-K), or with
+// stream-K (sk_groups > 0) the workgroups whose ranges meet the tile of
+// element (r, c).
+__device__ __forceinline__ int partial_count(int split, int sk_groups, int r, int c, int m, int n, int k) {
+  if (sk_groups <= 0) return split;
+  const int slices_all = k / kTileK, tiles_n = (n + kTileN - 1) / kTileN;
+  const long long total = static_cast<long long>((m + kTileM - 1) / kTileM) * tiles_n * slices_all;
+  const long long first = static_cast<long long>((r / kTileM) * tiles_n + c / kTileN) * slices_all;
+  return sk_owner(first + slices_all - 1, sk_groups, total) - sk_owner(first, sk_groups, total) + 1;
+}
+
+// C[r][c] (op)= sum_z part[z][r][c] (+ bias[c]) for the split-K partials
+// (partial_count of them for the element's tile).
 __global__ __launch_bounds__(kBlock) void gemm_reduce_kernel(const float *__restrict__ part,
-                                                             int split, float *__restrict__ C,
-                                                             int ldc, int m, int n, int mode,
-                                                             const float *__restrict__ bias) {
+                                                             int split, int sk_groups, int k,
+                                                             float *__restrict__ C, int ldc, int m, int n,
+                                                             int mode, const float *__restrict__ bias) {
   const size_t total = static_cast<size_t>(m) * n;
   for (size_t e = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; e < total;
        e += static_cast<size_t>(gridDim.x) * kBlock) {
     const int r = static_cast<int>(e / n), c = static_cast<int>(e % n);
+    const int parts = partial_count(split, sk_groups, r, c, m, n, k);
     float v = part[static_cast<size_t>(r) * ldc + c];
-    for (int z = 1; z < split; ++z) v += part[(static_cast<size_t>(z) * m + r) * ldc + c];
+    for (int z = 1; z < parts; ++z) v += part[(static_cast<size_t>(z) * m + r) * ldc + c];
     float *dst = C + static_cast<size_t>(r) * ldc + c;
     if (mode == kGemmAccumulate)
       *dst += v;
@@ -287,15 +340,16 @@ __global__ __launch_bounds__(kBlock) void rope_kv_rows_kernel(float *__restrict_
 // rmsnorm_rows_kernel / rope_kv_rows_kernel, so the results are the same
 // bits as those kernels after gemm_reduce_kernel.
 __global__ __launch_bounds__(kBlock) void gemm_reduce_rows_kernel(const float *__restrict__ part, int split,
-                                                                  float *__restrict__ C, int ldc, int m, int n,
-                                                                  int mode, const float *__restrict__ bias,
-                                                                  RowEpilogue epi) {
+                                                                  int sk_groups, int k, float *__restrict__ C,
+                                                                  int ldc, int m, int n, int mode,
+                                                                  const float *__restrict__ bias, RowEpilogue epi) {
   __shared__ float red[kWavesPerBlock];
   const int r = blockIdx.x;
   float *row = C + static_cast<size_t>(r) * ldc;
   for (int c = threadIdx.x; c < n; c += kBlock) {
+    const int parts = partial_count(split, sk_groups, r, c, m, n, k);
     float v = part[static_cast<size_t>(r) * ldc + c];
-    for (int z = 1; z < split; ++z) v += part[(static_cast<size_t>(z) * m + r) * ldc + c];
+    for (int z = 1; z < parts; ++z) v += part[(static_cast<size_t>(z) * m + r) * ldc + c];
     if (mode == kGemmAccumulate)
       row[c] += v;
     else
@@ -532,26 +586,47 @@ __global__ __launch_bounds__(kBlock) void attention_prefill_kernel(
 
 }  // namespace
 
+int gemm_streamk_slots(int m, int n, int k, int groups) {
+  if (m <= 0 || n <= 0 || k < kTileK || groups <= 0) return 0;
+  const int slices_all = k / kTileK, tiles_n = (n + kTileN - 1) / kTileN;
+  const int tiles = ((m + kTileM - 1) / kTileM) * tiles_n;
+  const long long total = static_cast<long long>(tiles) * slices_all;
+  int most = 0;
+  for (int t = 0; t < tiles; ++t) {
+    const long long first = static_cast<long long>(t) * slices_all;
+    most = std::max(most, sk_owner(first + slices_all - 1, groups, total) - sk_owner(first, groups, total) + 1);
+  }
+  return most;
+}
+
 hipError_t launch_gemm_nt(hipStream_t s, const float *A, int lda, const float *W, int ldw,
                           float *C, int ldc, int m, int n, int k, GemmMode mode,
-                          const float *bias, int split, float *workspace, const RowEpilogue *epi) {
-  if (k % kTileK != 0 || m <= 0 || n <= 0 || split < 1 || split > k / kTileK ||
-      (split > 1 && !workspace))
+                          const float *bias, int split, float *workspace, const RowEpilogue *epi,
+                          int sk_groups, size_t workspace_floats) {
+  if (k % kTileK != 0 || m <= 0 || n <= 0 || split < 1 || split > k / kTileK || sk_groups < 0 ||
+      ((split > 1 || sk_groups > 0) && !workspace))
     return hipErrorInvalidValue;
-  // A row epilogue runs in the split-K reduction, one workgroup per row.
-  if (epi && (split < 2 || ldc != n || (epi->kind == kRowNorm && (n != 896 || !epi->y || !epi->gain)) ||
+  // Stream-K: every tile's partial slots must fit the workspace.
+  if (sk_groups > 0 &&
+      static_cast<size_t>(gemm_streamk_slots(m, n, k, sk_groups)) * m * ldc > workspace_floats)
+    return hipErrorInvalidValue;
+  const bool partials = split > 1 || sk_groups > 0;
+  // A row epilogue runs in the partials' reduction, one workgroup per row.
+  if (epi && (!partials || ldc != n || (epi->kind == kRowNorm && (n != 896 || !epi->y || !epi->gain)) ||
               (epi->kind == kRowRope && n != (epi->nq + 2 * epi->nkv) * kHeadDim)))
     return hipErrorInvalidValue;
   if (mode == kGemmSwiGLU) return hipErrorInvalidValue;
-  const dim3 grid((n + kTileN - 1) / kTileN, (m + kTileM - 1) / kTileM, split);
-  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, W, nullptr, ldw, split > 1 ? workspace : C, ldc, m, n, k,
-                                         mode, bias);
-  if (split > 1 && epi) {
-    gemm_reduce_rows_kernel<<<m, kBlock, 0, s>>>(workspace, split, C, ldc, m, n, mode, bias, *epi);
-  } else if (split > 1) {
+  const dim3 grid = sk_groups > 0 ? dim3(sk_groups, 1, 1)
+                                  : dim3((n + kTileN - 1) / kTileN, (m + kTileM - 1) / kTileM, split);
+  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, W, nullptr, ldw, partials ? workspace : C, ldc, m, n, k,
+                                         mode, bias, sk_groups);
+  if (partials && epi) {
+    gemm_reduce_rows_kernel<<<m, kBlock, 0, s>>>(workspace, split, sk_groups, k, C, ldc, m, n, mode, bias,
+                                                 *epi);
+  } else if (partials) {
     const size_t total = static_cast<size_t>(m) * n;
     const int blocks = static_cast<int>(std::min<size_t>((total + kBlock - 1) / kBlock, 4096));
-    gemm_reduce_kernel<<<blocks, kBlock, 0, s>>>(workspace, split, C, ldc, m, n, mode, bias);
+    gemm_reduce_kernel<<<blocks, kBlock, 0, s>>>(workspace, split, sk_groups, k, C, ldc, m, n, mode, bias);
   }
   return hipGetLastError();
 }
@@ -589,7 +664,7 @@ hipError_t launch_gemm_swiglu(hipStream_t s, const float *A, int lda, const floa
                               int ldw, float *act, int ldc, int m, int inter, int k) {
   if (k % kTileK != 0 || m <= 0 || inter <= 0 || inter % (kTileN / 2) != 0) return hipErrorInvalidValue;
   const dim3 grid(inter / (kTileN / 2), (m + kTileM - 1) / kTileM, 1);
-  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, wg, wu, ldw, act, ldc, m, 2 * inter, k, kGemmSwiGLU, nullptr);
+  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, wg, wu, ldw, act, ldc, m, 2 * inter, k, kGemmSwiGLU, nullptr, 0);
   return hipGetLastError();
 }
 

@@ -32,12 +32,21 @@ struct RowEpilogue {
 // C[m][n] (row stride ldc) for A [m][k] (stride lda) and W [n][k] (stride
 // ldw), all FP32 row-major. m, n any size (edges masked); k a multiple of 32.
 // split > 1 divides k over that many workgroup slices whose partials go to
-// workspace (split * m * ldc floats) and are summed in a fixed order. epi
-// (split > 1, ldc == n) runs a row epilogue in that reduction.
+// workspace (split * m * ldc floats) and are summed in a fixed order.
+// sk_groups > 0 (stream-K) instead deals the tiles' 32-wide K slices to
+// sk_groups workgroups in equal contiguous ranges; a tile's partials (one per
+// workgroup meeting it, at most gemm_streamk_slots(m, n, k, sk_groups)) go
+// to workspace (that many times m * ldc floats, within workspace_floats) and
+// are summed in a fixed order. epi (partials, ldc == n) runs a row epilogue
+// in that reduction.
 hipError_t launch_gemm_nt(hipStream_t s, const float *A, int lda, const float *W, int ldw,
                           float *C, int ldc, int m, int n, int k, GemmMode mode,
                           const float *bias, int split = 1, float *workspace = nullptr,
-                          const RowEpilogue *epi = nullptr);
+                          const RowEpilogue *epi = nullptr, int sk_groups = 0, size_t workspace_floats = 0);
+
+// Partial slots a stream-K launch of sk_groups workgroups needs (0 for an
+// invalid shape).
+int gemm_streamk_slots(int m, int n, int k, int sk_groups);
 
 // out[r] = embed[tokens[r]] for r < rows (hidden floats each).
 hipError_t launch_embed_rows(hipStream_t s, const float *embed, const uint32_t *tokens, int rows,
