@@ -227,6 +227,24 @@ __global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict
             blockIdx.y * kTileM, blockIdx.x * kTileN, s_begin, s_end);
 }
 
+// Sum of the first `parts` partials of element e (part + z * stride + e), in
+// slot order: the first kBatch are requested before any is added (one round
+// trip), later ones one batch at a time.
+__device__ __forceinline__ float sum_partials(const float *__restrict__ part, size_t stride, size_t e, int parts) {
+  constexpr int kBatch = 8;
+  float v = 0.f;
+  for (int z0 = 0; z0 < parts; z0 += kBatch) {
+    float pv[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) pv[j] = z0 + j < parts ? part[static_cast<size_t>(z0 + j) * stride + e] : 0.f;
+    if (z0 == 0) v = pv[0];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      if ((z0 > 0 || j > 0) && z0 + j < parts) v += pv[j];
+  }
+  return v;
+}
+
 // Partial slots of a tile's product: split (classic split-K), or with
 // stream-K (sk_groups > 0) the workgroups whose ranges meet the tile of
 // element (r, c).
@@ -249,8 +267,7 @@ __global__ __launch_bounds__(kBlock) void gemm_reduce_kernel(const float *__rest
        e += static_cast<size_t>(gridDim.x) * kBlock) {
     const int r = static_cast<int>(e / n), c = static_cast<int>(e % n);
     const int parts = partial_count(split, sk_groups, r, c, m, n, k);
-    float v = part[static_cast<size_t>(r) * ldc + c];
-    for (int z = 1; z < parts; ++z) v += part[(static_cast<size_t>(z) * m + r) * ldc + c];
+    const float v = sum_partials(part, static_cast<size_t>(m) * ldc, static_cast<size_t>(r) * ldc + c, parts);
     float *dst = C + static_cast<size_t>(r) * ldc + c;
     if (mode == kGemmAccumulate)
       *dst += v;
@@ -348,8 +365,7 @@ __global__ __launch_bounds__(kBlock) void gemm_reduce_rows_kernel(const float *_
   float *row = C + static_cast<size_t>(r) * ldc;
   for (int c = threadIdx.x; c < n; c += kBlock) {
     const int parts = partial_count(split, sk_groups, r, c, m, n, k);
-    float v = part[static_cast<size_t>(r) * ldc + c];
-    for (int z = 1; z < parts; ++z) v += part[(static_cast<size_t>(z) * m + r) * ldc + c];
+    const float v = sum_partials(part, static_cast<size_t>(m) * ldc, static_cast<size_t>(r) * ldc + c, parts);
     if (mode == kGemmAccumulate)
       row[c] += v;
     else
