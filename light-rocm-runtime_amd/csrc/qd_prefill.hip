@@ -428,7 +428,9 @@ __device__ __forceinline__ void attention_prefill_block(
   const int w = wave_id();
   const int lane = lane_id();
   const int lr = lane & 15, lg = lane >> 4;
-  const float scale = rsqrtf(static_cast<float>(kHeadDim));
+  // Scores in base-2 units, s log2(e) / sqrt(64), so each softmax
+  // exponential is one v_exp_f32 (2^x): e^(s / 8 - m) = 2^(s log2(e) / 8 - m').
+  const float scale = 0.18033688011112042f;  // log2(e) / sqrt(64)
   const int last_row = min(rows, r0 + kQBlock) - 1;
   const int keys = pos0 + last_row + 1;  // causal extent of the block
   const int kblocks = (keys + kKBlock - 1) / kKBlock;
@@ -519,9 +521,9 @@ __device__ __forceinline__ void attention_prefill_block(
       float p0 = 0.f, p1 = 0.f;
       corr[r] = 1.f;
       if (m_new != -INFINITY) {
-        p0 = expf(sv[0] - m_new);
-        p1 = expf(sv[1] - m_new);
-        corr[r] = expf(m[r] - m_new);
+        p0 = __builtin_amdgcn_exp2f(sv[0] - m_new);
+        p1 = __builtin_amdgcn_exp2f(sv[1] - m_new);
+        corr[r] = __builtin_amdgcn_exp2f(m[r] - m_new);
       }
       l[r] = fmaf(l[r], corr[r], row16_sum(p0 + p1));
       m[r] = m_new;
@@ -572,7 +574,7 @@ __device__ __forceinline__ void attention_prefill_block(
 #pragma unroll
       for (int v = 0; v < kWavesPerBlock; ++v) {
         const float mv = sh.ml[v][q][0];
-        const float f = mv == -INFINITY ? 0.f : expf(mv - mx);
+        const float f = mv == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mv - mx);
         den = fmaf(f, sh.ml[v][q][1], den);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = fmaf(f, sh.o[v][q][d0 + e], acc[e]);
