@@ -335,8 +335,9 @@ __device__ __forceinline__ float row16_max(float v) {
 //                                   LDS to become MFMA A / B operands.
 // The four wave partials are merged into one record (m, l, acc[64]) per
 // head; the last chunk of (b, g) to finish merges all chunks (the same
-// merge as attn_merge) into attn[b][h*64 + d]. Scaling Q by 1/8 is exact,
-// so scores equal (q . k) / sqrt(64).
+// merge as attn_merge) into attn[b][h*64 + d]. Q is scaled by
+// kScoreScaleLog2 = log2(e) / sqrt(64), so scores and maxima are in base-2
+// units and every softmax exponential is one v_exp_f32 (2^x).
 struct GqaLds {
   float ps[kWavesPerBlock][16][17];   // P tile [head][pos]
   float vs[kWavesPerBlock][16][68];   // V tile [pos][dim]
@@ -370,7 +371,8 @@ __global__ __launch_bounds__(kBlock) void batch_attn_kernel(BatchLaunch p, int l
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const float4 v = ld4(qr + 16 * s);
-      qa[s] = make_float4(v.x * 0.125f, v.y * 0.125f, v.z * 0.125f, v.w * 0.125f);
+      qa[s] = make_float4(v.x * kScoreScaleLog2, v.y * kScoreScaleLog2, v.z * kScoreScaleLog2,
+                          v.w * kScoreScaleLog2);
     }
   } else {
 #pragma unroll
@@ -416,8 +418,8 @@ __global__ __launch_bounds__(kBlock) void batch_attn_kernel(BatchLaunch p, int l
     for (int r = 0; r < 4; ++r) {
       const float sv = valid ? sacc[r] : -INFINITY;
       const float mn = fmaxf(m[r], row16_max(sv));
-      const float pv = mn == -INFINITY ? 0.f : expf(sv - mn);
-      const float corr = mn == -INFINITY ? 1.f : expf(m[r] - mn);
+      const float pv = mn == -INFINITY ? 0.f : exp2_fast(sv - mn);
+      const float corr = mn == -INFINITY ? 1.f : exp2_fast(m[r] - mn);
       lsum[r] = fmaf(lsum[r], corr, row16_sum(pv));
       m[r] = mn;
 #pragma unroll
@@ -460,7 +462,7 @@ __global__ __launch_bounds__(kBlock) void batch_attn_kernel(BatchLaunch p, int l
     float lt = 0.f, a = 0.f;
 #pragma unroll
     for (int v = 0; v < kWavesPerBlock; ++v) {
-      const float f = sh.wm[v][h] == -INFINITY ? 0.f : expf(sh.wm[v][h] - mx);
+      const float f = sh.wm[v][h] == -INFINITY ? 0.f : exp2_fast(sh.wm[v][h] - mx);
       lt = fmaf(f, sh.wl[v][h], lt);
       a = fmaf(f, sh.wo[v][h][d], a);
     }
@@ -496,7 +498,7 @@ __global__ __launch_bounds__(kBlock) void batch_attn_kernel(BatchLaunch p, int l
     float num = 0.f, den = 0.f;
 #pragma unroll
     for (int c = 0; c < kAttnMaxChunks; ++c) {
-      const float f = c < chunks ? expf(cm[c] - mx) : 0.f;
+      const float f = c < chunks ? exp2_fast(cm[c] - mx) : 0.f;
       den = fmaf(f, cl[c], den);
       num = fmaf(f, ca[c], num);
     }
