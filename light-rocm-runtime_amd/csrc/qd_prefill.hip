@@ -45,7 +45,17 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 // Lane l reads k-quad 2 j + l / 32 of its row and feeds it to four MFMAs,
 // so MFMA (j, c) takes k = 8 j + 4 (l / 32) + c, in A and in B alike.
 constexpr int kTileM = 64, kTileN = 64, kTileK = 32;
-constexpr int kStages = 4;
+// Ring depth of the split-K / stream-K GEMMs (64 KiB of LDS: two workgroups
+// per CU) and of the gate/up + SwiGLU GEMM (32 KiB: five per CU, so its 1,216
+// tiles at M = 512 run as one round on 256 CUs instead of 2.4 rounds of 512).
+#ifndef QD_GEMM_STAGES
+#define QD_GEMM_STAGES 4
+#endif
+#ifndef QD_SWIGLU_STAGES
+#define QD_SWIGLU_STAGES 2
+#endif
+constexpr int kStages = QD_GEMM_STAGES;
+constexpr int kStagesSwiGLU = QD_SWIGLU_STAGES;
 constexpr int kStageFloats = (kTileM + kTileN) * kTileK;
 
 typedef __attribute__((address_space(3))) void gemm_lds_void;
@@ -87,6 +97,7 @@ __host__ __device__ inline int sk_owner(long long it, int groups, long long tota
 
 // One tile's product over K slices [s_begin, s_end) into C (plain, bias or
 // accumulate per mode; SwiGLU as described above).
+template <int kSt>
 __device__ __forceinline__ void gemm_tile(float *stage_lds, const float *__restrict__ A, int lda,
                                           const float *__restrict__ W, const float *__restrict__ W2,
                                           int ldw, float *__restrict__ C, int ldc, int m, int n, int mode,
@@ -124,13 +135,13 @@ __device__ __forceinline__ void gemm_tile(float *stage_lds, const float *__restr
   const int half = lane >> 5;
   f16v acc = {};
 #pragma unroll
-  for (int st = 0; st < kStages - 1; ++st)
+  for (int st = 0; st < kSt - 1; ++st)
     if (st < slices) issue(st, st);
   for (int sl = 0; sl < slices; ++sl) {
     // Slice sl's DMA has landed once at most 4 (per later slice in flight)
     // of this wave's loads are outstanding; the barrier makes every wave's
     // part visible and retires every wave's reads of the stage refilled next.
-    const int ahead = min(kStages - 2, slices - 1 - sl);
+    const int ahead = min(kSt - 2, slices - 1 - sl);
     if (ahead >= 2)
       asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
     else if (ahead == 1)
@@ -138,8 +149,8 @@ __device__ __forceinline__ void gemm_tile(float *stage_lds, const float *__restr
     else
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     gemm_lds_barrier();
-    if (sl + kStages - 1 < slices) issue(sl + kStages - 1, (sl + kStages - 1) % kStages);
-    const float *st = stage_lds + (sl % kStages) * kStageFloats;
+    if (sl + kSt - 1 < slices) issue(sl + kSt - 1, (sl + kSt - 1) % kSt);
+    const float *st = stage_lds + (sl % kSt) * kStageFloats;
     float4 av[4], bv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -189,13 +200,14 @@ __device__ __forceinline__ void gemm_tile(float *stage_lds, const float *__restr
   }
 }
 
+template <int kSt>
 __global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict__ A, int lda,
                                                          const float *__restrict__ W,
                                                          const float *__restrict__ W2, int ldw,
                                                          float *__restrict__ C, int ldc, int m,
                                                          int n, int k, int mode,
                                                          const float *__restrict__ bias, int sk_groups) {
-  __shared__ __attribute__((aligned(16))) float stage_lds[kStages * kStageFloats];
+  __shared__ __attribute__((aligned(16))) float stage_lds[kSt * kStageFloats];
   const int slices_all = k / kTileK;
   if (sk_groups > 0) {
     const int tiles_n = (n + kTileN - 1) / kTileN;
@@ -209,7 +221,7 @@ __global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict
       const int s_end = static_cast<int>(min(it1 - first, static_cast<long long>(slices_all)));
       const int slot = g - sk_owner(first, sk_groups, total);
       gemm_lds_barrier();  // the previous tile's last stage reads are done
-      gemm_tile(stage_lds, A, lda, W, W2, ldw, C + static_cast<size_t>(slot) * m * ldc, ldc, m, n, kGemmStore,
+      gemm_tile<kSt>(stage_lds, A, lda, W, W2, ldw, C + static_cast<size_t>(slot) * m * ldc, ldc, m, n, kGemmStore,
                 bias, false, tile % tiles_n, (tile / tiles_n) * kTileM, (tile % tiles_n) * kTileN, s_begin,
                 s_end);
       it = first + slices_all;
@@ -223,7 +235,7 @@ __global__ __launch_bounds__(kBlock) void gemm_nt_kernel(const float *__restrict
     C += static_cast<size_t>(blockIdx.z) * m * ldc;
     mode = kGemmStore;
   }
-  gemm_tile(stage_lds, A, lda, W, W2, ldw, C, ldc, m, n, mode, bias, split == 1, blockIdx.x,
+  gemm_tile<kSt>(stage_lds, A, lda, W, W2, ldw, C, ldc, m, n, mode, bias, split == 1, blockIdx.x,
             blockIdx.y * kTileM, blockIdx.x * kTileN, s_begin, s_end);
 }
 
@@ -636,7 +648,7 @@ hipError_t launch_gemm_nt(hipStream_t s, const float *A, int lda, const float *W
   if (mode == kGemmSwiGLU) return hipErrorInvalidValue;
   const dim3 grid = sk_groups > 0 ? dim3(sk_groups, 1, 1)
                                   : dim3((n + kTileN - 1) / kTileN, (m + kTileM - 1) / kTileM, split);
-  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, W, nullptr, ldw, partials ? workspace : C, ldc, m, n, k,
+  gemm_nt_kernel<kStages><<<grid, kBlock, 0, s>>>(A, lda, W, nullptr, ldw, partials ? workspace : C, ldc, m, n, k,
                                          mode, bias, sk_groups);
   if (partials && epi) {
     gemm_reduce_rows_kernel<<<m, kBlock, 0, s>>>(workspace, split, sk_groups, k, C, ldc, m, n, mode, bias,
@@ -682,7 +694,8 @@ hipError_t launch_gemm_swiglu(hipStream_t s, const float *A, int lda, const floa
                               int ldw, float *act, int ldc, int m, int inter, int k) {
   if (k % kTileK != 0 || m <= 0 || inter <= 0 || inter % (kTileN / 2) != 0) return hipErrorInvalidValue;
   const dim3 grid(inter / (kTileN / 2), (m + kTileM - 1) / kTileM, 1);
-  gemm_nt_kernel<<<grid, kBlock, 0, s>>>(A, lda, wg, wu, ldw, act, ldc, m, 2 * inter, k, kGemmSwiGLU, nullptr, 0);
+  gemm_nt_kernel<kStagesSwiGLU><<<grid, kBlock, 0, s>>>(A, lda, wg, wu, ldw, act, ldc, m, 2 * inter, k,
+                                                        kGemmSwiGLU, nullptr, 0);
   return hipGetLastError();
 }
 
