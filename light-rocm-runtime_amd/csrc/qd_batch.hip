@@ -530,7 +530,11 @@ __global__ __launch_bounds__(kBlock) void batch_oproj_kernel(BatchLaunch p,
   if (seq < p.rows) p.hidden[seq * kH + n0 + (t & 15)] += v;
 }
 
-// MLP RMSNorm + gate/up + SiLU: act[b][row] = silu(g) * u for tile blockIdx.x.
+// MLP RMSNorm + gate/up + SiLU: act[b][row] = silu(g) * u. Tile blockIdx.x
+// covers rows n0 .. n0 + 7 of the activation: tile column j < 8 is gate row
+// n0 + j and column j + 8 the up row n0 + j, so each lane streams one weight
+// row and the 608 tiles (of 57 KB each) spread evenly over the CUs. The up
+// sum crosses to its gate lane (column j + 8 -> j) by a lane exchange.
 __global__ __launch_bounds__(kBlock) void batch_gateup_kernel(BatchLaunch p,
                                                               const float *__restrict__ gain,
                                                               const float *__restrict__ wg,
@@ -539,28 +543,31 @@ __global__ __launch_bounds__(kBlock) void batch_gateup_kernel(BatchLaunch p,
   __shared__ float wss[kWavesPerBlock][16];
   __shared__ float ss[16];
   __shared__ float red[kWavesPerBlock][4][kWave];
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 8;
   const int kbase = wave_id() * kSteps * kStep;
-  const size_t wrow = static_cast<size_t>(n0 + tile_col()) * kH;
-  float4 wgv[kSteps], wuv[kSteps], xa[kSteps];
-  load_weights<kSteps>(wg + wrow, kbase, wgv);
-  load_weights<kSteps>(wu + wrow, kbase, wuv);
+  const int col = tile_col();
+  const float *wrow = (col < 8 ? wg : wu) + static_cast<size_t>(n0 + (col & 7)) * kH;
+  float4 wv[kSteps], xa[kSteps];
+  load_weights<kSteps>(wrow, kbase, wv);
   float4 gv[kSteps];
   load_operand<kSteps, kH>(p.hidden, p.rows, kbase, xa);
   load_gain<kSteps>(kbase, gain, gv);
   issue_fence();
   const float part = gain_operand<kSteps>(gv, xa);
-  f4v ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-  ag = tile_mfma<kSteps>(xa, wgv, ag);
-  au = tile_mfma<kSteps>(xa, wuv, au);
+  f4v acc = {0.f, 0.f, 0.f, 0.f};
+  acc = tile_mfma<kSteps>(xa, wv, acc);
   rows_sum_squares(part, wss, ss);
-  const float g0 = tile_reduce<kWavesPerBlock>(ag, red);
-  const float u0 = tile_reduce<kWavesPerBlock>(au, red);
+  const float v = tile_reduce<kWavesPerBlock>(acc, red);
+  // Thread t < 256 holds (sequence tile_seq(t), column t & 15); its partner
+  // column t ^ 8 sits in lane (t ^ 8) of the same wave.
+  const float other = __shfl_xor(v, 8, kWave);
   const int t = threadIdx.x;
   const int seq = tile_seq(t);
-  const float inv = rsqrtf(ss[seq] / static_cast<float>(kH) + p.eps);
-  const float g = g0 * inv, u = u0 * inv;
-  if (seq < p.rows) p.act[seq * kI + n0 + (t & 15)] = g / (1.f + expf(-g)) * u;
+  if (t < 4 * kWave && (t & 15) < 8 && seq < p.rows) {
+    const float inv = rsqrtf(ss[seq] / static_cast<float>(kH) + p.eps);
+    const float g = v * inv, u = other * inv;
+    p.act[seq * kI + n0 + (t & 7)] = g / (1.f + expf(-g)) * u;
+  }
 }
 
 // hidden[b][row] += Wd[row] . act[b]; K = 4864 split over kDownSplit
@@ -848,7 +855,7 @@ hipError_t launch_batch_layer(hipStream_t s, const BatchLaunch &b, const LayerPt
   }
   {
     Scope scope(m, kBGateUp);
-    batch_gateup_kernel<<<kI / 16, kBlock, 0, s>>>(b, w.mlp_norm, w.wg, w.wu);
+    batch_gateup_kernel<<<kI / 8, kBlock, 0, s>>>(b, w.mlp_norm, w.wg, w.wu);
   }
   {
     Scope scope(m, kBDown);
