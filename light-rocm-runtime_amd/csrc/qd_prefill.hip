@@ -447,13 +447,21 @@ __device__ __forceinline__ void attention_prefill_block(
   const int keys = pos0 + last_row + 1;  // causal extent of the block
   const int kblocks = (keys + kKBlock - 1) / kKBlock;
 
-  // Query operand: lane supplies Q[row lr][dim 4 s + lg] for s < 16.
+  // Query operand: lane supplies Q[row lr][dim 16 lg + s] at k-step s < 16
+  // (the K operand takes the same dims), so each lane's 16 dims are
+  // contiguous: four float4 reads.
   float qa[kHeadDim / 4];
   {
     const int qrow = min(r0 + lr, rows - 1);
-    const float *q = qkv + static_cast<size_t>(qrow) * ld + h * kHeadDim;
+    const float4 *q4 = reinterpret_cast<const float4 *>(qkv + static_cast<size_t>(qrow) * ld + h * kHeadDim + 16 * lg);
 #pragma unroll
-    for (int s = 0; s < kHeadDim / 4; ++s) qa[s] = q[4 * s + lg];
+    for (int j = 0; j < 4; ++j) {
+      const float4 v = q4[j];
+      qa[4 * j] = v.x;
+      qa[4 * j + 1] = v.y;
+      qa[4 * j + 2] = v.z;
+      qa[4 * j + 3] = v.w;
+    }
   }
   // Running state of the lane's four query rows lg * 4 + r.
   float m[4], l[4];
@@ -491,14 +499,8 @@ __device__ __forceinline__ void attention_prefill_block(
     for (int i = 0; i < kKBlock / 4; ++i) {
       const int row = lg + 4 * i;
       const float4 kv = kr[i], vv = vr[i];
-      ks[row][4 * lr + 0] = kv.x;
-      ks[row][4 * lr + 1] = kv.y;
-      ks[row][4 * lr + 2] = kv.z;
-      ks[row][4 * lr + 3] = kv.w;
-      vs[row][4 * lr + 0] = vv.x;
-      vs[row][4 * lr + 1] = vv.y;
-      vs[row][4 * lr + 2] = vv.z;
-      vs[row][4 * lr + 3] = vv.w;
+      *reinterpret_cast<float4 *>(&ks[row][4 * lr]) = kv;
+      *reinterpret_cast<float4 *>(&vs[row][4 * lr]) = vv;
     }
     if (kb + kWavesPerBlock < kblocks) load_block(kb + kWavesPerBlock);
     // S tiles: keys k0 + 16 tt + lr. Every B operand is read from LDS before
@@ -506,9 +508,15 @@ __device__ __forceinline__ void attention_prefill_block(
     // chains run interleaved; each chain keeps its order over st.
     float kop[2][kHeadDim / 4];
 #pragma unroll
-    for (int st = 0; st < kHeadDim / 4; ++st) {
-      kop[0][st] = ks[lr][4 * st + lg];
-      kop[1][st] = ks[16 + lr][4 * st + lg];
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const float4 v = *reinterpret_cast<const float4 *>(&ks[16 * tt + lr][16 * lg + 4 * j]);
+        kop[tt][4 * j] = v.x;
+        kop[tt][4 * j + 1] = v.y;
+        kop[tt][4 * j + 2] = v.z;
+        kop[tt][4 * j + 3] = v.w;
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     f4v s[2] = {f4v{0.f, 0.f, 0.f, 0.f}, f4v{0.f, 0.f, 0.f, 0.f}};
@@ -547,7 +555,8 @@ __device__ __forceinline__ void attention_prefill_block(
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[dt][r] *= corr[r];
     // O += P . V: A = P[row lr][key 4 st + lg], B = V[key 4 st + lg][dim 16 dt + lr],
-    // the operands read from LDS first as for S.
+    // the operands read from LDS first as for S (this key order keeps the V
+    // reads of the four lane groups on different banks).
     float pa[kKBlock / 4], vb[kKBlock / 4][4];
 #pragma unroll
     for (int st = 0; st < kKBlock / 4; ++st) {
@@ -604,7 +613,7 @@ __device__ __forceinline__ void attention_prefill_block(
 __global__ __launch_bounds__(kBlock) void attention_prefill_kernel(
     const float *__restrict__ qkv, int rows, int pos0, int nq, int nkv,
     const float *__restrict__ k_cache, const float *__restrict__ v_cache, float *__restrict__ out) {
-  __shared__ PrefillAttnLds sh;
+  __shared__ __attribute__((aligned(16))) PrefillAttnLds sh;
   const int nqb = (rows + kQBlock - 1) / kQBlock;
   const int p = blockIdx.x;
   attention_prefill_block(sh, p, qkv, rows, pos0, nq, nkv, k_cache, v_cache, out);
